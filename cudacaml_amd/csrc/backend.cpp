@@ -1,0 +1,475 @@
+// Backend_hip: compile (plan + templates + JIT + pools) and the executor
+// that walks the host plan, behind the C ABI of include/cchip_backend.h.
+//
+// Restates lib/backend_cuda/executor.ml:23-244 and
+// lib/backend_cuda/cudacaml_backend_cuda.ml:23-111 on HIP: a compiled
+// program owns `streams` executors, each with its own stream and buffer
+// pool allocated once at compile time; a run only uploads, launches and
+// downloads, all ordered by the executor's stream; run_resident substitutes
+// the caller's device buffers for the plan's own by name.
+
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <mutex>
+
+#include "../../include/cchip_backend.h"
+#include "internal.hpp"
+
+using namespace cchip;
+
+namespace {
+
+struct DeviceGuard {
+  int prev = -1;
+  explicit DeviceGuard(int dev) {
+    ensure_init();
+    check_hip(hipGetDevice(&prev), "hipGetDevice");
+    if (prev != dev) check_hip(hipSetDevice(dev), "hipSetDevice");
+  }
+  ~DeviceGuard() {
+    int cur = -1;
+    if (hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+  }
+};
+
+struct Executor {
+  hipStream_t stream = nullptr;
+  std::vector<void *> bufs;
+  int *err_host = nullptr;  // pinned word the error flag is read into
+};
+
+const char *err_message(int code) {
+  if (code & 1) return "Backend_hip: gather index out of bounds";
+  if (code & 2) return "Backend_hip: scatter_add index out of bounds";
+  return "Backend_hip: scan look-back did not complete (device-side timeout)";
+}
+
+}  // namespace
+
+struct cchip_program {
+  ProgramIR ir;
+  std::shared_ptr<Module> mod;
+  std::vector<void *> kfn;
+  int device = 0;
+  std::vector<Executor> execs;
+  int next = 0;
+  bool released = false;
+  std::mutex mu;
+  // timing hook
+  int timed = -1;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> ev_used, ev_free;
+};
+
+struct cchip_job {
+  cchip_program *prog = nullptr;
+  int lane = 0;
+  hipEvent_t done = nullptr;
+  bool waited = false;
+  int status = 0;
+  std::string msg;
+};
+
+namespace {
+
+void release_program(cchip_program *p) {
+  if (p->released) return;
+  p->released = true;
+  DeviceGuard dg(p->device);
+  for (auto &e : p->execs) {
+    if (e.stream) (void)hipStreamSynchronize(e.stream);
+    else (void)hipDeviceSynchronize();
+    for (void *b : e.bufs) rt_free(b);
+    e.bufs.clear();
+    if (e.err_host) (void)hipHostFree(e.err_host);
+    e.err_host = nullptr;
+    if (e.stream) (void)hipStreamDestroy(e.stream);
+    e.stream = nullptr;
+  }
+  for (auto &pr : p->ev_used) {
+    (void)hipEventDestroy(pr.first);
+    (void)hipEventDestroy(pr.second);
+  }
+  for (auto &pr : p->ev_free) {
+    (void)hipEventDestroy(pr.first);
+    (void)hipEventDestroy(pr.second);
+  }
+  p->ev_used.clear();
+  p->ev_free.clear();
+  p->mod.reset();
+}
+
+const IOSpec *find_param(const ProgramIR &ir, const std::string &name) {
+  for (auto &p : ir.params)
+    if (p.name == name) return &p;
+  return nullptr;
+}
+
+// Every input must be present, with the param's exact byte size, before any
+// device work is issued (executor.ml:12-21, :192-208).
+std::vector<int> bind_inputs(const cchip_program *p, int n, const char *const *names, const size_t *bytes,
+                             const char *who) {
+  std::vector<int> which(p->ir.params.size(), -1);
+  for (size_t k = 0; k < p->ir.params.size(); k++) {
+    const IOSpec &ps = p->ir.params[k];
+    for (int i = 0; i < n; i++)
+      if (names[i] && ps.name == names[i]) {
+        which[k] = i;
+        break;
+      }
+    if (which[k] < 0) throw InvalidArgument(std::string(who) + ": missing input " + ps.name);
+    size_t want = (size_t)p->ir.bufs[ps.buf].bytes();
+    if (bytes[which[k]] != want)
+      throw InvalidArgument(strf("%s: input %s is %zu bytes, parameter %s needs %zu", who, ps.name.c_str(),
+                                 bytes[which[k]], p->ir.bufs[ps.buf].name.c_str(), want));
+  }
+  return which;
+}
+
+void launch_kernels(cchip_program *p, Executor &e, const std::vector<void *> &ptr, bool timing) {
+  for (auto &op : p->ir.plan) {
+    if (op.kind != OpK::Launch) continue;
+    const KernelSpec &k = p->ir.kernels[op.kernel];
+    std::vector<void *> vals(k.args.size());
+    std::vector<void *> args(k.args.size());
+    for (size_t i = 0; i < k.args.size(); i++) {
+      vals[i] = ptr[k.args[i]];
+      args[i] = &vals[i];
+    }
+    bool timed = timing && op.kernel == p->timed;
+    std::pair<hipEvent_t, hipEvent_t> ev{nullptr, nullptr};
+    if (timed) {
+      if (!p->ev_free.empty()) {
+        ev = p->ev_free.back();
+        p->ev_free.pop_back();
+      } else {
+        check_hip(hipEventCreate(&ev.first), "hipEventCreate");
+        check_hip(hipEventCreate(&ev.second), "hipEventCreate");
+      }
+      check_hip(hipEventRecord(ev.first, e.stream), "hipEventRecord");
+    }
+    check_hip(hipModuleLaunchKernel((hipFunction_t)p->kfn[op.kernel], k.grid, k.grid_y, 1, k.block, k.block_y, 1,
+                                    k.shared_bytes, e.stream, args.data(), nullptr),
+              "hipModuleLaunchKernel");
+    if (timed) {
+      check_hip(hipEventRecord(ev.second, e.stream), "hipEventRecord");
+      p->ev_used.push_back(ev);
+    }
+  }
+}
+
+// Reads the error word after the work already queued; on a flag, clears it
+// and raises the interpreter's error.
+void check_err_after(cchip_program *p, Executor &e, const std::vector<void *> &ptr, bool synced) {
+  if (p->ir.err_buf < 0) return;
+  if (!synced) check_hip(hipStreamSynchronize(e.stream), "hipStreamSynchronize");
+  int code = *e.err_host;
+  if (code) {
+    *e.err_host = 0;
+    check_hip(hipMemcpy(ptr[p->ir.err_buf], e.err_host, sizeof(int), hipMemcpyHostToDevice), "hipMemcpy");
+    throw InvalidArgument(err_message(code));
+  }
+}
+
+void queue_err_read(cchip_program *p, Executor &e, const std::vector<void *> &ptr) {
+  if (p->ir.err_buf < 0) return;
+  check_hip(hipMemcpyAsync(e.err_host, ptr[p->ir.err_buf], sizeof(int), hipMemcpyDeviceToHost, e.stream),
+            "hipMemcpyAsync err");
+}
+
+void issue_host_run(cchip_program *p, int lane, int n, const char *const *names, const void *const *host,
+                    const size_t *bytes, void *const *outputs) {
+  if (p->released) throw Failure("Executor.run: this executor has been released");
+  std::vector<int> which = bind_inputs(p, n, names, bytes, "Executor.run");
+  Executor &e = p->execs[lane];
+  const std::vector<void *> &ptr = e.bufs;
+  for (size_t k = 0; k < p->ir.params.size(); k++) {
+    const IOSpec &ps = p->ir.params[k];
+    size_t nb = (size_t)p->ir.bufs[ps.buf].bytes();
+    if (nb)
+      check_hip(hipMemcpyAsync(ptr[ps.buf], host[which[k]], nb, hipMemcpyHostToDevice, e.stream), "upload");
+  }
+  launch_kernels(p, e, ptr, lane == 0);
+  for (size_t o = 0; o < p->ir.outputs.size(); o++) {
+    const IOSpec &os = p->ir.outputs[o];
+    size_t nb = (size_t)p->ir.bufs[os.buf].bytes();
+    if (nb) check_hip(hipMemcpyAsync(outputs[o], ptr[os.buf], nb, hipMemcpyDeviceToHost, e.stream), "download");
+  }
+  queue_err_read(p, e, ptr);
+}
+
+void run_resident_impl(cchip_program *p, int n, const char *const *names, void *const *dev_inputs,
+                       const size_t *bytes, void **outs_alloc, void *const *outs_given, bool sync) {
+  if (p->released) throw Failure("Executor.run_resident: this executor has been released");
+  std::vector<int> which = bind_inputs(p, n, names, bytes, "Executor.run_resident");
+  Executor &e = p->execs[0];
+  std::vector<void *> ptr = e.bufs;
+  std::vector<bool> overridden(ptr.size(), false);
+  for (size_t k = 0; k < p->ir.params.size(); k++) {
+    ptr[p->ir.params[k].buf] = dev_inputs[which[k]];
+    overridden[p->ir.params[k].buf] = true;
+  }
+  // Outputs: substitute a fresh (or caller-given) buffer for the plan's own
+  // so the producing kernel writes straight into it; a name already bound
+  // (an output that is a param, or one buffer downloaded twice) is copied.
+  std::vector<std::pair<int, void *>> copies;
+  std::vector<void *> fresh;
+  try {
+    for (size_t o = 0; o < p->ir.outputs.size(); o++) {
+      const IOSpec &os = p->ir.outputs[o];
+      void *dst;
+      if (outs_given) {
+        dst = outs_given[o];
+      } else {
+        dst = rt_alloc((size_t)p->ir.bufs[os.buf].bytes());
+        fresh.push_back(dst);
+      }
+      if (overridden[os.buf]) copies.emplace_back(os.buf, dst);
+      else {
+        ptr[os.buf] = dst;
+        overridden[os.buf] = true;
+      }
+      if (outs_alloc) outs_alloc[o] = dst;
+    }
+    launch_kernels(p, e, ptr, true);
+    for (auto &c : copies) {
+      size_t nb = (size_t)p->ir.bufs[c.first].bytes();
+      if (nb) check_hip(hipMemcpyAsync(c.second, ptr[c.first], nb, hipMemcpyDeviceToDevice, e.stream), "copy_device");
+    }
+    if (sync) {
+      queue_err_read(p, e, e.bufs);
+      check_hip(hipStreamSynchronize(e.stream), "hipStreamSynchronize");
+      check_err_after(p, e, e.bufs, true);
+    }
+  } catch (...) {
+    if (sync) (void)hipStreamSynchronize(e.stream);
+    for (void *f : fresh) rt_free(f);
+    throw;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+void cchip_free(void *p) { free(p); }
+
+static char *dup_string(const std::string &s) {
+  char *c = (char *)malloc(s.size() + 1);
+  memcpy(c, s.c_str(), s.size() + 1);
+  return c;
+}
+
+int cchip_backend_source(const char *graph, char **source) {
+  return guarded([&] {
+    Graph g = parse_wire(graph);
+    ProgramIR ir = lower_program(g);
+    *source = dup_string(ir.source);
+  });
+}
+
+int cchip_backend_plan(const char *graph, char **plan) {
+  return guarded([&] {
+    Graph g = parse_wire(graph);
+    ProgramIR ir = lower_program(g);
+    *plan = dup_string(plan_to_string(ir));
+  });
+}
+
+int cchip_backend_compile(const char *graph, int device, int streams, cchip_program **program) {
+  return guarded([&] {
+    if (streams < 1) throw InvalidArgument("Backend_hip.compile_on: streams must be >= 1");
+    Graph g = parse_wire(graph);
+    auto p = std::make_unique<cchip_program>();
+    p->ir = lower_program(g);
+    p->device = device;
+    ensure_init();
+    int ndev = 0;
+    check_hip(hipGetDeviceCount(&ndev), "hipGetDeviceCount");
+    if (device < 0 || device >= ndev) throw InvalidArgument(strf("Backend_hip.compile_on: no device %d", device));
+    DeviceGuard dg(device);
+    p->mod = jit_compile("cchip_" + g.name, p->ir.source);
+    for (auto &k : p->ir.kernels) p->kfn.push_back(module_kernel(*p->mod, k.name));
+    p->execs.resize(streams);
+    try {
+      for (int s = 0; s < streams; s++) {
+        Executor &e = p->execs[s];
+        if (s > 0) check_hip(hipStreamCreateWithFlags(&e.stream, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+        check_hip(hipHostMalloc((void **)&e.err_host, sizeof(int), hipHostMallocPortable), "hipHostMalloc");
+        *e.err_host = 0;
+        e.bufs.assign(p->ir.bufs.size(), nullptr);
+        for (size_t b = 0; b < p->ir.bufs.size(); b++) {
+          e.bufs[b] = rt_alloc((size_t)p->ir.bufs[b].bytes());
+          // Scratch (per-row counters, look-back status) and the error word
+          // start at zero; the kernels leave them at zero again.
+          if (p->ir.bufs[b].role == BufRole::Scratch || p->ir.bufs[b].role == BufRole::Err)
+            check_hip(hipMemset(e.bufs[b], 0, (size_t)std::max<int64_t>(1, p->ir.bufs[b].bytes())), "hipMemset");
+        }
+      }
+    } catch (...) {
+      release_program(p.get());
+      throw;
+    }
+    *program = p.release();
+  });
+}
+
+int cchip_program_release(cchip_program *p) {
+  return guarded([&] {
+    if (!p) throw InvalidArgument("null program");
+    std::lock_guard<std::mutex> lk(p->mu);
+    release_program(p);
+  });
+}
+
+int cchip_program_destroy(cchip_program *p) {
+  int rc = cchip_program_release(p);
+  delete p;
+  return rc;
+}
+
+int cchip_program_device(const cchip_program *p) { return p->device; }
+int cchip_program_streams(const cchip_program *p) { return (int)p->execs.size(); }
+int cchip_program_buffer_count(const cchip_program *p) {
+  return p->released || p->execs.empty() ? 0 : (int)p->execs[0].bufs.size();
+}
+int cchip_program_kernel_count(const cchip_program *p) { return (int)p->ir.kernels.size(); }
+const char *cchip_program_kernel_name(const cchip_program *p, int i) {
+  if (i < 0 || i >= (int)p->ir.kernels.size()) return nullptr;
+  return p->ir.kernels[i].name.c_str();
+}
+
+static int io_info(const std::vector<IOSpec> &v, int i, const char **name, int *dtype, int *rank, int64_t *dims) {
+  return guarded([&] {
+    if (i < 0 || i >= (int)v.size()) throw InvalidArgument(strf("index %d out of range", i));
+    const IOSpec &s = v[i];
+    if (name) *name = s.name.c_str();
+    if (dtype) *dtype = (int)s.dt;
+    if (rank) *rank = (int)s.shape.size();
+    if (dims)
+      for (size_t k = 0; k < s.shape.size() && k < 8; k++) dims[k] = s.shape[k];
+  });
+}
+
+int cchip_program_num_params(const cchip_program *p) { return (int)p->ir.params.size(); }
+int cchip_program_param(const cchip_program *p, int i, const char **name, int *dtype, int *rank, int64_t *dims) {
+  return io_info(p->ir.params, i, name, dtype, rank, dims);
+}
+int cchip_program_num_outputs(const cchip_program *p) { return (int)p->ir.outputs.size(); }
+int cchip_program_output(const cchip_program *p, int i, const char **name, int *dtype, int *rank, int64_t *dims) {
+  return io_info(p->ir.outputs, i, name, dtype, rank, dims);
+}
+
+int cchip_program_run(cchip_program *p, int n, const char *const *names, const void *const *host,
+                      const size_t *bytes, void *const *outputs) {
+  return guarded([&] {
+    std::lock_guard<std::mutex> lk(p->mu);
+    DeviceGuard dg(p->device);
+    issue_host_run(p, 0, n, names, host, bytes, outputs);
+    Executor &e = p->execs[0];
+    check_hip(hipStreamSynchronize(e.stream), "hipStreamSynchronize");
+    check_err_after(p, e, e.bufs, true);
+  });
+}
+
+int cchip_program_run_async(cchip_program *p, int n, const char *const *names, const void *const *host,
+                            const size_t *bytes, void *const *outputs, cchip_job **job) {
+  return guarded([&] {
+    std::lock_guard<std::mutex> lk(p->mu);
+    DeviceGuard dg(p->device);
+    int lane = p->next;
+    p->next = (p->next + 1) % (int)p->execs.size();
+    issue_host_run(p, lane, n, names, host, bytes, outputs);
+    auto j = std::make_unique<cchip_job>();
+    j->prog = p;
+    j->lane = lane;
+    check_hip(hipEventCreateWithFlags(&j->done, hipEventDisableTiming), "hipEventCreate");
+    check_hip(hipEventRecord(j->done, p->execs[lane].stream), "hipEventRecord");
+    *job = j.release();
+  });
+}
+
+int cchip_job_wait(cchip_job *j) {
+  if (j->waited) {
+    if (j->status) set_last_error(j->msg);
+    return j->status;
+  }
+  int rc = guarded([&] {
+    cchip_program *p = j->prog;
+    DeviceGuard dg(p->device);
+    check_hip(hipEventSynchronize(j->done), "hipEventSynchronize");
+    std::lock_guard<std::mutex> lk(p->mu);
+    if (p->released) return;
+    Executor &e = p->execs[j->lane];
+    check_err_after(p, e, e.bufs, true);
+  });
+  j->waited = true;
+  j->status = rc;
+  if (rc) j->msg = cchip_last_error();
+  return rc;
+}
+
+int cchip_job_free(cchip_job *j) {
+  if (!j) return 0;
+  if (j->done) (void)hipEventDestroy(j->done);
+  delete j;
+  return 0;
+}
+
+int cchip_program_run_resident(cchip_program *p, int n, const char *const *names, void *const *dev_inputs,
+                               const size_t *bytes, void **outputs) {
+  return guarded([&] {
+    std::lock_guard<std::mutex> lk(p->mu);
+    DeviceGuard dg(p->device);
+    run_resident_impl(p, n, names, dev_inputs, bytes, outputs, nullptr, true);
+  });
+}
+
+int cchip_program_run_resident_into(cchip_program *p, int n, const char *const *names, void *const *dev_inputs,
+                                    const size_t *bytes, void *const *dev_outputs, int sync) {
+  return guarded([&] {
+    std::lock_guard<std::mutex> lk(p->mu);
+    DeviceGuard dg(p->device);
+    run_resident_impl(p, n, names, dev_inputs, bytes, nullptr, dev_outputs, sync != 0);
+  });
+}
+
+int cchip_program_stream(const cchip_program *p, int lane, void **stream) {
+  return guarded([&] {
+    if (lane < 0 || lane >= (int)p->execs.size()) throw InvalidArgument("no such lane");
+    *stream = p->execs[lane].stream;
+  });
+}
+
+int cchip_program_time_kernel(cchip_program *p, const char *name) {
+  return guarded([&] {
+    std::lock_guard<std::mutex> lk(p->mu);
+    p->timed = -1;
+    if (!name) return;
+    for (size_t k = 0; k < p->ir.kernels.size(); k++)
+      if (p->ir.kernels[k].name == name) p->timed = (int)k;
+    if (p->timed < 0) throw InvalidArgument(std::string("no kernel named ") + name);
+    for (auto &e : p->ev_used) p->ev_free.push_back(e);
+    p->ev_used.clear();
+  });
+}
+
+int cchip_program_timing(cchip_program *p, int *launches, double *total_ms) {
+  return guarded([&] {
+    std::lock_guard<std::mutex> lk(p->mu);
+    DeviceGuard dg(p->device);
+    double tot = 0;
+    for (auto &e : p->ev_used) {
+      check_hip(hipEventSynchronize(e.second), "hipEventSynchronize");
+      float ms = 0;
+      check_hip(hipEventElapsedTime(&ms, e.first, e.second), "hipEventElapsedTime");
+      tot += ms;
+    }
+    *launches = (int)p->ev_used.size();
+    *total_ms = tot;
+    for (auto &e : p->ev_used) p->ev_free.push_back(e);
+    p->ev_used.clear();
+  });
+}
+
+}  // extern "C"

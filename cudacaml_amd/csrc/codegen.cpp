@@ -1,0 +1,1343 @@
+// Graph -> ProgramIR: the fusion inliner, the element-expression printer and
+// the gfx950 kernel templates.
+//
+// The inliner restates Lower's elem/inline_node/expr_of/inputs_of
+// (lib/lower/lower.ml:113-197): a materialised node is a load, anything else
+// is inlined, so map chains, gathers, transposes and RNG draws fuse into
+// whatever consumes them. Each kernel root then picks a CDNA4 template by
+// root kind (the role Lower.kernels_of plays at lower.ml:214-958), and the
+// host plan keeps the reference's shape (lower.ml:968-1012): allocate params
+// then computed buffers, upload, launch root by root, download, free.
+//
+// The printer keeps the interpreter's arithmetic (cudacaml_backend_interp.ml)
+// rather than C's: integer + - * and negation wrap through unsigned, shifts
+// mask their count and Shr is logical, Min/Max propagate NaN and order -0
+// below +0, float->int casts truncate through int64 then wrap, and an F32
+// constant that f32 cannot hold exactly stays a double until an operation
+// rounds it (an F32 Const is the unrounded double in the interpreter).
+
+#include <cmath>
+#include <cstring>
+#include <functional>
+#include <set>
+#include <sstream>
+#include <unordered_map>
+
+#include "internal.hpp"
+
+namespace cchip {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Value classes: how a scalar is carried in the generated code.
+// F32D is an f32-typed value that is still a double (an unrounded constant).
+// ---------------------------------------------------------------------------
+
+enum class VC { F32, F32D, F64, I32, I64, B };
+
+const char *vc_type(VC c) {
+  switch (c) {
+    case VC::F32: return "float";
+    case VC::F32D: return "double";
+    case VC::F64: return "double";
+    case VC::I32: return "int";
+    case VC::I64: return "long long";
+    default: return "bool";
+  }
+}
+
+VC storage_vc(DT d) {
+  switch (d) {
+    case DT::F32: return VC::F32;
+    case DT::F64: return VC::F64;
+    case DT::I32: return VC::I32;
+    case DT::I64: return VC::I64;
+    default: return VC::B;
+  }
+}
+
+struct Val {
+  std::string s;
+  VC c;
+};
+
+std::string f32_lit(float v) {
+  if (std::isnan(v)) return "__builtin_nanf(\"\")";
+  if (std::isinf(v)) return v > 0 ? "__builtin_inff()" : "(-__builtin_inff())";
+  char b[64];
+  snprintf(b, sizeof b, "%af", (double)v);
+  return std::string("(") + b + ")";
+}
+
+std::string f64_lit(double v) {
+  if (std::isnan(v)) return "__builtin_nan(\"\")";
+  if (std::isinf(v)) return v > 0 ? "__builtin_inf()" : "(-__builtin_inf())";
+  char b[64];
+  snprintf(b, sizeof b, "%a", v);
+  return std::string("(") + b + ")";
+}
+
+std::string i32_lit(int64_t v) {
+  int32_t x = (int32_t)v;
+  if (x == INT32_MIN) return "(-2147483647 - 1)";
+  return std::to_string(x);
+}
+
+std::string i64_lit(int64_t v) {
+  if (v == INT64_MIN) return "(-9223372036854775807LL - 1LL)";
+  return std::to_string(v) + "LL";
+}
+
+// A value in storage form (what a buffer of dtype d holds).
+std::string as_storage(const Val &v, DT d) {
+  if (d == DT::F32 && v.c == VC::F32D) return "(float)(" + v.s + ")";
+  return v.s;
+}
+
+std::string as_double(const Val &v) {
+  if (v.c == VC::F32) return "(double)(" + v.s + ")";
+  return v.s;
+}
+
+std::string zero_of(DT d) {
+  switch (d) {
+    case DT::F32: return "0.0f";
+    case DT::F64: return "0.0";
+    case DT::I32: return "0";
+    case DT::I64: return "0LL";
+    default: return "false";
+  }
+}
+
+// ---------------------------------------------------------------------------
+// The element generator: one __device__ function per (root, operand).
+// ---------------------------------------------------------------------------
+
+struct ElemFn {
+  std::string name;
+  std::string code;
+  DT dt = DT::F32;
+  std::vector<int> ident;  // buffers loaded at the function's own index: passed by value
+  std::vector<int> ptrs;   // buffers loaded anywhere else: passed by pointer
+  bool uses_err = false;
+
+  // Call with the identity-loaded values given by `identval(buf)`.
+  std::string call(const std::string &idx, const std::function<std::string(int)> &identval) const {
+    std::string s = name + "(" + idx;
+    for (int b : ident) s += ", " + identval(b);
+    for (int b : ptrs) s += ", b" + std::to_string(b);
+    if (uses_err) s += ", err";
+    return s + ")";
+  }
+  std::string call_scalar(const std::string &idx) const {
+    return call(idx, [&](int b) { return "b" + std::to_string(b) + "[" + idx + "]"; });
+  }
+};
+
+class Gen {
+ public:
+  Gen(const Graph &g, const Plan &p, const std::vector<int> &buf_of) : g_(g), p_(p), buf_of_(buf_of) {}
+
+  // f(i) = the value of tensor `t` at flat index i. If `inline_root`, t is
+  // computed (inlined) even though it is materialised: it is the kernel's
+  // own output (lower.ml:120-126).
+  ElemFn element_fn(const std::string &name, int t, bool inline_root, bool allow_ident) {
+    reset(allow_ident);
+    Val idx{"i", VC::I32};
+    Val r = inline_root ? inline_node(t, idx) : elem(t, idx);
+    ElemFn f;
+    f.name = name;
+    f.dt = g_.ts[t].dt;
+    f.ident = ident_;
+    f.ptrs = ptrs_;
+    f.uses_err = uses_err_;
+    std::ostringstream os;
+    os << "__device__ __forceinline__ " << dt_ctype(f.dt) << " " << name << "(const int i";
+    for (int b : ident_) os << ", const " << dt_ctype(bufdt(b)) << " a" << b;
+    for (int b : ptrs_) os << ", const " << dt_ctype(bufdt(b)) << "* __restrict__ b" << b;
+    if (uses_err_) os << ", int* __restrict__ err";
+    os << ") {\n" << body_.str() << "  return " << as_storage(r, f.dt) << ";\n}\n";
+    f.code = os.str();
+    return f;
+  }
+
+  // The combine function of a Reduce/Scan: T f(T x0, T x1), Index = 0 as in
+  // Lower (lower.ml:278).
+  std::string combine_fn(const std::string &name, int body, DT dt) {
+    reset(false);
+    std::vector<Val> env = {{"x0", storage_vc(dt)}, {"x1", storage_vc(dt)}};
+    std::unordered_map<int, Val> memo;
+    Val r = expr(body, env, Val{"0", VC::I32}, memo);
+    std::ostringstream os;
+    os << "__device__ __forceinline__ " << dt_ctype(dt) << " " << name << "(const " << dt_ctype(dt) << " x0, const "
+       << dt_ctype(dt) << " x1) {\n"
+       << body_.str() << "  return " << as_storage(r, dt) << ";\n}\n";
+    return os.str();
+  }
+
+  std::string const_fn(const std::string &name, int body, DT dt) {
+    reset(false);
+    std::unordered_map<int, Val> memo;
+    Val r = expr(body, {}, Val{"0", VC::I32}, memo);
+    std::ostringstream os;
+    os << "__device__ __forceinline__ " << dt_ctype(dt) << " " << name << "() {\n"
+       << body_.str() << "  return " << as_storage(r, dt) << ";\n}\n";
+    return os.str();
+  }
+
+  DT bufdt(int b) const { return bufdt_(b); }
+  std::function<DT(int)> bufdt_;
+
+ private:
+  const Graph &g_;
+  const Plan &p_;
+  const std::vector<int> &buf_of_;
+  std::ostringstream body_;
+  int ntmp_ = 0;
+  bool allow_ident_ = true;
+  std::vector<int> ident_, ptrs_;
+  bool uses_err_ = false;
+  std::map<std::pair<int, std::string>, Val> tmemo_;
+
+  void reset(bool allow_ident) {
+    body_.str("");
+    body_.clear();
+    ntmp_ = 0;
+    allow_ident_ = allow_ident;
+    ident_.clear();
+    ptrs_.clear();
+    uses_err_ = false;
+    tmemo_.clear();
+  }
+
+  Val def(VC c, const std::string &rhs) {
+    std::string n = "v" + std::to_string(ntmp_++);
+    body_ << "  const " << vc_type(c) << " " << n << " = " << rhs << ";\n";
+    return {n, c};
+  }
+
+  static void add_unique(std::vector<int> &v, int x) {
+    for (int y : v)
+      if (y == x) return;
+    v.push_back(x);
+  }
+
+  Val elem(int t, const Val &idx) {
+    auto key = std::make_pair(t, idx.s);
+    auto it = tmemo_.find(key);
+    if (it != tmemo_.end()) return it->second;
+    Val r;
+    if (p_.materialized[t]) {
+      int b = buf_of_[t];
+      DT d = g_.ts[t].dt;
+      if (allow_ident_ && idx.s == "i") {
+        add_unique(ident_, b);
+        r = {"a" + std::to_string(b), storage_vc(d)};
+      } else {
+        add_unique(ptrs_, b);
+        r = def(storage_vc(d), "b" + std::to_string(b) + "[" + idx.s + "]");
+      }
+    } else {
+      r = inline_node(t, idx);
+    }
+    tmemo_[key] = r;
+    return r;
+  }
+
+  Val inline_node(int t, const Val &idx) {
+    const TNode &n = g_.ts[t];
+    switch (n.kind) {
+      case TK::Iota: return idx;
+      case TK::Map: {
+        std::unordered_map<int, Val> memo;
+        return expr(n.body, {elem(n.a, idx)}, idx, memo);
+      }
+      case TK::Map2: {
+        std::unordered_map<int, Val> memo;
+        Val a = elem(n.a, idx);
+        Val b = elem(n.b, idx);
+        return expr(n.body, {a, b}, idx, memo);
+      }
+      case TK::Gather: {
+        // out[i] = src[idx[i]], bounds-checked against the source extent:
+        // the interpreter raises on an index out of range (R8); here the
+        // kernel raises a flag the host turns into the same error.
+        Val j = elem(n.a, idx);
+        const TNode &src = g_.ts[n.b];
+        uses_err_ = true;
+        if (src.numel == 0) {
+          body_ << "  cc_flag(err, 1);\n";
+          return def(storage_vc(src.dt), zero_of(src.dt));
+        }
+        std::string jn = "v" + std::to_string(ntmp_++);
+        body_ << "  int " << jn << " = " << j.s << ";\n";
+        body_ << "  if ((unsigned)" << jn << " >= " << src.numel << "u) { cc_flag(err, 1); " << jn << " = 0; }\n";
+        return elem(n.b, Val{jn, VC::I32});
+      }
+      case TK::Reshape: return elem(n.a, idx);
+      case TK::Broadcast: return elem(n.a, Val{"0", VC::I32});
+      default:
+        throw Failure("Lower: Param/Reduce/Scan/Scatter_add/Matmul must be materialised");
+    }
+  }
+
+  Val expr(int x, const std::vector<Val> &env, const Val &idx, std::unordered_map<int, Val> &memo) {
+    auto it = memo.find(x);
+    if (it != memo.end()) return it->second;
+    Val r = expr1(x, env, idx, memo);
+    memo[x] = r;
+    return r;
+  }
+
+  Val expr1(int x, const std::vector<Val> &env, const Val &idx, std::unordered_map<int, Val> &memo) {
+    const XNode &n = g_.xs[x];
+    auto go = [&](int y) { return expr(y, env, idx, memo); };
+    switch (n.kind) {
+      case XK::Const:
+        switch (n.dt) {
+          case DT::F32: {
+            float f = (float)n.f;
+            if ((double)f == n.f || std::isnan(n.f)) return {f32_lit(f), VC::F32};
+            return {f64_lit(n.f), VC::F32D};
+          }
+          case DT::F64: return {f64_lit(n.f), VC::F64};
+          case DT::I32: return {i32_lit(n.i), VC::I32};
+          case DT::I64: return {i64_lit(n.i), VC::I64};
+          default: return {n.i ? "true" : "false", VC::B};
+        }
+      case XK::Arg:
+        if (n.arg >= (int)env.size()) throw Failure(strf("Lower: unbound Arg %d", n.arg));
+        return env[n.arg];
+      case XK::Index: return idx;
+      case XK::Bin: return binop(n, go(n.a), go(n.b));
+      case XK::Un: return unop(n, go(n.a));
+      case XK::Cmp: {
+        Val a = go(n.a), b = go(n.b);
+        static const char *ops[] = {"==", "!=", "<", "<=", ">", ">="};
+        std::string sa = a.s, sb = b.s;
+        if (a.c == VC::F32D || b.c == VC::F32D) {
+          sa = as_double(a);
+          sb = as_double(b);
+        }
+        return def(VC::B, "(" + sa + " " + ops[n.op] + " " + sb + ")");
+      }
+      case XK::Logic: {
+        Val a = go(n.a), b = go(n.b);
+        return def(VC::B, "(" + a.s + (n.op == 0 ? " && " : " || ") + b.s + ")");
+      }
+      case XK::Not: return def(VC::B, "(!" + go(n.a).s + ")");
+      case XK::Select: {
+        Val c = go(n.a), a = go(n.b), b = go(n.c);
+        if (a.c == b.c) return def(a.c, "(" + c.s + " ? " + a.s + " : " + b.s + ")");
+        // F32 and F32D meet: keep the exact double.
+        return def(VC::F32D, "(" + c.s + " ? " + as_double(a) + " : " + as_double(b) + ")");
+      }
+      case XK::Cast: return cast(n.dt, g_.xs[n.a].dt, go(n.a));
+    }
+    throw Failure("codegen: bad expression");
+  }
+
+  Val binop(const XNode &n, const Val &a, const Val &b) {
+    switch (n.dt) {
+      case DT::F32: {
+        bool exact = a.c == VC::F32 && b.c == VC::F32;
+        static const char *sym[] = {"+", "-", "*", "/"};
+        if (n.op <= B_DIV) {
+          if (exact) return def(VC::F32, "(" + a.s + " " + sym[n.op] + " " + b.s + ")");
+          return def(VC::F32, "(float)(" + as_double(a) + " " + sym[n.op] + " " + as_double(b) + ")");
+        }
+        const char *fn = n.op == B_MIN ? "cc_min" : "cc_max";
+        if (exact) return def(VC::F32, std::string(fn) + "f(" + a.s + ", " + b.s + ")");
+        return def(VC::F32, std::string("(float)") + fn + "d(" + as_double(a) + ", " + as_double(b) + ")");
+      }
+      case DT::F64: {
+        static const char *sym[] = {"+", "-", "*", "/"};
+        if (n.op <= B_DIV) return def(VC::F64, "(" + a.s + " " + sym[n.op] + " " + b.s + ")");
+        return def(VC::F64, std::string(n.op == B_MIN ? "cc_mind(" : "cc_maxd(") + a.s + ", " + b.s + ")");
+      }
+      case DT::I32:
+      case DT::I64: {
+        bool w = n.dt == DT::I64;
+        const char *T = w ? "long long" : "int";
+        const char *U = w ? "cc_u64" : "cc_u32";
+        VC vc = w ? VC::I64 : VC::I32;
+        auto wrap = [&](const char *sym) {
+          return def(vc, std::string("((") + T + ")((" + U + ")(" + a.s + ") " + sym + " (" + U + ")(" + b.s + ")))");
+        };
+        switch (n.op) {
+          case B_ADD: return wrap("+");
+          case B_SUB: return wrap("-");
+          case B_MUL: return wrap("*");
+          case B_DIV: return def(vc, std::string(w ? "cc_divl(" : "cc_divi(") + a.s + ", " + b.s + ")");
+          case B_MIN: return def(vc, "((" + a.s + " < " + b.s + ") ? " + a.s + " : " + b.s + ")");
+          case B_MAX: return def(vc, "((" + a.s + " > " + b.s + ") ? " + a.s + " : " + b.s + ")");
+          case B_AND: return wrap("&");
+          case B_OR: return wrap("|");
+          case B_XOR: return wrap("^");
+          case B_SHL:
+          case B_SHR: {
+            const char *sym = n.op == B_SHL ? "<<" : ">>";
+            const char *mask = w ? "63" : "31";
+            return def(vc, std::string("((") + T + ")((" + U + ")(" + a.s + ") " + sym + " ((" + U + ")(" + b.s +
+                               ") & " + mask + ")))");
+          }
+        }
+        break;
+      }
+      default: break;
+    }
+    throw Failure("codegen: binop on bool");
+  }
+
+  Val unop(const XNode &n, const Val &a) {
+    static const char *f32n[] = {"", "sqrtf", "expf", "logf", "fabsf", "sinf", "cosf", "erff", "erfinvf"};
+    static const char *f64n[] = {"", "sqrt", "exp", "log", "fabs", "sin", "cos", "erf", "erfinv"};
+    switch (n.dt) {
+      case DT::F32:
+        if (n.op == U_NEG) {
+          if (a.c == VC::F32) return def(VC::F32, "(-" + a.s + ")");
+          return def(VC::F32, "(float)(-" + a.s + ")");
+        }
+        if (a.c == VC::F32) return def(VC::F32, std::string(f32n[n.op]) + "(" + a.s + ")");
+        return def(VC::F32, std::string("(float)") + f64n[n.op] + "(" + a.s + ")");
+      case DT::F64:
+        if (n.op == U_NEG) return def(VC::F64, "(-" + a.s + ")");
+        return def(VC::F64, std::string(f64n[n.op]) + "(" + a.s + ")");
+      case DT::I32:
+        if (n.op == U_NEG) return def(VC::I32, "((int)(0u - (cc_u32)(" + a.s + ")))");
+        return def(VC::I32, "((" + a.s + " < 0) ? (int)(0u - (cc_u32)(" + a.s + ")) : " + a.s + ")");
+      case DT::I64:
+        if (n.op == U_NEG) return def(VC::I64, "((long long)(0ull - (cc_u64)(" + a.s + ")))");
+        return def(VC::I64, "((" + a.s + " < 0) ? (long long)(0ull - (cc_u64)(" + a.s + ")) : " + a.s + ")");
+      default: break;
+    }
+    throw Failure("codegen: unop on bool");
+  }
+
+  // R6 (cudacaml_backend_interp.ml:198-237).
+  Val cast(DT to, DT from, const Val &a) {
+    if (to == from) return a;
+    switch (from) {
+      case DT::F32:
+      case DT::F64: {
+        std::string d = as_double(a);
+        switch (to) {
+          case DT::F32: return def(VC::F32, "(float)(" + d + ")");
+          case DT::F64: return def(VC::F64, d);
+          case DT::I32: return def(VC::I32, "cc_f2i(" + d + ")");
+          case DT::I64: return def(VC::I64, "cc_f2l(" + d + ")");
+          default: return def(VC::B, "(" + d + " != 0.0)");
+        }
+      }
+      case DT::I32:
+      case DT::I64:
+        switch (to) {
+          case DT::F32: return def(VC::F32, "(float)(double)(" + a.s + ")");
+          case DT::F64: return def(VC::F64, "(double)(" + a.s + ")");
+          case DT::I32: return def(VC::I32, "((int)(cc_u32)(cc_u64)(" + a.s + "))");
+          case DT::I64: return def(VC::I64, "((long long)(" + a.s + "))");
+          default: return def(VC::B, "(" + a.s + " != 0)");
+        }
+      default:
+        switch (to) {
+          case DT::F32: return def(VC::F32, "(" + a.s + " ? 1.0f : 0.0f)");
+          case DT::F64: return def(VC::F64, "(" + a.s + " ? 1.0 : 0.0)");
+          case DT::I32: return def(VC::I32, "(" + a.s + " ? 1 : 0)");
+          case DT::I64: return def(VC::I64, "(" + a.s + " ? 1LL : 0LL)");
+          default: return a;
+        }
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
+// The prelude every generated module starts with.
+// ---------------------------------------------------------------------------
+
+const char *kPrelude = R"PRELUDE(// Generated by cchip (Backend_hip) for gfx950.
+typedef unsigned int cc_u32;
+typedef unsigned long long cc_u64;
+template <typename T> struct __attribute__((aligned(4 * sizeof(T)))) cc_v4 { T x, y, z, w; };
+
+// Float.min / Float.max of OCaml: NaN if either operand is NaN, -0 below +0.
+__device__ __forceinline__ float cc_minf(float x, float y) {
+  if (x != x || y != y) return __builtin_nanf("");
+  if (x < y) return x;
+  if (y < x) return y;
+  return __builtin_signbit(x) ? x : y;
+}
+__device__ __forceinline__ float cc_maxf(float x, float y) {
+  if (x != x || y != y) return __builtin_nanf("");
+  if (x > y) return x;
+  if (y > x) return y;
+  return __builtin_signbit(x) ? y : x;
+}
+__device__ __forceinline__ double cc_mind(double x, double y) {
+  if (x != x || y != y) return __builtin_nan("");
+  if (x < y) return x;
+  if (y < x) return y;
+  return __builtin_signbit(x) ? x : y;
+}
+__device__ __forceinline__ double cc_maxd(double x, double y) {
+  if (x != x || y != y) return __builtin_nan("");
+  if (x > y) return x;
+  if (y > x) return y;
+  return __builtin_signbit(x) ? y : x;
+}
+// Int32.div / Int64.div: truncation, min_int / -1 wraps. Division by zero
+// raises in the interpreter; on the device it yields 0.
+__device__ __forceinline__ int cc_divi(int a, int b) {
+  return b == 0 ? 0 : (b == -1 ? (int)(0u - (cc_u32)a) : a / b);
+}
+__device__ __forceinline__ long long cc_divl(long long a, long long b) {
+  return b == 0 ? 0 : (b == -1 ? (long long)(0ull - (cc_u64)a) : a / b);
+}
+// Int64.of_float (truncation; NaN and out-of-range give min_int as the
+// x86-64 conversion does), then Int64.to_int32 (wrap).
+__device__ __forceinline__ long long cc_f2l(double x) {
+  return (x != x || x >= 9223372036854775808.0 || x < -9223372036854775808.0) ? (long long)0x8000000000000000ull
+                                                                              : (long long)x;
+}
+__device__ __forceinline__ int cc_f2i(double x) { return (int)(cc_u32)(cc_u64)cc_f2l(x); }
+__device__ __forceinline__ void cc_flag(int* err, int code) {
+  __hip_atomic_fetch_or(err, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void cc_atomic_add(float* p, float v) { unsafeAtomicAdd(p, v); }
+__device__ __forceinline__ void cc_atomic_add(double* p, double v) { unsafeAtomicAdd(p, v); }
+__device__ __forceinline__ void cc_atomic_add(int* p, int v) { atomicAdd(p, v); }
+__device__ __forceinline__ cc_u64 cc_bits(float v) { return (cc_u64)__float_as_uint(v); }
+__device__ __forceinline__ cc_u64 cc_bits(int v) { return (cc_u64)(cc_u32)v; }
+__device__ __forceinline__ cc_u64 cc_bits(double v) { return (cc_u64)__double_as_longlong(v); }
+__device__ __forceinline__ cc_u64 cc_bits(long long v) { return (cc_u64)v; }
+template <typename T> __device__ __forceinline__ T cc_from_bits(cc_u64 b);
+template <> __device__ __forceinline__ float cc_from_bits<float>(cc_u64 b) { return __uint_as_float((cc_u32)b); }
+template <> __device__ __forceinline__ int cc_from_bits<int>(cc_u64 b) { return (int)(cc_u32)b; }
+template <> __device__ __forceinline__ double cc_from_bits<double>(cc_u64 b) { return __longlong_as_double((long long)b); }
+template <> __device__ __forceinline__ long long cc_from_bits<long long>(cc_u64 b) { return (long long)b; }
+)PRELUDE";
+
+std::string subst(std::string s, const std::map<std::string, std::string> &vars) {
+  for (auto &kv : vars) {
+    std::string key = "${" + kv.first + "}";
+    size_t pos = 0;
+    while ((pos = s.find(key, pos)) != std::string::npos) {
+      s.replace(pos, key.size(), kv.second);
+      pos += kv.second.size();
+    }
+  }
+  return s;
+}
+
+int64_t pow2ceil(int64_t n) {
+  int64_t p = 1;
+  while (p < n) p <<= 1;
+  return p;
+}
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---------------------------------------------------------------------------
+// The lowering proper
+// ---------------------------------------------------------------------------
+
+struct Lowering {
+  const Graph &g;
+  Plan plan;
+  ProgramIR prog;
+  std::vector<int> buf_of;  // tensor position -> buffer index (-1 if none)
+  std::ostringstream src;
+  Gen gen;
+  bool need_err = false;
+
+  explicit Lowering(const Graph &gr) : g(gr), plan(fusion_plan(gr)), gen(gr, plan, buf_of) {
+    gen.bufdt_ = [this](int b) { return prog.bufs[b].dt; };
+  }
+
+  int add_buf(const std::string &name, DT dt, int64_t numel, BufRole role) {
+    BufSpec b;
+    b.name = name;
+    b.dt = dt;
+    b.numel = numel;
+    b.role = role;
+    prog.bufs.push_back(b);
+    return (int)prog.bufs.size() - 1;
+  }
+
+  int err_buf() {
+    if (prog.err_buf < 0) prog.err_buf = add_buf("err", DT::I32, 1, BufRole::Err);
+    return prog.err_buf;
+  }
+
+  std::string ty(int b) const { return dt_ctype(prog.bufs[b].dt); }
+
+  // Kernel parameter list: every buffer the element functions read, then
+  // the written buffers, then the error word.
+  struct Params {
+    std::vector<int> in, out;
+    bool err = false;
+  };
+
+  static void add_in(Params &p, const ElemFn &f) {
+    auto add = [&](int b) {
+      for (int x : p.in)
+        if (x == b) return;
+      p.in.push_back(b);
+    };
+    for (int b : f.ident) add(b);
+    for (int b : f.ptrs) add(b);
+    if (f.uses_err) p.err = true;
+  }
+
+  std::string param_list(const Params &p, std::vector<int> &args) {
+    std::ostringstream os;
+    bool first = true;
+    auto sep = [&]() {
+      if (!first) os << ", ";
+      first = false;
+    };
+    for (int b : p.in) {
+      sep();
+      os << "const " << ty(b) << "* __restrict__ b" << b;
+      args.push_back(b);
+    }
+    for (int b : p.out) {
+      sep();
+      os << ty(b) << "* __restrict__ b" << b;
+      args.push_back(b);
+    }
+    if (p.err) {
+      sep();
+      os << "int* __restrict__ err";
+      args.push_back(err_buf());
+      need_err = true;
+    }
+    return os.str();
+  }
+
+  int add_kernel(const std::string &name, const std::vector<int> &args, int grid, int block, const std::string &role,
+                 int grid_y = 1) {
+    KernelSpec k;
+    k.name = name;
+    k.args = args;
+    k.grid = std::max(1, grid);
+    k.grid_y = std::max(1, grid_y);
+    k.block = block;
+    k.role = role;
+    prog.kernels.push_back(k);
+    return (int)prog.kernels.size() - 1;
+  }
+
+  // Loads of the identity-indexed buffers of `f` as 4-wide vectors at `i`.
+  static std::string vec_loads(const ElemFn &f, const std::string &i, const std::string &indent,
+                               const std::function<std::string(int)> &tyof) {
+    std::string s;
+    for (int b : f.ident)
+      s += indent + "const cc_v4<" + tyof(b) + "> l" + std::to_string(b) + " = *(const cc_v4<" + tyof(b) +
+           ">*)(b" + std::to_string(b) + " + " + i + ");\n";
+    return s;
+  }
+
+  static std::string lane_call(const ElemFn &f, const std::string &i, int k) {
+    static const char *comp[] = {"x", "y", "z", "w"};
+    std::string idx = k == 0 ? i : "(" + i + " + " + std::to_string(k) + ")";
+    return f.call(idx, [&](int b) { return "l" + std::to_string(b) + "." + comp[k]; });
+  }
+
+  std::function<std::string(int)> tyof() {
+    return [this](int b) { return ty(b); };
+  }
+
+  // ---- element-wise root (K1 -> vectorised grid-stride map) --------------
+  std::vector<int> lower_map(int t) {
+    const TNode &n = g.ts[t];
+    std::string kname = "k_" + std::to_string(n.id);
+    int out = buf_of[t];
+    ElemFn f = gen.element_fn("f_" + std::to_string(n.id), t, true, true);
+    src << f.code;
+    Params p;
+    add_in(p, f);
+    p.out.push_back(out);
+    std::vector<int> args;
+    std::string params = param_list(p, args);
+    int64_t N = n.numel;
+    if (N == 0) return {};
+    std::string T = dt_ctype(n.dt);
+    std::ostringstream k;
+    k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
+      << "  const int stride = gridDim.x * 256;\n"
+      << "  const int nvec = " << N / 4 << ";\n"
+      << "  for (int v = blockIdx.x * 256 + threadIdx.x; v < nvec; v += stride) {\n"
+      << "    const int i = v * 4;\n"
+      << vec_loads(f, "i", "    ", tyof()) << "    cc_v4<" << T << "> r;\n";
+    static const char *comp[] = {"x", "y", "z", "w"};
+    for (int u = 0; u < 4; u++) k << "    r." << comp[u] << " = " << lane_call(f, "i", u) << ";\n";
+    k << "    *(cc_v4<" << T << ">*)(b" << out << " + i) = r;\n"
+      << "  }\n"
+      << "  for (int i = nvec * 4 + blockIdx.x * 256 + threadIdx.x; i < " << N << "; i += stride)\n"
+      << "    b" << out << "[i] = " << f.call_scalar("i") << ";\n"
+      << "}\n";
+    src << k.str();
+    int64_t nvec = std::max<int64_t>(1, N / 4);
+    int grid = (int)std::min<int64_t>(cdiv(nvec, 256), 65536);
+    return {add_kernel(kname, args, grid, 256, "map")};
+  }
+
+  // ---- Reduce root (K2-K4 -> wave / block / split-row reductions) --------
+  std::vector<int> lower_reduce(int t) {
+    const TNode &n = g.ts[t];
+    const TNode &s = g.ts[n.a];
+    std::string id = std::to_string(n.id);
+    std::string kname = "k_" + id;
+    std::string T = dt_ctype(n.dt);
+    int out = buf_of[t];
+    int64_t len = row_length(s.shape);
+    int64_t rows = n.numel;
+    std::string cmb = "c_" + id, ini = "z_" + id;
+    src << gen.combine_fn(cmb, n.body, n.dt) << gen.const_fn(ini, n.init, n.dt);
+    if (rows == 0) return {};
+    if (len == 0) {
+      // Every row is empty: the output is init (R2).
+      Params p;
+      p.out.push_back(out);
+      std::vector<int> args;
+      std::string params = param_list(p, args);
+      src << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
+          << "  for (int r = blockIdx.x * 256 + threadIdx.x; r < " << rows << "; r += gridDim.x * 256) b" << out
+          << "[r] = " << ini << "();\n}\n";
+      return {add_kernel(kname, args, (int)std::min<int64_t>(cdiv(rows, 256), 4096), 256, "reduce_empty")};
+    }
+    ElemFn f = gen.element_fn("f_" + id, n.a, false, true);
+    src << f.code;
+    bool vec = len % 4 == 0;
+    if (len <= 2048) {
+      // One wave (or a power-of-two segment of one) per row.
+      int64_t S = std::min<int64_t>(64, pow2ceil(len));
+      int64_t rpw = 64 / S;
+      Params p;
+      add_in(p, f);
+      p.out.push_back(out);
+      std::vector<int> args;
+      std::string params = param_list(p, args);
+      std::ostringstream k;
+      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
+        << "  const int lane = threadIdx.x & 63;\n"
+        << "  const int seg = lane / " << S << ";\n"
+        << "  const int sl = lane - seg * " << S << ";\n"
+        << "  const int wave = (blockIdx.x * 256 + threadIdx.x) >> 6;\n"
+        << "  const int nwaves = gridDim.x * 4;\n"
+        << "  for (int rb = wave * " << rpw << "; rb < " << rows << "; rb += nwaves * " << rpw << ") {\n"
+        << "    const int r = rb + seg;\n"
+        << "    " << T << " acc = " << ini << "();\n"
+        << "    if (r < " << rows << ") {\n"
+        << "      for (int j = sl; j < " << len << "; j += " << S << ") {\n"
+        << "        const int i = r * " << len << " + j;\n"
+        << "        acc = " << cmb << "(acc, " << f.call_scalar("i") << ");\n"
+        << "      }\n"
+        << "    }\n";
+      for (int64_t off = S / 2; off > 0; off /= 2) k << "    acc = " << cmb << "(acc, __shfl_xor(acc, " << off << "));\n";
+      k << "    if (r < " << rows << " && sl == 0) b" << out << "[r] = acc;\n"
+        << "  }\n}\n";
+      src << k.str();
+      int64_t waves = cdiv(rows, rpw);
+      int grid = (int)std::min<int64_t>(cdiv(waves, 4), 16384);
+      return {add_kernel(kname, args, grid, 256, "reduce_wave")};
+    }
+    std::string block_reduce =
+        "    for (int off = 32; off > 0; off >>= 1) acc = " + cmb +
+        "(acc, __shfl_xor(acc, off));\n"
+        "    if (lane == 0) wpart[wid] = acc;\n"
+        "    __syncthreads();\n";
+    auto fold_loop = [&](const std::string &lo, const std::string &hi) {
+      std::ostringstream l;
+      if (vec) {
+        l << "    for (int j = " << lo << " + threadIdx.x * 4; j < " << hi << "; j += 1024) {\n"
+          << "      const int i = base + j;\n"
+          << vec_loads(f, "i", "      ", tyof());
+        for (int u = 0; u < 4; u++) l << "      acc = " << cmb << "(acc, " << lane_call(f, "i", u) << ");\n";
+        l << "    }\n";
+      } else {
+        l << "    for (int j = " << lo << " + threadIdx.x; j < " << hi << "; j += 256) {\n"
+          << "      const int i = base + j;\n"
+          << "      acc = " << cmb << "(acc, " << f.call_scalar("i") << ");\n"
+          << "    }\n";
+      }
+      return l.str();
+    };
+    if (rows >= 512) {
+      // One workgroup per row.
+      Params p;
+      add_in(p, f);
+      p.out.push_back(out);
+      std::vector<int> args;
+      std::string params = param_list(p, args);
+      std::ostringstream k;
+      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
+        << "  __shared__ " << T << " wpart[4];\n"
+        << "  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;\n"
+        << "  for (int r = blockIdx.x; r < " << rows << "; r += gridDim.x) {\n"
+        << "    const int base = r * " << len << ";\n"
+        << "    " << T << " acc = " << ini << "();\n"
+        << fold_loop("0", std::to_string(len)) << block_reduce << "    if (threadIdx.x == 0) {\n"
+        << "      " << T << " t = wpart[0];\n"
+        << "      t = " << cmb << "(t, wpart[1]);\n"
+        << "      t = " << cmb << "(t, wpart[2]);\n"
+        << "      t = " << cmb << "(t, wpart[3]);\n"
+        << "      b" << out << "[r] = t;\n"
+        << "    }\n"
+        << "    __syncthreads();\n"
+        << "  }\n}\n";
+      src << k.str();
+      int grid = (int)std::min<int64_t>(rows, 1 << 20);
+      return {add_kernel(kname, args, grid, 256, "reduce_block")};
+    }
+    // Few long rows: split each row over G workgroups; the last one to
+    // finish a row folds the row's partials (one launch, no second pass).
+    int64_t unit = vec ? 1024 : 256;
+    int64_t G = std::max<int64_t>(1, std::min<int64_t>(cdiv(2048, rows), cdiv(len, 4096)));
+    int64_t chunk = cdiv(cdiv(len, G), unit) * unit;
+    G = cdiv(len, chunk);
+    int part = add_buf("t" + id + "_partials", n.dt, rows * G, BufRole::Scratch);
+    int cnt = add_buf("t" + id + "_count", DT::I32, rows, BufRole::Scratch);
+    Params p;
+    add_in(p, f);
+    p.out.push_back(out);
+    p.out.push_back(part);
+    p.out.push_back(cnt);
+    std::vector<int> args;
+    std::string params = param_list(p, args);
+    std::ostringstream k;
+    k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
+      << "  __shared__ " << T << " wpart[4];\n"
+      << "  __shared__ int s_last;\n"
+      << "  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;\n"
+      << "  const int r = blockIdx.x / " << G << ";\n"
+      << "  const int g = blockIdx.x - r * " << G << ";\n"
+      << "  const int base = r * " << len << ";\n"
+      << "  const int lo = g * " << chunk << ";\n"
+      << "  const int hi = min(lo + " << chunk << ", " << len << ");\n"
+      << "  {\n"
+      << "    " << T << " acc = " << ini << "();\n"
+      << fold_loop("lo", "hi") << block_reduce << "    if (threadIdx.x == 0) {\n"
+      << "      " << T << " t = wpart[0];\n"
+      << "      t = " << cmb << "(t, wpart[1]);\n"
+      << "      t = " << cmb << "(t, wpart[2]);\n"
+      << "      t = " << cmb << "(t, wpart[3]);\n"
+      << "      __hip_atomic_store(&b" << part << "[blockIdx.x], t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
+      << "      const int prev = __hip_atomic_fetch_add(&b" << cnt
+      << "[r], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);\n"
+      << "      s_last = prev == " << G - 1 << ";\n"
+      << "    }\n"
+      << "    __syncthreads();\n"
+      << "  }\n"
+      << "  if (s_last) {\n"
+      << "    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, \"agent\");\n"
+      << "    " << T << " acc = " << ini << "();\n"
+      << "    for (int q = threadIdx.x; q < " << G << "; q += 256)\n"
+      << "      acc = " << cmb << "(acc, __hip_atomic_load(&b" << part << "[r * " << G
+      << " + q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));\n"
+      << block_reduce << "    if (threadIdx.x == 0) {\n"
+      << "      " << T << " t = wpart[0];\n"
+      << "      t = " << cmb << "(t, wpart[1]);\n"
+      << "      t = " << cmb << "(t, wpart[2]);\n"
+      << "      t = " << cmb << "(t, wpart[3]);\n"
+      << "      b" << out << "[r] = t;\n"
+      << "      __hip_atomic_store(&b" << cnt << "[r], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
+      << "    }\n"
+      << "  }\n}\n";
+    src << k.str();
+    return {add_kernel(kname, args, (int)(rows * G), 256, "reduce_split")};
+  }
+
+  // ---- Scan root (K5-K8 -> wave / block / decoupled look-back scans) -----
+  std::vector<int> lower_scan(int t) {
+    const TNode &n = g.ts[t];
+    std::string id = std::to_string(n.id);
+    std::string kname = "k_" + id;
+    std::string T = dt_ctype(n.dt);
+    int out = buf_of[t];
+    int64_t len = row_length(n.shape);
+    int64_t rows = len == 0 ? 0 : n.numel / len;
+    std::string cmb = "c_" + id, ini = "z_" + id;
+    src << gen.combine_fn(cmb, n.body, n.dt) << gen.const_fn(ini, n.init, n.dt);
+    if (rows == 0) return {};
+    ElemFn f = gen.element_fn("f_" + id, n.a, false, true);
+    src << f.code;
+    bool wide = dt_size(n.dt) == 8;
+    if (len <= 64) {
+      int64_t S = pow2ceil(len);
+      int64_t rpw = 64 / S;
+      Params p;
+      add_in(p, f);
+      p.out.push_back(out);
+      std::vector<int> args;
+      std::string params = param_list(p, args);
+      std::ostringstream k;
+      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
+        << "  const int lane = threadIdx.x & 63;\n"
+        << "  const int seg = lane / " << S << ";\n"
+        << "  const int sl = lane - seg * " << S << ";\n"
+        << "  const int wave = (blockIdx.x * 256 + threadIdx.x) >> 6;\n"
+        << "  const int nwaves = gridDim.x * 4;\n"
+        << "  for (int rb = wave * " << rpw << "; rb < " << rows << "; rb += nwaves * " << rpw << ") {\n"
+        << "    const int r = rb + seg;\n"
+        << "    const bool valid = r < " << rows << " && sl < " << len << ";\n"
+        << "    const int i = r * " << len << " + sl;\n"
+        << "    " << T << " v = " << ini << "();\n"
+        << "    if (valid) v = " << f.call_scalar("i") << ";\n"
+        << "    if (sl == 0) v = " << cmb << "(" << ini << "(), v);\n";
+      for (int64_t off = 1; off < S; off *= 2)
+        k << "    { const " << T << " u = __shfl_up(v, " << off << "); if (sl >= " << off << ") v = " << cmb
+          << "(u, v); }\n";
+      k << "    if (valid) b" << out << "[i] = v;\n"
+        << "  }\n}\n";
+      src << k.str();
+      int64_t waves = cdiv(rows, rpw);
+      int grid = (int)std::min<int64_t>(cdiv(waves, 4), 65536);
+      return {add_kernel(kname, args, grid, 256, "scan_wave")};
+    }
+    // Shared pieces of the block-level scan: striped load into LDS, each
+    // thread scans ITEMS consecutive elements, the block scans the thread
+    // totals, and the prefix is folded back in. LDS is padded one slot per
+    // 32 so the blocked reads are conflict-free.
+    auto block_scan = [&](int64_t items, const std::string &rowlen, const std::string &first_cond) {
+      std::ostringstream b;
+      b << "    " << T << " v[" << items << "];\n"
+        << "#pragma unroll\n"
+        << "    for (int q = 0; q < " << items << "; q++) { const int e = threadIdx.x * " << items
+        << " + q; v[q] = sm[e + (e >> 5)]; }\n"
+        << "    if (" << first_cond << ") v[0] = " << cmb << "(" << ini << "(), v[0]);\n"
+        << "#pragma unroll\n"
+        << "    for (int q = 1; q < " << items << "; q++) v[q] = " << cmb << "(v[q - 1], v[q]);\n"
+        << "    " << T << " incl = v[" << items - 1 << "];\n";
+      for (int off = 1; off < 64; off *= 2)
+        b << "    { const " << T << " u = __shfl_up(incl, " << off << "); if (lane >= " << off << ") incl = " << cmb
+          << "(u, incl); }\n";
+      b << "    const " << T << " excl = __shfl_up(incl, 1);\n"
+        << "    if (lane == 63) wsum[wid] = incl;\n"
+        << "    __syncthreads();\n"
+        << "    bool has = false;\n"
+        << "    " << T << " pre = " << ini << "();\n"
+        << "    for (int w = 0; w < wid; w++) { pre = has ? " << cmb << "(pre, wsum[w]) : wsum[w]; has = true; }\n"
+        << "    if (lane > 0) { pre = has ? " << cmb << "(pre, excl) : excl; has = true; }\n"
+        << "    if (has) {\n"
+        << "#pragma unroll\n"
+        << "      for (int q = 0; q < " << items << "; q++) v[q] = " << cmb << "(pre, v[q]);\n"
+        << "    }\n";
+      (void)rowlen;
+      return b.str();
+    };
+    auto striped_load = [&](int64_t padded, const std::string &base, const std::string &valid_len, bool vec) {
+      std::ostringstream b;
+      if (vec) {
+        b << "    for (int e = threadIdx.x * 4; e < " << padded << "; e += 1024) {\n"
+          << "      if (e < " << valid_len << ") {\n"
+          << "        const int i = " << base << " + e;\n"
+          << vec_loads(f, "i", "        ", tyof());
+        static const char *comp[] = {"x", "y", "z", "w"};
+        for (int u = 0; u < 4; u++)
+          b << "        { const int ee = e + " << u << "; sm[ee + (ee >> 5)] = " << lane_call(f, "i", u) << "; }\n";
+        (void)comp;
+        b << "      } else {\n"
+          << "        for (int u = 0; u < 4; u++) { const int ee = e + u; sm[ee + (ee >> 5)] = " << ini << "(); }\n"
+          << "      }\n"
+          << "    }\n";
+      } else {
+        b << "    for (int e = threadIdx.x; e < " << padded << "; e += 256) {\n"
+          << "      " << T << " x = " << ini << "();\n"
+          << "      if (e < " << valid_len << ") x = " << f.call_scalar(base + " + e") << ";\n"
+          << "      sm[e + (e >> 5)] = x;\n"
+          << "    }\n";
+      }
+      b << "    __syncthreads();\n";
+      return b.str();
+    };
+    int64_t block_max = wide ? 8192 : 16384;
+    if (len <= block_max && rows >= 128) {
+      int64_t items = cdiv(len, 256);
+      int64_t padded = items * 256;
+      // Vector loads need every row start and the padded tail to stay in
+      // 4-element groups.
+      bool vec = len % 4 == 0;
+      Params p;
+      add_in(p, f);
+      p.out.push_back(out);
+      std::vector<int> args;
+      std::string params = param_list(p, args);
+      std::ostringstream k;
+      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
+        << "  __shared__ " << T << " sm[" << padded + padded / 32 << "];\n"
+        << "  __shared__ " << T << " wsum[4];\n"
+        << "  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;\n"
+        << "  for (int r = blockIdx.x; r < " << rows << "; r += gridDim.x) {\n"
+        << "    const int base = r * " << len << ";\n"
+        << striped_load(padded, "base", std::to_string(len), vec) << block_scan(items, "", "threadIdx.x == 0")
+        << "#pragma unroll\n"
+        << "    for (int q = 0; q < " << items << "; q++) { const int e = threadIdx.x * " << items
+        << " + q; sm[e + (e >> 5)] = v[q]; }\n"
+        << "    __syncthreads();\n"
+        << "    for (int e = threadIdx.x; e < " << len << "; e += 256) b" << out << "[base + e] = sm[e + (e >> 5)];\n"
+        << "    __syncthreads();\n"
+        << "  }\n}\n";
+      src << k.str();
+      int grid = (int)std::min<int64_t>(rows, 1 << 20);
+      return {add_kernel(kname, args, grid, 256, "scan_block")};
+    }
+    // Long rows: single-pass scan with decoupled look-back. Tiles are handed
+    // out in launch order by an atomic counter, so a tile only ever waits on
+    // tiles whose workgroups are already running. Status words carry the
+    // flag (1 = aggregate, 2 = inclusive prefix) in the high half and the
+    // value bits in the low half; 8-byte values use two words, each tagged.
+    int64_t items = wide ? 8 : 16;
+    int64_t tile = 256 * items;
+    int64_t tpr = cdiv(len, tile);
+    int64_t tiles = rows * tpr;
+    int words = wide ? 2 : 1;
+    int status = add_buf("t" + id + "_status", DT::I64, tiles * words, BufRole::Scratch);
+    int ctr = add_buf("t" + id + "_tiles", DT::I32, 2, BufRole::Scratch);
+    need_err = true;
+    int e = err_buf();
+    // init kernel: zero the status words and the tile counter.
+    std::string iname = kname + "_init";
+    {
+      std::ostringstream k;
+      k << "extern \"C\" __global__ __launch_bounds__(256) void " << iname << "(long long* __restrict__ b" << status
+        << ", int* __restrict__ b" << ctr << ") {\n"
+        << "  const int stride = gridDim.x * 256;\n"
+        << "  for (int q = blockIdx.x * 256 + threadIdx.x; q < " << tiles * words << "; q += stride) b" << status
+        << "[q] = 0;\n"
+        << "  if (blockIdx.x == 0 && threadIdx.x < 2) b" << ctr << "[threadIdx.x] = 0;\n"
+        << "}\n";
+      src << k.str();
+    }
+    int kinit =
+        add_kernel(iname, {status, ctr}, (int)std::min<int64_t>(cdiv(tiles * words, 256), 1024), 256, "scan_init");
+    Params p;
+    add_in(p, f);
+    p.out.push_back(out);
+    std::vector<int> args;
+    std::string params = param_list(p, args);
+    args.push_back(status);
+    args.push_back(ctr);
+    if (!p.err) args.push_back(e);
+    std::string pub, poll;
+    if (!wide) {
+      pub =
+          "__hip_atomic_store(&st[TILE], ((cc_u64)(FLAG) << 32) | cc_bits(VAL), __ATOMIC_RELAXED, "
+          "__HIP_MEMORY_SCOPE_AGENT)";
+    } else {
+      pub =
+          "{ const cc_u64 bb = cc_bits(VAL); "
+          "__hip_atomic_store(&st[2 * (TILE)], ((cc_u64)(FLAG) << 32) | (bb & 0xffffffffull), __ATOMIC_RELAXED, "
+          "__HIP_MEMORY_SCOPE_AGENT); "
+          "__hip_atomic_store(&st[2 * (TILE) + 1], ((cc_u64)(FLAG) << 32) | (bb >> 32), __ATOMIC_RELAXED, "
+          "__HIP_MEMORY_SCOPE_AGENT); }";
+    }
+    auto publish = [&](const std::string &tl, const std::string &flag, const std::string &val) {
+      std::string s = pub;
+      auto rep = [&](const std::string &a, const std::string &b) {
+        size_t q = 0;
+        while ((q = s.find(a, q)) != std::string::npos) {
+          s.replace(q, a.size(), b);
+          q += b.size();
+        }
+      };
+      rep("TILE", tl);
+      rep("FLAG", flag);
+      rep("VAL", val);
+      return s;
+    };
+    std::ostringstream k;
+    k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params
+      << (params.empty() ? "" : ", ") << "cc_u64* __restrict__ st, int* __restrict__ ctr"
+      << (p.err ? "" : ", int* __restrict__ err") << ") {\n"
+      << "  __shared__ " << T << " sm[" << tile + tile / 32 << "];\n"
+      << "  __shared__ " << T << " wsum[4];\n"
+      << "  __shared__ " << T << " s_agg;\n"
+      << "  __shared__ " << T << " s_prefix;\n"
+      << "  __shared__ int s_tile;\n"
+      << "  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;\n"
+      << "  if (threadIdx.x == 0) s_tile = atomicAdd(ctr, 1);\n"
+      << "  __syncthreads();\n"
+      << "  const int tile = s_tile;\n"
+      << "  const int row = tile / " << tpr << ";\n"
+      << "  const int tin = tile - row * " << tpr << ";\n"
+      << "  const int base = row * " << len << " + tin * " << tile << ";\n"
+      << "  const int len = min(" << tile << ", " << len << " - tin * " << tile << ");\n"
+      << "  {\n"
+      << striped_load(tile, "base", "len", len % 4 == 0 && tile % 4 == 0)
+      << block_scan(items, "", "tin == 0 && threadIdx.x == 0") << "    if (threadIdx.x == 255) {\n"
+      << "      s_agg = v[" << items - 1 << "];\n"
+      << "      " << publish("tile", "tin == 0 ? 2 : 1", "v[" + std::to_string(items - 1) + "]") << ";\n"
+      << "    }\n"
+      << "    __syncthreads();\n"
+      << "    if (tin > 0 && wid == 0) {\n"
+      << "      const int rowstart = row * " << tpr << ";\n"
+      << "      " << T << " acc = " << ini << "();\n"
+      << "      bool have = false;\n"
+      << "      int j = tile - 1;\n"
+      << "      unsigned spins = 0;\n"
+      << "      while (true) {\n"
+      << "        const int q = j - lane;\n"
+      << "        int flag = 2;\n"
+      << "        " << T << " val = " << ini << "();\n"
+      << "        if (q >= rowstart) {\n"
+      << "          while (true) {\n";
+    if (!wide) {
+      k << "            const cc_u64 w = __hip_atomic_load(&st[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
+        << "            flag = (int)(w >> 32);\n"
+        << "            if (flag != 0) { val = cc_from_bits<" << T << ">(w & 0xffffffffull); break; }\n";
+    } else {
+      k << "            const cc_u64 w0 = __hip_atomic_load(&st[2 * q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
+        << "            const cc_u64 w1 = __hip_atomic_load(&st[2 * q + 1], __ATOMIC_RELAXED, "
+           "__HIP_MEMORY_SCOPE_AGENT);\n"
+        << "            flag = (int)(w0 >> 32);\n"
+        << "            if (flag != 0 && flag == (int)(w1 >> 32)) { val = cc_from_bits<" << T
+        << ">((w0 & 0xffffffffull) | (w1 << 32)); break; }\n";
+    }
+    k << "            if (++spins > (1u << 24)) { cc_flag(err, 4); flag = 2; break; }\n"
+      << "            __builtin_amdgcn_s_sleep(1);\n"
+      << "          }\n"
+      << "        }\n"
+      << "        const cc_u64 pm = __ballot(flag == 2);\n"
+      << "        const int L = pm ? (__ffsll((long long)pm) - 1) : 63;\n"
+      << "        " << T << " w = lane <= L ? val : " << ini << "();\n";
+    for (int off = 1; off < 64; off *= 2)
+      k << "        { const " << T << " o = __shfl_down(w, " << off << "); if ((lane & " << (2 * off - 1)
+        << ") == 0) w = " << cmb << "(o, w); }\n";
+    k << "        w = __shfl(w, 0);\n"
+      << "        acc = have ? " << cmb << "(w, acc) : w;\n"
+      << "        have = true;\n"
+      << "        if (pm) break;\n"
+      << "        j -= 64;\n"
+      << "      }\n"
+      << "      if (lane == 0) {\n"
+      << "        s_prefix = acc;\n"
+      << "        const " << T << " incl = " << cmb << "(acc, s_agg);\n"
+      << "        " << publish("tile", "2", "incl") << ";\n"
+      << "      }\n"
+      << "    }\n"
+      << "    __syncthreads();\n"
+      << "    if (tin > 0) {\n"
+      << "      const " << T << " pfx = s_prefix;\n"
+      << "#pragma unroll\n"
+      << "      for (int q = 0; q < " << items << "; q++) v[q] = " << cmb << "(pfx, v[q]);\n"
+      << "    }\n"
+      << "#pragma unroll\n"
+      << "    for (int q = 0; q < " << items << "; q++) { const int e = threadIdx.x * " << items
+      << " + q; sm[e + (e >> 5)] = v[q]; }\n"
+      << "    __syncthreads();\n"
+      << "    for (int e = threadIdx.x; e < len; e += 256) b" << out << "[base + e] = sm[e + (e >> 5)];\n"
+      << "  }\n}\n";
+    src << k.str();
+    int kscan = add_kernel(kname, args, (int)tiles, 256, "scan_lookback");
+    return {kinit, kscan};
+  }
+
+  // ---- Scatter_add root (K9 zero fill + K10 atomics) ---------------------
+  std::vector<int> lower_scatter(int t) {
+    const TNode &n = g.ts[t];
+    std::string id = std::to_string(n.id);
+    std::string kname = "k_" + id;
+    std::string T = dt_ctype(n.dt);
+    int out = buf_of[t];
+    int64_t M = n.numel;
+    int64_t N = g.ts[n.a].numel;
+    std::vector<int> ks;
+    if (M > 0) {
+      std::ostringstream z;
+      z << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_zero(" << T << "* __restrict__ b"
+        << out << ") {\n"
+        << "  for (int i = blockIdx.x * 256 + threadIdx.x; i < " << M << "; i += gridDim.x * 256) b" << out
+        << "[i] = " << zero_of(n.dt) << ";\n}\n";
+      src << z.str();
+      ks.push_back(add_kernel(kname + "_zero", {out}, (int)std::min<int64_t>(cdiv(M, 256), 16384), 256, "scatter_zero"));
+    }
+    if (N == 0) return ks;
+    ElemFn fi = gen.element_fn("fi_" + id, n.a, false, true);
+    ElemFn fs = gen.element_fn("fs_" + id, n.b, false, true);
+    src << fi.code << fs.code;
+    Params p;
+    add_in(p, fi);
+    add_in(p, fs);
+    p.out.push_back(out);
+    p.err = true;
+    std::vector<int> args;
+    std::string params = param_list(p, args);
+    // Identity loads shared by both functions are loaded once.
+    ElemFn both;
+    both.ident = fi.ident;
+    for (int b : fs.ident) {
+      bool dup = false;
+      for (int x : both.ident) dup |= x == b;
+      if (!dup) both.ident.push_back(b);
+    }
+    std::ostringstream k;
+    k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
+      << "  const int stride = gridDim.x * 256;\n"
+      << "  const int nvec = " << N / 4 << ";\n"
+      << "  for (int v = blockIdx.x * 256 + threadIdx.x; v < nvec; v += stride) {\n"
+      << "    const int i = v * 4;\n"
+      << vec_loads(both, "i", "    ", tyof());
+    for (int u = 0; u < 4; u++)
+      k << "    { const int j = " << lane_call(fi, "i", u) << "; const " << T << " x = " << lane_call(fs, "i", u)
+        << ";\n      if ((unsigned)j < " << M << "u) cc_atomic_add(b" << out << " + j, x); else cc_flag(err, 2); }\n";
+    k << "  }\n"
+      << "  for (int i = nvec * 4 + blockIdx.x * 256 + threadIdx.x; i < " << N << "; i += stride) {\n"
+      << "    const int j = " << fi.call_scalar("i") << "; const " << T << " x = " << fs.call_scalar("i") << ";\n"
+      << "    if ((unsigned)j < " << M << "u) cc_atomic_add(b" << out << " + j, x); else cc_flag(err, 2);\n"
+      << "  }\n}\n";
+    src << k.str();
+    int64_t nvec = std::max<int64_t>(1, N / 4);
+    ks.push_back(add_kernel(kname, args, (int)std::min<int64_t>(cdiv(nvec, 256), 65536), 256, "scatter_atomic"));
+    return ks;
+  }
+
+  // ---- Matmul root (K11) --------------------------------------------------
+  // Generic tiled product: one output per thread, k ascending, each product
+  // and sum rounded separately, zero-padded edge tiles. For float dtypes
+  // this reproduces the interpreter's rounding exactly (R9).
+  std::vector<int> lower_matmul(int t) {
+    const TNode &n = g.ts[t];
+    std::string id = std::to_string(n.id);
+    std::string kname = "k_" + id;
+    std::string T = dt_ctype(n.dt);
+    int out = buf_of[t];
+    int64_t M = n.shape[0], N = n.shape[1];
+    int64_t K = g.ts[n.a].shape[1];
+    if (M == 0 || N == 0) return {};
+    ElemFn fa = gen.element_fn("fa_" + id, n.a, false, false);
+    ElemFn fb = gen.element_fn("fb_" + id, n.b, false, false);
+    src << fa.code << fb.code;
+    Params p;
+    add_in(p, fa);
+    add_in(p, fb);
+    p.out.push_back(out);
+    std::vector<int> args;
+    std::string params = param_list(p, args);
+    auto mul = [&](const std::string &a, const std::string &b) {
+      if (dt_is_float(n.dt)) return "(" + a + " * " + b + ")";
+      std::string U = n.dt == DT::I64 ? "cc_u64" : "cc_u32";
+      return "((" + T + ")((" + U + ")(" + a + ") * (" + U + ")(" + b + ")))";
+    };
+    auto add = [&](const std::string &a, const std::string &b) {
+      if (dt_is_float(n.dt)) return "(" + a + " + " + b + ")";
+      std::string U = n.dt == DT::I64 ? "cc_u64" : "cc_u32";
+      return "((" + T + ")((" + U + ")(" + a + ") + (" + U + ")(" + b + ")))";
+    };
+    int64_t nt = cdiv(K, 16);
+    std::ostringstream k;
+    k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
+      << "  __shared__ " << T << " sa[16][17];\n"
+      << "  __shared__ " << T << " sb[16][17];\n"
+      << "  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;\n"
+      << "  const int row = blockIdx.y * 16 + ty, col = blockIdx.x * 16 + tx;\n"
+      << "  " << T << " acc = " << zero_of(n.dt) << ";\n"
+      << "  for (int kt = 0; kt < " << nt << "; kt++) {\n"
+      << "    const int ka = kt * 16 + tx, kb = kt * 16 + ty;\n"
+      << "    sa[ty][tx] = (row < " << M << " && ka < " << K << ") ? " << fa.call_scalar("row * " + std::to_string(K) + " + ka")
+      << " : " << zero_of(n.dt) << ";\n"
+      << "    sb[ty][tx] = (kb < " << K << " && col < " << N << ") ? " << fb.call_scalar("kb * " + std::to_string(N) + " + col")
+      << " : " << zero_of(n.dt) << ";\n"
+      << "    __syncthreads();\n"
+      << "#pragma unroll\n"
+      << "    for (int q = 0; q < 16; q++) acc = " << add("acc", mul("sa[ty][q]", "sb[q][tx]")) << ";\n"
+      << "    __syncthreads();\n"
+      << "  }\n"
+      << "  if (row < " << M << " && col < " << N << ") b" << out << "[row * " << N << " + col] = acc;\n"
+      << "}\n";
+    src << k.str();
+    return {add_kernel(kname, args, (int)cdiv(N, 16), 256, "matmul_tiled", (int)cdiv(M, 16))};
+  }
+
+  void run() {
+    prog.name = g.name;
+    buf_of.assign(g.ts.size(), -1);
+    // Buffers: params first (in Graph.params order = topological order of
+    // params), then the computed materialised nodes (lower.ml:977-990).
+    for (size_t i = 0; i < g.ts.size(); i++)
+      if (plan.materialized[i] && g.ts[i].kind == TK::Param)
+        buf_of[i] = add_buf("p_" + g.ts[i].pname, g.ts[i].dt, g.ts[i].numel, BufRole::Param);
+    for (size_t i = 0; i < g.ts.size(); i++)
+      if (plan.materialized[i] && g.ts[i].kind != TK::Param)
+        buf_of[i] = add_buf("t" + std::to_string(g.ts[i].id), g.ts[i].dt, g.ts[i].numel, BufRole::Computed);
+    int ncomputed = (int)prog.bufs.size();
+    src << kPrelude;
+    std::vector<std::vector<int>> launches;
+    std::vector<std::vector<int>> scratch_of;
+    for (int r : plan.roots) {
+      size_t before = prog.bufs.size();
+      std::vector<int> ks;
+      switch (g.ts[r].kind) {
+        case TK::Map:
+        case TK::Map2:
+        case TK::Iota:
+        case TK::Gather:
+        case TK::Reshape:
+        case TK::Broadcast: ks = lower_map(r); break;
+        case TK::Reduce: ks = lower_reduce(r); break;
+        case TK::Scan: ks = lower_scan(r); break;
+        case TK::Scatter: ks = lower_scatter(r); break;
+        case TK::Matmul: ks = lower_matmul(r); break;
+        default: throw Failure("Lower: a Param never gets a kernel");
+      }
+      std::vector<int> sc;
+      for (size_t b = before; b < prog.bufs.size(); b++)
+        if (prog.bufs[b].role == BufRole::Scratch) sc.push_back((int)b);
+      launches.push_back(ks);
+      scratch_of.push_back(sc);
+    }
+    prog.source = src.str();
+    for (size_t i = 0; i < g.ts.size(); i++)
+      if (g.ts[i].kind == TK::Param) prog.params.push_back({g.ts[i].pname, g.ts[i].dt, g.ts[i].shape, buf_of[i]});
+    for (auto &o : g.outputs) prog.outputs.push_back({o.first, g.ts[o.second].dt, g.ts[o.second].shape, buf_of[o.second]});
+    // Host plan.
+    for (int b = 0; b < ncomputed; b++) prog.plan.push_back({OpK::Alloc, b, -1, ""});
+    if (prog.err_buf >= 0) prog.plan.push_back({OpK::Alloc, prog.err_buf, -1, ""});
+    for (auto &p : prog.params) prog.plan.push_back({OpK::Upload, p.buf, -1, p.name});
+    for (size_t r = 0; r < launches.size(); r++) {
+      for (int b : scratch_of[r]) prog.plan.push_back({OpK::Alloc, b, -1, ""});
+      for (int k : launches[r]) prog.plan.push_back({OpK::Launch, -1, k, ""});
+      for (int b : scratch_of[r]) prog.plan.push_back({OpK::Free, b, -1, ""});
+    }
+    for (auto &o : prog.outputs) prog.plan.push_back({OpK::Download, o.buf, -1, o.name});
+    for (int b = 0; b < ncomputed; b++) prog.plan.push_back({OpK::Free, b, -1, ""});
+    if (prog.err_buf >= 0) prog.plan.push_back({OpK::Free, prog.err_buf, -1, ""});
+  }
+};
+
+}  // namespace
+
+ProgramIR lower_program(const Graph &g) {
+  Lowering l(g);
+  l.run();
+  return l.prog;
+}
+
+std::string plan_to_string(const ProgramIR &p) {
+  std::ostringstream os;
+  os << "program " << p.name << "\n";
+  for (size_t i = 0; i < p.bufs.size(); i++) {
+    const BufSpec &b = p.bufs[i];
+    static const char *roles[] = {"param", "computed", "scratch", "err"};
+    os << "buffer " << i << " " << b.name << " " << dt_name(b.dt) << " " << b.numel << " " << roles[(int)b.role]
+       << "\n";
+  }
+  for (auto &k : p.kernels) {
+    os << "kernel " << k.name << " " << k.role << " grid " << k.grid << " " << k.grid_y << " block " << k.block
+       << " args";
+    for (int a : k.args) os << " " << a;
+    os << "\n";
+  }
+  for (auto &o : p.plan) {
+    switch (o.kind) {
+      case OpK::Alloc: os << "alloc " << p.bufs[o.buf].name << "\n"; break;
+      case OpK::Upload: os << "upload " << o.name << " " << p.bufs[o.buf].name << "\n"; break;
+      case OpK::Launch: os << "launch " << p.kernels[o.kernel].name << "\n"; break;
+      case OpK::Download: os << "download " << o.name << " " << p.bufs[o.buf].name << "\n"; break;
+      case OpK::Free: os << "free " << p.bufs[o.buf].name << "\n"; break;
+    }
+  }
+  return os.str();
+}
+
+}  // namespace cchip

@@ -1,0 +1,155 @@
+"""Parity on the device: every graph runs on Backend_hip and on the CPU
+oracle, through ``differential.check`` (the reference's contract) and the
+per-output policy (bit-exact integers, 2 ulp f32 element-wise, 1e-4 f32
+accumulations, 1e-12 f64). Mirrors the reference's system tests S1-S13
+(test/system/test_system.ml:117-219) at sizes the oracle finishes in
+seconds."""
+
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from cudacaml_amd import backend_hip as H
+from cudacaml_amd import differential as Diff
+from cudacaml_amd import dsl as D
+from cudacaml_amd import rng
+from cudacaml_amd.examples import black_scholes as bs
+from cudacaml_amd.examples import configs as C
+from cudacaml_amd.examples import programs as P
+from cudacaml_amd.examples import saxpy as sx
+from cudacaml_amd.ir import F32, F64, I32, I64, Graph
+
+pytestmark = pytest.mark.gpu
+
+
+def both(g, inputs):
+    exp = oracle.Interp.run(oracle.Interp.compile(g), inputs)
+    c = H.compile(g)
+    try:
+        got = H.run(c, inputs)
+    finally:
+        c.release()
+    return exp, got
+
+
+def assert_policy(g, inputs):
+    exp, got = both(g, inputs)
+    vs = Diff.policy_check(g, exp, got)
+    bad = [v for v in vs if not v.ok]
+    assert not bad, bad
+    return exp, got
+
+
+def diff(g, inputs, tolerance=1e-5):
+    ok, msg = Diff.check(oracle.Interp, H, g, inputs, tolerance=tolerance)
+    assert ok, msg
+
+
+@pytest.mark.parametrize("e", P.all_examples(), ids=lambda e: e.name)
+def test_s1_examples(device, e):
+    diff(e.graph(), e.inputs())
+    assert_policy(e.graph(), e.inputs())
+
+
+@pytest.mark.parametrize("n", [0, 1, 255, 256, 257, 1009, 300000])
+def test_s2_saxpy_sizes(device, n):
+    x = np.arange(n, dtype=np.float32)
+    y = (n - np.arange(n)).astype(np.float32)
+    diff(sx.program(n, 3.0), [("x", x), ("y", y)])
+
+
+def test_s3_sum_4m(device):
+    n = 1 << 22
+    x = (np.arange(n) % 7 - 3).astype(np.float32)
+    diff(P.sum_(n).graph(), [("x", x)], tolerance=1e-3)
+
+
+def test_s4_chain_one_kernel(device):
+    e = P.chain(4096)
+    c = H.compile(e.graph())
+    assert len(c.kernel_names()) == 1
+    c.release()
+    diff(e.graph(), e.inputs())
+
+
+def test_s6_i32_arithmetic(device):
+    x = D.param("x", I32, (9,))
+    r = D.map(lambda e: D.div(D.sub(e, D.const(I32, 4)), D.const(I32, 2)), x)
+    diff(Graph.create("i32", [("r", r)]), [("x", np.arange(9, dtype=np.int32))])
+
+
+def test_s8_u32_bit_exact(device):
+    g = Graph.create("u32", [("r", rng.u32(D.scalar("seed", I32), (1 << 20,)))])
+    diff(g, [("seed", np.array(12345, dtype=np.int32))], tolerance=0.0)
+
+
+def test_s9_normal_moments(device):
+    g = Graph.create("n", [("z", rng.normal(F32, D.scalar("seed", I32), (1 << 20,)))])
+    c = H.compile(g)
+    z = H.run(c, [("seed", np.array(99, dtype=np.int32))])[0][1].astype(np.float64)
+    c.release()
+    assert abs(z.mean()) < 0.01
+    assert abs(z.var() - 1.0) < 0.02
+
+
+def test_s10_rows(device):
+    dims = (1024, 4096)
+    x = (np.arange(dims[0] * dims[1]) % 11 - 5).astype(np.float32).reshape(dims)
+    xx = D.param("x", F32, dims)
+    z = D.const(F32, 0.0)
+    g = Graph.create("rows", [("r", D.reduce_rows(D.add, z, xx)), ("p", D.scan_rows(D.add, z, xx))])
+    diff(g, [("x", x)], tolerance=1e-3)
+
+
+@pytest.mark.parametrize("dtype,tol", [(F32, 1e-4), (F64, 1e-9)])
+def test_s11_matmul(device, dtype, tol):
+    a = D.param("a", dtype, (256, 192))
+    b = D.param("b", dtype, (192, 128))
+    g = Graph.create("mm", [("c", D.matmul(a, b))])
+    fa = (np.arange(256 * 192) % 13 / 7.0 - 0.9).astype(dtype.np).reshape(256, 192)
+    fb = (np.arange(192 * 128) % 17 / 5.0 - 1.6).astype(dtype.np).reshape(192, 128)
+    diff(g, [("a", fa), ("b", fb)], tolerance=tol)
+
+
+def test_s12_scatter_histogram(device):
+    n = 100000
+    idx = D.param("idx", I32, (n,))
+    gi = Graph.create("hi", [("h", D.scatter_add(idx, D.param("s", I32, (n,)), (7,)))])
+    iv = (np.arange(n) % 7).astype(np.int32)
+    diff(gi, [("idx", iv), ("s", np.ones(n, dtype=np.int32))])
+    idx = D.param("idx", I32, (n,))
+    gf = Graph.create("hf", [("h", D.scatter_add(idx, D.param("s", F32, (n,)), (7,)))])
+    diff(gf, [("idx", iv), ("s", (np.arange(n) % 13 / 4.0).astype(np.float32))], tolerance=1e-4)
+
+
+def test_s13_bs_greeks_f64(device):
+    g = bs.call_greeks(65536, F64)
+    diff(g, bs.inputs(F64, seed=7), tolerance=1e-6)
+
+
+def test_config_rows_small(device):
+    g = C.rows(256, 8192)
+    x = C.uniform_pm1(3, (256, 8192))
+    assert_policy(g, [("x", x)])
+
+
+def test_config_global_scan_bit_exact(device):
+    n = 1 << 22
+    g = C.global_scan(n)
+    v = C.small_ints(4, (n,))
+    exp, got = both(g, [("v", v)])
+    np.testing.assert_array_equal(exp[0][1], got[0][1])
+
+
+def test_config_scatter_gather(device):
+    n, bins = 1 << 20, 1 << 14
+    g = C.scatter_gather(n, bins)
+    inputs = [("idx", C.bin_indices(6, n, bits=14)), ("src", C.uniform_pm1(5, (n,)))]
+    assert_policy(g, inputs)
+
+
+def test_config_mc_paths_small(device):
+    g = C.mc_paths(4096, 64, F32)
+    assert_policy(g, bs.inputs(F32, seed=7))
