@@ -1,0 +1,295 @@
+"""Benchmark of the Backend_hip hot path on one MI355X.
+
+``python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME]``
+
+The default workload is the configuration BASELINE.json's metric is quoted
+on, config 2 (row ops): reduce_rows(add), reduce_rows(max) and
+scan_rows(add) over an f32 [8192; 8192] matrix, plus an inclusive scan of
+an i32 vector of 2^28 elements. One step is one run of both compiled
+programs over inputs already resident in HBM (run_resident_into, outputs
+preallocated, no host traffic). ``value`` is algorithmic bytes per second
+over the K timed steps (each materialised input read once, each output
+written once, per kernel of the plan). Other configs (``--config saxpy``,
+``chain``, ``scatter``, ``gather``, ``matmul``, ``matmul64``, ``matmul_grad``,
+``mc``, ``mc64``) print their own line in the same format.
+
+The JSON line also carries ``roofline`` for the dominant kernel (its
+algorithmic bytes or flops per launch over its mean launch time, timed with
+HIP events on the executor's stream inside the timed region) and
+``cpu_baseline``: the CPU oracle (a C restatement of the reference
+interpreter, single-threaded) timed on a bounded sample of the same
+workload on this host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+FP32_MFMA_TFLOPS = 157.3
+FP64_MFMA_TFLOPS = 78.6
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def plan_bytes(H, graph, kernel_filter=None):
+    """Algorithmic bytes of every kernel of the plan: each distinct buffer
+    argument counted once, scratch excluded."""
+    text = H.plan(graph)
+    bufs = {}
+    kernels = []
+    for line in text.splitlines():
+        f = line.split()
+        if f[0] == "buffer":
+            size = {"f32": 4, "f64": 8, "i32": 4, "i64": 8}[f[3]] * int(f[4])
+            bufs[int(f[1])] = (f[2], size, f[5])
+        elif f[0] == "kernel":
+            args = [int(x) for x in f[f.index("args") + 1:]]
+            kernels.append((f[1], f[2], args))
+    out = {}
+    for name, role, args in kernels:
+        if role in ("scan_init",):
+            continue
+        b = sum(bufs[a][1] for a in set(args) if bufs[a][2] in ("param", "computed"))
+        out[name] = (role, b)
+    return out
+
+
+class Workload:
+    def __init__(self, name, programs, unit, dtype, describe):
+        self.name = name
+        self.programs = programs  # list of (graph, compiled, inputs residents, output residents)
+        self.unit = unit
+        self.dtype = dtype
+        self.describe = describe
+
+
+def device_inputs(H, gen_graph, seed):
+    import numpy as np
+
+    c = H.compile(gen_graph)
+    seed_r = H.upload(np.array(seed, dtype=np.int32))
+    out = H.run_resident(c, [("seed", seed_r)])
+    H.free_resident(seed_r)
+    c.release()
+    return out[0][1]
+
+
+def alloc_outputs(H, c):
+    from cudacaml_amd.runtime import Buffer
+
+    return [(o.name, H.Resident(Buffer.alloc(o.nbytes), o.dtype, o.shape)) for o in c.outputs]
+
+
+def build_workload(name, H, C):
+    """Compile the programs of one config and put its inputs in HBM."""
+    from cudacaml_amd.examples import black_scholes as bs
+    from cudacaml_amd.ir import F32, F64
+
+    progs = []
+
+    def add(g, inputs):
+        c = H.compile(g)
+        progs.append((g, c, inputs, alloc_outputs(H, c)))
+
+    if name == "rows":
+        x = device_inputs(H, C.gen_uniform_pm1((C.ROWS2, C.ROWS2)), 3)
+        v = device_inputs(H, C.gen_small_ints((C.SCAN2,)), 4)
+        add(C.rows(), [("x", x)])
+        add(C.global_scan(), [("v", v)])
+        return Workload(name, progs, "GB/s", "f32/i32",
+                        "config2: reduce_rows add+max and scan_rows add over f32[8192,8192]; "
+                        "inclusive scan over i32[2^28]")
+    if name in ("saxpy", "chain"):
+        x = device_inputs(H, C.gen_uniform_pm1((C.N1,)), 1)
+        if name == "saxpy":
+            y = device_inputs(H, C.gen_uniform_pm1((C.N1,)), 2)
+            add(C.saxpy(), [("x", x), ("y", y)])
+            desc = "config1: saxpy r=2x+y, s=sum r over f32[2^24]"
+        else:
+            add(C.chain(), [("x", x)])
+            desc = "config1b: 5-map chain over f32[2^24], one fused kernel"
+        return Workload(name, progs, "GB/s", "f32", desc)
+    if name in ("scatter", "scatter_perm"):
+        src = device_inputs(H, C.gen_uniform_pm1((C.N3,)), 5)
+        if name == "scatter":
+            idx = device_inputs(H, C.gen_bin_indices(C.N3, 20), 6)
+            add(C.scatter_gather(), [("idx", idx), ("src", src)])
+            desc = "config3: scatter_add of f32[2^26] into 2^20 bins (uniform idx) + gather back"
+        else:
+            import numpy as np
+
+            perm = H.upload(C.permutation(7, C.N3))
+            add(C.scatter_gather(C.N3, C.N3), [("idx", perm), ("src", src)])
+            desc = "config3b: scatter_add of f32[2^26] through a permutation into 2^26 bins + gather back"
+            del np
+        return Workload(name, progs, "GB/s", "f32", desc)
+    if name in ("matmul", "matmul64", "matmul_grad"):
+        dt = F64 if name == "matmul64" else F32
+        n = C.MM_F64 if name == "matmul64" else C.MM_F32
+        a = device_inputs(H, C.gen_normals((n, n), dt), 8)
+        b = device_inputs(H, C.gen_normals((n, n), dt), 9)
+        g = C.matmul_grad(n, dt) if name == "matmul_grad" else C.matmul(n, dt)
+        add(g, [("a", a), ("b", b)])
+        return Workload(name, progs, "TFLOP/s", dt.name, "config4: %s %s %dx%d" % (name, dt.name, n, n))
+    if name in ("mc", "mc64", "mc_greeks"):
+        dt = F64 if name == "mc64" else F32
+        g = C.mc_greeks() if name == "mc_greeks" else C.mc_paths(C.PATHS5, C.STEPS5, dt)
+        ins = [(k, H.upload(v)) for k, v in bs.inputs(dt, seed=7)]
+        add(g, ins)
+        return Workload(name, progs, "paths/s", dt.name,
+                        "config5: BS MC %s 2^22 paths x 64 steps %s" % ("greeks" if name == "mc_greeks" else "price",
+                                                                        dt.name))
+    raise SystemExit("unknown config %s" % name)
+
+
+def step(H, w, sync=False):
+    for g, c, ins, outs in w.programs:
+        H.run_resident_into(c, ins, outs, sync=sync)
+
+
+def cpu_baseline(name, C, H=None):
+    """The oracle on a bounded sample of the workload; returns (value, unit,
+    sample description, seconds). The sample's inputs are the leading part
+    of the benchmark's own inputs (same generator, same seeds), drawn on the
+    device when one is given."""
+    import oracle
+
+    if name == "rows":
+        r = 4096
+        n = 1 << 27
+        if H is not None:
+            x = H.download(device_inputs(H, C.gen_uniform_pm1((r, C.ROWS2)), 3))
+            v = H.download(device_inputs(H, C.gen_small_ints((n,)), 4))
+        else:
+            x = C.uniform_pm1(3, (r, C.ROWS2))
+            v = C.small_ints(4, (n,))
+        g1, g2 = C.rows(r, C.ROWS2), C.global_scan(n)
+        c1, c2 = oracle.Interp.compile(g1), oracle.Interp.compile(g2)
+        t0 = time.perf_counter()
+        oracle.Interp.run(c1, [("x", x)])
+        oracle.Interp.run(c2, [("v", v)])
+        dt = time.perf_counter() - t0
+        nbytes = 3 * x.nbytes + 2 * r * 4 + x.nbytes + 2 * v.nbytes
+        return nbytes / dt / 1e9, "GB/s", "rows graph on f32[4096,8192] + global scan on i32[2^27]", dt
+    raise SystemExit("no CPU baseline for %s" % name)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="rows")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this backend runs on one GPU; multi-GPU runs (Multi) are out of scope. Use --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    from cudacaml_amd import backend_hip as H
+    from cudacaml_amd.examples import configs as C
+    from cudacaml_amd.runtime import Device
+
+    if not Device.available():
+        raise SystemExit("bench.py: no HIP device")
+    info = Device.info()
+    log("device: %s %s, %d CUs" % (info.name, info.arch, info.multiprocessors))
+    t0 = time.perf_counter()
+    w = build_workload(args.config, H, C)
+    log("compiled and generated inputs in %.1fs" % (time.perf_counter() - t0))
+
+    # Per-kernel algorithmic bytes; the dominant kernel is the one with the
+    # most bytes (or the matmul, for flops).
+    kinfo = {}
+    for g, c, _, _ in w.programs:
+        for k, (role, b) in plan_bytes(H, g).items():
+            kinfo[k] = (role, b, c)
+    dom = max(kinfo.items(), key=lambda kv: kv[1][1])[0]
+    if args.config.startswith("matmul"):
+        dom = [k for k, v in kinfo.items() if v[0].startswith("matmul")][0]
+    dom_role, dom_bytes, dom_c = kinfo[dom]
+
+    for _ in range(args.warmup):
+        step(H, w)
+    Device.synchronize()
+    H.time_kernel(dom_c, dom)
+    Device.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(H, w)
+    Device.synchronize()
+    elapsed = time.perf_counter() - t0
+    launches, dom_ms = H.timing(dom_c)
+    H.time_kernel(dom_c, None)
+    step(H, w, sync=True)  # surfaces any device-side error of the timed runs
+
+    ms_per_step = elapsed * 1e3 / args.steps
+    total_bytes = sum(b for _, (_, b, _) in kinfo.items())
+    if w.unit == "GB/s":
+        value = total_bytes * args.steps / elapsed / 1e9
+    elif w.unit == "TFLOP/s":
+        flops = 0
+        for g, c, _, _ in w.programs:
+            for t in g.order:
+                if t.kind == "matmul":
+                    flops += 2 * t.shape[0] * t.shape[1] * t.a.shape[1]
+        value = flops * args.steps / elapsed / 1e12
+    else:
+        value = C.PATHS5 * args.steps / elapsed
+    dom_avg_ms = dom_ms / max(1, launches)
+    if w.unit == "TFLOP/s":
+        g = w.programs[0][0]
+        mm = [t for t in g.order if t.kind == "matmul"][0]
+        fl = 2 * mm.shape[0] * mm.shape[1] * mm.a.shape[1]
+        peak = FP64_MFMA_TFLOPS if w.dtype == "f64" else FP32_MFMA_TFLOPS
+        achieved = fl / (dom_avg_ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
+                "frac": round(achieved / peak, 4), "traffic": None}
+    else:
+        achieved = dom_bytes / (dom_avg_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None}
+    roof["kernel"] = dom
+    roof["template"] = dom_role
+    roof["launch_ms"] = round(dom_avg_ms, 4)
+    roof["algorithmic_bytes"] = dom_bytes
+
+    cpu = None
+    if not args.no_cpu and args.config == "rows":
+        v, unit, sample, secs = cpu_baseline(args.config, C, H)
+        cpu = {"value": round(v, 3), "unit": unit, "cores": 1, "kind": "port",
+               "sample": sample + " (%.1fs, C restatement of the OCaml interpreter)" % secs}
+
+    line = {
+        "metric": "HBM GB/s & % peak (fused map/reduce/scan); matmul TFLOP/s; MC paths/s",
+        "value": round(value, 2),
+        "unit": w.unit,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": w.dtype,
+        "data": "synthetic (Philox-4x32-10 inputs generated on the device)",
+        "config": {"workload": w.describe, "parallelism": "single GPU", "algorithmic_bytes_per_step": total_bytes},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -264,6 +264,7 @@ class Gen {
         // kernel raises a flag the host turns into the same error.
         Val j = elem(n.a, idx);
         const TNode &src = g_.ts[n.b];
+        if (transpose_source(g_, t) >= 0 && !p_.materialized[n.a]) return elem(n.b, j);
         uses_err_ = true;
         if (src.numel == 0) {
           body_ << "  cc_flag(err, 1);\n";
@@ -459,31 +460,13 @@ typedef unsigned int cc_u32;
 typedef unsigned long long cc_u64;
 template <typename T> struct __attribute__((aligned(4 * sizeof(T)))) cc_v4 { T x, y, z, w; };
 
-// Float.min / Float.max of OCaml: NaN if either operand is NaN, -0 below +0.
-__device__ __forceinline__ float cc_minf(float x, float y) {
-  if (x != x || y != y) return __builtin_nanf("");
-  if (x < y) return x;
-  if (y < x) return y;
-  return __builtin_signbit(x) ? x : y;
-}
-__device__ __forceinline__ float cc_maxf(float x, float y) {
-  if (x != x || y != y) return __builtin_nanf("");
-  if (x > y) return x;
-  if (y > x) return y;
-  return __builtin_signbit(x) ? y : x;
-}
-__device__ __forceinline__ double cc_mind(double x, double y) {
-  if (x != x || y != y) return __builtin_nan("");
-  if (x < y) return x;
-  if (y < x) return y;
-  return __builtin_signbit(x) ? x : y;
-}
-__device__ __forceinline__ double cc_maxd(double x, double y) {
-  if (x != x || y != y) return __builtin_nan("");
-  if (x > y) return x;
-  if (y > x) return y;
-  return __builtin_signbit(x) ? y : x;
-}
+// Float.min / Float.max of OCaml: NaN if either operand is NaN, -0 below
+// +0. These are IEEE 754-2019 minimum/maximum, which gfx950 executes as
+// one v_minimum3_f32 / v_maximum3_f32.
+__device__ __forceinline__ float cc_minf(float x, float y) { return __builtin_elementwise_minimum(x, y); }
+__device__ __forceinline__ float cc_maxf(float x, float y) { return __builtin_elementwise_maximum(x, y); }
+__device__ __forceinline__ double cc_mind(double x, double y) { return __builtin_elementwise_minimum(x, y); }
+__device__ __forceinline__ double cc_maxd(double x, double y) { return __builtin_elementwise_maximum(x, y); }
 // Int32.div / Int64.div: truncation, min_int / -1 wraps. Division by zero
 // raises in the interpreter; on the device it yields 0.
 __device__ __forceinline__ int cc_divi(int a, int b) {
@@ -535,6 +518,24 @@ int64_t pow2ceil(int64_t n) {
 }
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Launch-shape knobs for sweeps: CCHIP_TUNE="key=value,key=value". Every
+// key has a default that is the shipped configuration; a knob only changes
+// tile sizes and grid shapes, never what is computed.
+int64_t tune(const char *key, int64_t dflt) {
+  const char *env = getenv("CCHIP_TUNE");
+  if (!env) return dflt;
+  std::string s = env, k = std::string(key) + "=";
+  size_t p = 0;
+  while (p < s.size()) {
+    size_t e = s.find(',', p);
+    if (e == std::string::npos) e = s.size();
+    std::string item = s.substr(p, e - p);
+    if (item.compare(0, k.size(), k) == 0) return strtoll(item.c_str() + k.size(), nullptr, 10);
+    p = e + 1;
+  }
+  return dflt;
+}
 
 // ---------------------------------------------------------------------------
 // The lowering proper
@@ -678,8 +679,155 @@ struct Lowering {
       << "}\n";
     src << k.str();
     int64_t nvec = std::max<int64_t>(1, N / 4);
-    int grid = (int)std::min<int64_t>(cdiv(nvec, 256), 65536);
+    int grid = (int)std::min<int64_t>(cdiv(nvec, 256), tune("map_blocks", 65536));
     return {add_kernel(kname, args, grid, 256, "map")};
+  }
+
+  // ---- Row-sequential reduce/scan ----------------------------------------
+  // With enough rows, one lane owns one row and folds it strictly left to
+  // right from init, in exactly the interpreter's order (R2), so f32 sums
+  // and prefix sums are bit-identical to it. Workgroups stage R rows x W
+  // columns through LDS with coalesced (4-wide) global accesses; the next
+  // tile's loads are in flight in registers while the lanes fold the
+  // current one. Used when rows >= 1024, where there are enough lanes to
+  // keep HBM busy.
+  std::vector<int> lower_rows_seq(int t, bool scan, const ElemFn &f, const std::string &cmb, const std::string &ini,
+                                  int64_t rows, int64_t len) {
+    const TNode &n = g.ts[t];
+    std::string kname = "k_" + std::to_string(n.id);
+    std::string T = dt_ctype(n.dt);
+    int out = buf_of[t];
+    int64_t elems = tune("rs_bytes", 32768) / dt_size(n.dt);  // LDS bytes per tile
+    int64_t min_groups = tune("rs_groups", 512);
+    int64_t R = 1;
+    while (R < 64 && rows / (R * 2) >= min_groups) R *= 2;
+    int64_t W = std::min<int64_t>(elems / R, std::max<int64_t>(4, pow2ceil(len)));
+    elems = R * W;
+    int64_t E = cdiv(elems, 1024);  // 4-element groups per thread
+    int64_t NT = cdiv(len, W);
+    int64_t REM = len - (NT - 1) * W;
+    int64_t S = W + 4;               // row stride keeps 4-element groups 16-byte aligned
+    int64_t CH = std::min<int64_t>(16, W);
+    bool vec = len % 4 == 0;
+    Params p;
+    add_in(p, f);
+    p.out.push_back(out);
+    std::vector<int> args;
+    std::string params = param_list(p, args);
+    static const char *comp[] = {"x", "y", "z", "w"};
+    std::string V4 = "cc_v4<" + T + ">";
+    std::ostringstream k;
+    k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
+      << "  __shared__ " << V4 << " sm4[" << R * S / 4 << "];\n"
+      << "  " << T << "* const sm = (" << T << "*)sm4;\n"
+      << "  " << T << " rg[" << E * 4 << "];\n"
+      << "  for (int g0 = blockIdx.x * " << R << "; g0 < " << rows << "; g0 += gridDim.x * " << R << ") {\n";
+    // Tile c0 into registers: group u of thread t covers flat tile elements
+    // q..q+3 with q = 4 (t + 256 u), at row q / W, column q % W.
+    auto load = [&](const std::string &c0) {
+      std::ostringstream l;
+      l << "    {\n"
+        << "      const int c0 = " << c0 << ";\n"
+        << "#pragma unroll\n"
+        << "      for (int u = 0; u < " << E << "; u++) {\n"
+        << "        const int q = 4 * (threadIdx.x + 256 * u);\n"
+        << "        const int rr = q / " << W << ", j = q - rr * " << W << ";\n"
+        << "        const int row = min(g0 + rr, " << rows - 1 << ");\n"
+        << "        if (q < " << elems << ") {\n";
+      // Groups past the last row or column read a valid element instead
+      // (row clamped, column 0) and are never consumed: no load sits
+      // behind a branch, so a thread's loads are all in flight together.
+      if (vec) {
+        l << "          const int i = row * " << len << " + (c0 + j < " << len << " ? c0 + j : 0);\n"
+          << vec_loads(f, "i", "          ", tyof());
+        for (int c = 0; c < 4; c++) l << "          rg[4 * u + " << c << "] = " << lane_call(f, "i", c) << ";\n";
+      } else {
+        for (int c = 0; c < 4; c++)
+          l << "          { const int i = row * " << len << " + (c0 + j + " << c << " < " << len << " ? c0 + j + " << c
+            << " : 0); rg[4 * u + " << c << "] = " << f.call_scalar("i") << "; }\n";
+      }
+      l << "        }\n"
+        << "      }\n"
+        << "    }\n";
+      return l.str();
+    };
+    auto to_lds = [&]() {
+      std::ostringstream l;
+      l << "#pragma unroll\n"
+        << "    for (int u = 0; u < " << E << "; u++) {\n"
+        << "      const int q = 4 * (threadIdx.x + 256 * u);\n"
+        << "      const int rr = q / " << W << ", j = q - rr * " << W << ";\n"
+        << "      if (q < " << elems << ") {\n"
+        << "        " << V4 << " w;\n";
+      for (int c = 0; c < 4; c++) l << "        w." << comp[c] << " = rg[4 * u + " << c << "];\n";
+      l << "        sm4[(rr * " << S << " + j) / 4] = w;\n"
+        << "      }\n"
+        << "    }\n";
+      return l.str();
+    };
+    k << load("0") << to_lds();
+    k << "    if (" << NT << " > 1) {\n" << load(std::to_string(W)) << "    }\n"
+      << "    __syncthreads();\n"
+      << "    " << T << " acc = " << ini << "();\n"
+      << "    for (int kt = 0; kt < " << NT << "; kt++) {\n"
+      << "      const int c0 = kt * " << W << ";\n"
+      << "      if (threadIdx.x < " << R << " && g0 + threadIdx.x < " << rows << ") {\n"
+      << "        " << T << "* const s = sm + threadIdx.x * " << S << ";\n"
+      << "        if (kt + 1 < " << NT << " || " << REM << " == " << W << ") {\n"
+      << "          for (int j0 = 0; j0 < " << W << "; j0 += " << CH << ") {\n"
+      << "            " << T << " tv[" << CH << "];\n"
+      << "#pragma unroll\n"
+      << "            for (int u = 0; u < " << CH / 4 << "; u++) {\n"
+      << "              const " << V4 << " w = ((const " << V4 << "*)(s + j0))[u];\n"
+      << "              tv[4 * u] = w.x; tv[4 * u + 1] = w.y; tv[4 * u + 2] = w.z; tv[4 * u + 3] = w.w;\n"
+      << "            }\n"
+      << "#pragma unroll\n"
+      << "            for (int u = 0; u < " << CH << "; u++) { acc = " << cmb << "(acc, tv[u]);"
+      << (scan ? " tv[u] = acc;" : "") << " }\n";
+    if (scan)
+      k << "#pragma unroll\n"
+        << "            for (int u = 0; u < " << CH / 4 << "; u++) {\n"
+        << "              " << V4 << " w; w.x = tv[4 * u]; w.y = tv[4 * u + 1]; w.z = tv[4 * u + 2]; w.w = tv[4 * u + 3];\n"
+        << "              ((" << V4 << "*)(s + j0))[u] = w;\n"
+        << "            }\n";
+    k << "          }\n"
+      << "        } else {\n"
+      << "          for (int j = 0; j < " << REM << "; j++) { acc = " << cmb << "(acc, s[j]);"
+      << (scan ? " s[j] = acc;" : "") << " }\n"
+      << "        }\n"
+      << "      }\n"
+      << "      __syncthreads();\n";
+    if (scan) {
+      k << "#pragma unroll\n"
+        << "      for (int u = 0; u < " << E << "; u++) {\n"
+        << "        const int q = 4 * (threadIdx.x + 256 * u);\n"
+        << "        const int rr = q / " << W << ", j = q - rr * " << W << ";\n"
+        << "        const int row = g0 + rr;\n"
+        << "        if (q < " << elems << " && row < " << rows << ") {\n"
+        << "          const int i = row * " << len << " + c0 + j;\n"
+        << "          const " << V4 << " o = sm4[(rr * " << S << " + j) / 4];\n";
+      if (vec) {
+        k << "          if (c0 + j < " << len << ") *(" << V4 << "*)(b" << out << " + i) = o;\n";
+      } else {
+        for (int c = 0; c < 4; c++)
+          k << "          if (c0 + j + " << c << " < " << len << ") b" << out << "[i + " << c << "] = o." << comp[c]
+            << ";\n";
+      }
+      k << "        }\n"
+        << "      }\n"
+        << "      __syncthreads();\n";
+    }
+    k << "      if (kt + 1 < " << NT << ") {\n" << to_lds() << "      }\n"
+      << "      if (kt + 2 < " << NT << ") {\n" << load("(kt + 2) * " + std::to_string(W)) << "      }\n"
+      << "      __syncthreads();\n"
+      << "    }\n";
+    if (!scan)
+      k << "    if (threadIdx.x < " << R << " && g0 + threadIdx.x < " << rows << ") b" << out
+        << "[g0 + threadIdx.x] = acc;\n";
+    k << "  }\n}\n";
+    src << k.str();
+    int grid = (int)std::min<int64_t>(cdiv(rows, R), 1 << 20);
+    return {add_kernel(kname, args, grid, 256, scan ? "scan_rowseq" : "reduce_rowseq")};
   }
 
   // ---- Reduce root (K2-K4 -> wave / block / split-row reductions) --------
@@ -708,6 +856,7 @@ struct Lowering {
     }
     ElemFn f = gen.element_fn("f_" + id, n.a, false, true);
     src << f.code;
+    if (rows >= 1024) return lower_rows_seq(t, false, f, cmb, ini, rows, len);
     bool vec = len % 4 == 0;
     if (len <= 2048) {
       // One wave (or a power-of-two segment of one) per row.
@@ -862,6 +1011,7 @@ struct Lowering {
     if (rows == 0) return {};
     ElemFn f = gen.element_fn("f_" + id, n.a, false, true);
     src << f.code;
+    if (rows >= 1024) return lower_rows_seq(t, true, f, cmb, ini, rows, len);
     bool wide = dt_size(n.dt) == 8;
     if (len <= 64) {
       int64_t S = pow2ceil(len);
@@ -895,110 +1045,34 @@ struct Lowering {
       int grid = (int)std::min<int64_t>(cdiv(waves, 4), 65536);
       return {add_kernel(kname, args, grid, 256, "scan_wave")};
     }
-    // Shared pieces of the block-level scan: striped load into LDS, each
-    // thread scans ITEMS consecutive elements, the block scans the thread
-    // totals, and the prefix is folded back in. LDS is padded one slot per
-    // 32 so the blocked reads are conflict-free.
-    auto block_scan = [&](int64_t items, const std::string &rowlen, const std::string &first_cond) {
-      std::ostringstream b;
-      b << "    " << T << " v[" << items << "];\n"
-        << "#pragma unroll\n"
-        << "    for (int q = 0; q < " << items << "; q++) { const int e = threadIdx.x * " << items
-        << " + q; v[q] = sm[e + (e >> 5)]; }\n"
-        << "    if (" << first_cond << ") v[0] = " << cmb << "(" << ini << "(), v[0]);\n"
-        << "#pragma unroll\n"
-        << "    for (int q = 1; q < " << items << "; q++) v[q] = " << cmb << "(v[q - 1], v[q]);\n"
-        << "    " << T << " incl = v[" << items - 1 << "];\n";
-      for (int off = 1; off < 64; off *= 2)
-        b << "    { const " << T << " u = __shfl_up(incl, " << off << "); if (lane >= " << off << ") incl = " << cmb
-          << "(u, incl); }\n";
-      b << "    const " << T << " excl = __shfl_up(incl, 1);\n"
-        << "    if (lane == 63) wsum[wid] = incl;\n"
-        << "    __syncthreads();\n"
-        << "    bool has = false;\n"
-        << "    " << T << " pre = " << ini << "();\n"
-        << "    for (int w = 0; w < wid; w++) { pre = has ? " << cmb << "(pre, wsum[w]) : wsum[w]; has = true; }\n"
-        << "    if (lane > 0) { pre = has ? " << cmb << "(pre, excl) : excl; has = true; }\n"
-        << "    if (has) {\n"
-        << "#pragma unroll\n"
-        << "      for (int q = 0; q < " << items << "; q++) v[q] = " << cmb << "(pre, v[q]);\n"
-        << "    }\n";
-      (void)rowlen;
-      return b.str();
-    };
-    auto striped_load = [&](int64_t padded, const std::string &base, const std::string &valid_len, bool vec) {
-      std::ostringstream b;
-      if (vec) {
-        b << "    for (int e = threadIdx.x * 4; e < " << padded << "; e += 1024) {\n"
-          << "      if (e < " << valid_len << ") {\n"
-          << "        const int i = " << base << " + e;\n"
-          << vec_loads(f, "i", "        ", tyof());
-        static const char *comp[] = {"x", "y", "z", "w"};
-        for (int u = 0; u < 4; u++)
-          b << "        { const int ee = e + " << u << "; sm[ee + (ee >> 5)] = " << lane_call(f, "i", u) << "; }\n";
-        (void)comp;
-        b << "      } else {\n"
-          << "        for (int u = 0; u < 4; u++) { const int ee = e + u; sm[ee + (ee >> 5)] = " << ini << "(); }\n"
-          << "      }\n"
-          << "    }\n";
-      } else {
-        b << "    for (int e = threadIdx.x; e < " << padded << "; e += 256) {\n"
-          << "      " << T << " x = " << ini << "();\n"
-          << "      if (e < " << valid_len << ") x = " << f.call_scalar(base + " + e") << ";\n"
-          << "      sm[e + (e >> 5)] = x;\n"
-          << "    }\n";
-      }
-      b << "    __syncthreads();\n";
-      return b.str();
-    };
-    int64_t block_max = wide ? 8192 : 16384;
-    if (len <= block_max && rows >= 128) {
-      int64_t items = cdiv(len, 256);
-      int64_t padded = items * 256;
-      // Vector loads need every row start and the padded tail to stay in
-      // 4-element groups.
-      bool vec = len % 4 == 0;
-      Params p;
-      add_in(p, f);
-      p.out.push_back(out);
-      std::vector<int> args;
-      std::string params = param_list(p, args);
-      std::ostringstream k;
-      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
-        << "  __shared__ " << T << " sm[" << padded + padded / 32 << "];\n"
-        << "  __shared__ " << T << " wsum[4];\n"
-        << "  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;\n"
-        << "  for (int r = blockIdx.x; r < " << rows << "; r += gridDim.x) {\n"
-        << "    const int base = r * " << len << ";\n"
-        << striped_load(padded, "base", std::to_string(len), vec) << block_scan(items, "", "threadIdx.x == 0")
-        << "#pragma unroll\n"
-        << "    for (int q = 0; q < " << items << "; q++) { const int e = threadIdx.x * " << items
-        << " + q; sm[e + (e >> 5)] = v[q]; }\n"
-        << "    __syncthreads();\n"
-        << "    for (int e = threadIdx.x; e < " << len << "; e += 256) b" << out << "[base + e] = sm[e + (e >> 5)];\n"
-        << "    __syncthreads();\n"
-        << "  }\n}\n";
-      src << k.str();
-      int grid = (int)std::min<int64_t>(rows, 1 << 20);
-      return {add_kernel(kname, args, grid, 256, "scan_block")};
-    }
-    // Long rows: single-pass scan with decoupled look-back. Tiles are handed
-    // out in launch order by an atomic counter, so a tile only ever waits on
-    // tiles whose workgroups are already running. Status words carry the
-    // flag (1 = aggregate, 2 = inclusive prefix) in the high half and the
-    // value bits in the low half; 8-byte values use two words, each tagged.
-    int64_t items = wide ? 8 : 16;
-    int64_t tile = 256 * items;
+    // Rows longer than 64 with few rows: a register-resident tile scan.
+    // A tile is U slices of 1024 elements; thread t holds the 4 contiguous
+    // elements 4t..4t+3 of every slice (one 16-byte load each, all in
+    // flight together). The scan runs in that layout: a 4-element scan per
+    // thread, a wave scan of thread totals per slice, one barrier to share
+    // the 4 wave totals of every slice, and the slice prefixes are folded
+    // in with earlier elements always on the left. When a row spans
+    // several tiles they are chained by a single-pass decoupled look-back:
+    // tiles are handed out in launch order by an atomic counter, so a tile
+    // only waits on tiles whose workgroups are already running; status
+    // words carry the flag (1 aggregate, 2 inclusive prefix) in the high
+    // half and the value bits in the low half (8-byte values use two
+    // words, each tagged).
+    int64_t Umax = tune(wide ? "lb_slices8" : "lb_slices4", wide ? 8 : 16);
+    if (Umax < 1) throw InvalidArgument("CCHIP_TUNE: look-back slices must be >= 1");
+    int64_t U = std::min<int64_t>(Umax, std::max<int64_t>(1, cdiv(len, 1024)));
+    int64_t tile = 1024 * U;
     int64_t tpr = cdiv(len, tile);
     int64_t tiles = rows * tpr;
+    bool chained = tpr > 1;
+    bool vec = len % 4 == 0;
     int words = wide ? 2 : 1;
-    int status = add_buf("t" + id + "_status", DT::I64, tiles * words, BufRole::Scratch);
-    int ctr = add_buf("t" + id + "_tiles", DT::I32, 2, BufRole::Scratch);
-    need_err = true;
-    int e = err_buf();
-    // init kernel: zero the status words and the tile counter.
-    std::string iname = kname + "_init";
-    {
+    int status = -1, ctr = -1, kinit = -1;
+    if (chained) {
+      status = add_buf("t" + id + "_status", DT::I64, tiles * words, BufRole::Scratch);
+      ctr = add_buf("t" + id + "_tiles", DT::I32, 2, BufRole::Scratch);
+      need_err = true;
+      std::string iname = kname + "_init";
       std::ostringstream k;
       k << "extern \"C\" __global__ __launch_bounds__(256) void " << iname << "(long long* __restrict__ b" << status
         << ", int* __restrict__ b" << ctr << ") {\n"
@@ -1008,18 +1082,20 @@ struct Lowering {
         << "  if (blockIdx.x == 0 && threadIdx.x < 2) b" << ctr << "[threadIdx.x] = 0;\n"
         << "}\n";
       src << k.str();
+      kinit =
+          add_kernel(iname, {status, ctr}, (int)std::min<int64_t>(cdiv(tiles * words, 256), 1024), 256, "scan_init");
     }
-    int kinit =
-        add_kernel(iname, {status, ctr}, (int)std::min<int64_t>(cdiv(tiles * words, 256), 1024), 256, "scan_init");
     Params p;
     add_in(p, f);
     p.out.push_back(out);
+    if (chained) p.err = true;
     std::vector<int> args;
     std::string params = param_list(p, args);
-    args.push_back(status);
-    args.push_back(ctr);
-    if (!p.err) args.push_back(e);
-    std::string pub, poll;
+    if (chained) {
+      args.push_back(status);
+      args.push_back(ctr);
+    }
+    std::string pub;
     if (!wide) {
       pub =
           "__hip_atomic_store(&st[TILE], ((cc_u64)(FLAG) << 32) | cc_bits(VAL), __ATOMIC_RELAXED, "
@@ -1033,104 +1109,163 @@ struct Lowering {
           "__HIP_MEMORY_SCOPE_AGENT); }";
     }
     auto publish = [&](const std::string &tl, const std::string &flag, const std::string &val) {
-      std::string s = pub;
+      std::string r = pub;
       auto rep = [&](const std::string &a, const std::string &b) {
         size_t q = 0;
-        while ((q = s.find(a, q)) != std::string::npos) {
-          s.replace(q, a.size(), b);
+        while ((q = r.find(a, q)) != std::string::npos) {
+          r.replace(q, a.size(), b);
           q += b.size();
         }
       };
       rep("TILE", tl);
       rep("FLAG", flag);
       rep("VAL", val);
-      return s;
+      return r;
     };
+    static const char *comp[] = {"x", "y", "z", "w"};
     std::ostringstream k;
-    k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params
-      << (params.empty() ? "" : ", ") << "cc_u64* __restrict__ st, int* __restrict__ ctr"
-      << (p.err ? "" : ", int* __restrict__ err") << ") {\n"
-      << "  __shared__ " << T << " sm[" << tile + tile / 32 << "];\n"
-      << "  __shared__ " << T << " wsum[4];\n"
-      << "  __shared__ " << T << " s_agg;\n"
+    k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params;
+    if (chained) k << ", cc_u64* __restrict__ st, int* __restrict__ ctr";
+    k << ") {\n"
+      << "  __shared__ " << T << " wsum[" << U << "][4];\n"
       << "  __shared__ " << T << " s_prefix;\n"
-      << "  __shared__ int s_tile;\n"
-      << "  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;\n"
-      << "  if (threadIdx.x == 0) s_tile = atomicAdd(ctr, 1);\n"
-      << "  __syncthreads();\n"
-      << "  const int tile = s_tile;\n"
-      << "  const int row = tile / " << tpr << ";\n"
+      << "  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;\n";
+    if (chained) {
+      k << "  __shared__ int s_tile;\n"
+        << "  if (threadIdx.x == 0) s_tile = atomicAdd(ctr, 1);\n"
+        << "  __syncthreads();\n"
+        << "  const int tile = s_tile;\n";
+    } else {
+      k << "  const int tile = blockIdx.x;\n";
+    }
+    k << "  const int row = tile / " << tpr << ";\n"
       << "  const int tin = tile - row * " << tpr << ";\n"
       << "  const int base = row * " << len << " + tin * " << tile << ";\n"
-      << "  const int len = min(" << tile << ", " << len << " - tin * " << tile << ");\n"
-      << "  {\n"
-      << striped_load(tile, "base", "len", len % 4 == 0 && tile % 4 == 0)
-      << block_scan(items, "", "tin == 0 && threadIdx.x == 0") << "    if (threadIdx.x == 255) {\n"
-      << "      s_agg = v[" << items - 1 << "];\n"
-      << "      " << publish("tile", "tin == 0 ? 2 : 1", "v[" + std::to_string(items - 1) + "]") << ";\n"
-      << "    }\n"
-      << "    __syncthreads();\n"
-      << "    if (tin > 0 && wid == 0) {\n"
-      << "      const int rowstart = row * " << tpr << ";\n"
-      << "      " << T << " acc = " << ini << "();\n"
-      << "      bool have = false;\n"
-      << "      int j = tile - 1;\n"
-      << "      unsigned spins = 0;\n"
-      << "      while (true) {\n"
-      << "        const int q = j - lane;\n"
-      << "        int flag = 2;\n"
-      << "        " << T << " val = " << ini << "();\n"
-      << "        if (q >= rowstart) {\n"
-      << "          while (true) {\n";
-    if (!wide) {
-      k << "            const cc_u64 w = __hip_atomic_load(&st[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
-        << "            flag = (int)(w >> 32);\n"
-        << "            if (flag != 0) { val = cc_from_bits<" << T << ">(w & 0xffffffffull); break; }\n";
+      << "  const int tl = min(" << tile << ", " << len << " - tin * " << tile << ");\n"
+      << "  " << T << " v[" << U << "][4];\n"
+      << "#pragma unroll\n"
+      << "  for (int u = 0; u < " << U << "; u++) {\n"
+      << "    const int e = threadIdx.x * 4 + 1024 * u;\n";
+    // Groups past the tile read the tile's first group (always valid) and
+    // take init: no load sits behind a branch.
+    if (vec) {
+      k << "    const bool ok = e < tl;\n"
+        << "    const int i = base + (ok ? e : 0);\n"
+        << vec_loads(f, "i", "    ", tyof());
+      for (int c = 0; c < 4; c++)
+        k << "    v[u][" << c << "] = ok ? " << lane_call(f, "i", c) << " : " << ini << "();\n";
     } else {
-      k << "            const cc_u64 w0 = __hip_atomic_load(&st[2 * q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
-        << "            const cc_u64 w1 = __hip_atomic_load(&st[2 * q + 1], __ATOMIC_RELAXED, "
-           "__HIP_MEMORY_SCOPE_AGENT);\n"
-        << "            flag = (int)(w0 >> 32);\n"
-        << "            if (flag != 0 && flag == (int)(w1 >> 32)) { val = cc_from_bits<" << T
-        << ">((w0 & 0xffffffffull) | (w1 << 32)); break; }\n";
+      for (int c = 0; c < 4; c++)
+        k << "    { const bool ok = e + " << c << " < tl; const int i = base + (ok ? e + " << c << " : 0); v[u][" << c
+          << "] = ok ? " << f.call_scalar("i") << " : " << ini << "(); }\n";
     }
-    k << "            if (++spins > (1u << 24)) { cc_flag(err, 4); flag = 2; break; }\n"
-      << "            __builtin_amdgcn_s_sleep(1);\n"
-      << "          }\n"
-      << "        }\n"
-      << "        const cc_u64 pm = __ballot(flag == 2);\n"
-      << "        const int L = pm ? (__ffsll((long long)pm) - 1) : 63;\n"
-      << "        " << T << " w = lane <= L ? val : " << ini << "();\n";
+    k << "  }\n"
+      << "  if (tin == 0 && threadIdx.x == 0) v[0][0] = " << cmb << "(" << ini << "(), v[0][0]);\n"
+      << "  " << T << " ex[" << U << "];\n"
+      << "#pragma unroll\n"
+      << "  for (int u = 0; u < " << U << "; u++) {\n"
+      << "    v[u][1] = " << cmb << "(v[u][0], v[u][1]);\n"
+      << "    v[u][2] = " << cmb << "(v[u][1], v[u][2]);\n"
+      << "    v[u][3] = " << cmb << "(v[u][2], v[u][3]);\n"
+      << "    " << T << " incl = v[u][3];\n";
     for (int off = 1; off < 64; off *= 2)
-      k << "        { const " << T << " o = __shfl_down(w, " << off << "); if ((lane & " << (2 * off - 1)
-        << ") == 0) w = " << cmb << "(o, w); }\n";
-    k << "        w = __shfl(w, 0);\n"
-      << "        acc = have ? " << cmb << "(w, acc) : w;\n"
-      << "        have = true;\n"
-      << "        if (pm) break;\n"
-      << "        j -= 64;\n"
-      << "      }\n"
-      << "      if (lane == 0) {\n"
-      << "        s_prefix = acc;\n"
-      << "        const " << T << " incl = " << cmb << "(acc, s_agg);\n"
-      << "        " << publish("tile", "2", "incl") << ";\n"
-      << "      }\n"
-      << "    }\n"
-      << "    __syncthreads();\n"
-      << "    if (tin > 0) {\n"
-      << "      const " << T << " pfx = s_prefix;\n"
+      k << "    { const " << T << " o = __shfl_up(incl, " << off << "); if (lane >= " << off << ") incl = " << cmb
+        << "(o, incl); }\n";
+    k << "    ex[u] = __shfl_up(incl, 1);\n"
+      << "    if (lane == 63) wsum[u][wid] = incl;\n"
+      << "  }\n"
+      << "  __syncthreads();\n"
+      << "  " << T << " run = " << ini << "();\n"
       << "#pragma unroll\n"
-      << "      for (int q = 0; q < " << items << "; q++) v[q] = " << cmb << "(pfx, v[q]);\n"
+      << "  for (int u = 0; u < " << U << "; u++) {\n"
+      << "    bool hp = u > 0;\n"
+      << "    " << T << " pf = run;\n"
+      << "    for (int w = 0; w < wid; w++) { pf = hp ? " << cmb << "(pf, wsum[u][w]) : wsum[u][w]; hp = true; }\n"
+      << "    if (lane > 0) { pf = hp ? " << cmb << "(pf, ex[u]) : ex[u]; hp = true; }\n"
+      << "    if (hp) {\n"
+      << "      v[u][0] = " << cmb << "(pf, v[u][0]); v[u][1] = " << cmb << "(pf, v[u][1]);\n"
+      << "      v[u][2] = " << cmb << "(pf, v[u][2]); v[u][3] = " << cmb << "(pf, v[u][3]);\n"
       << "    }\n"
-      << "#pragma unroll\n"
-      << "    for (int q = 0; q < " << items << "; q++) { const int e = threadIdx.x * " << items
-      << " + q; sm[e + (e >> 5)] = v[q]; }\n"
-      << "    __syncthreads();\n"
-      << "    for (int e = threadIdx.x; e < len; e += 256) b" << out << "[base + e] = sm[e + (e >> 5)];\n"
-      << "  }\n}\n";
+      << "    " << T << " su = " << cmb << "(" << cmb << "(" << cmb << "(wsum[u][0], wsum[u][1]), wsum[u][2]), wsum[u][3]);\n"
+      << "    run = u > 0 ? " << cmb << "(run, su) : su;\n"
+      << "  }\n";
+    if (chained) {
+      k << "  if (threadIdx.x == 0) " << publish("tile", "tin == 0 ? 2 : 1", "run") << ";\n"
+        << "  if (tin > 0) {\n"
+        << "    if (wid == 0) {\n"
+        << "      const int rowstart = row * " << tpr << ";\n"
+        << "      " << T << " acc = " << ini << "();\n"
+        << "      bool have = false;\n"
+        << "      int j = tile - 1;\n"
+        << "      unsigned spins = 0;\n"
+        << "      while (true) {\n"
+        << "        const int q = j - lane;\n"
+        << "        int flag = 2;\n"
+        << "        " << T << " val = " << ini << "();\n"
+        << "        if (q >= rowstart) {\n"
+        << "          while (true) {\n";
+      if (!wide) {
+        k << "            const cc_u64 w = __hip_atomic_load(&st[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
+          << "            flag = (int)(w >> 32);\n"
+          << "            if (flag != 0) { val = cc_from_bits<" << T << ">(w & 0xffffffffull); break; }\n";
+      } else {
+        k << "            const cc_u64 w0 = __hip_atomic_load(&st[2 * q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
+          << "            const cc_u64 w1 = __hip_atomic_load(&st[2 * q + 1], __ATOMIC_RELAXED, "
+             "__HIP_MEMORY_SCOPE_AGENT);\n"
+          << "            flag = (int)(w0 >> 32);\n"
+          << "            if (flag != 0 && flag == (int)(w1 >> 32)) { val = cc_from_bits<" << T
+          << ">((w0 & 0xffffffffull) | (w1 << 32)); break; }\n";
+      }
+      k << "            if (++spins > (1u << 24)) { cc_flag(err, 4); flag = 2; break; }\n"
+        << "            __builtin_amdgcn_s_sleep(1);\n"
+        << "          }\n"
+        << "        }\n"
+        << "        const cc_u64 pm = __ballot(flag == 2);\n"
+        << "        const int L = pm ? (__ffsll((long long)pm) - 1) : 63;\n"
+        << "        " << T << " w = lane <= L ? val : " << ini << "();\n";
+      for (int off = 1; off < 64; off *= 2)
+        k << "        { const " << T << " o = __shfl_down(w, " << off << "); if ((lane & " << (2 * off - 1)
+          << ") == 0) w = " << cmb << "(o, w); }\n";
+      k << "        w = __shfl(w, 0);\n"
+        << "        acc = have ? " << cmb << "(w, acc) : w;\n"
+        << "        have = true;\n"
+        << "        if (pm) break;\n"
+        << "        j -= 64;\n"
+        << "      }\n"
+        << "      if (lane == 0) {\n"
+        << "        s_prefix = acc;\n"
+        << "        const " << T << " incl = " << cmb << "(acc, run);\n"
+        << "        " << publish("tile", "2", "incl") << ";\n"
+        << "      }\n"
+        << "    }\n"
+        << "    __syncthreads();\n"
+        << "    const " << T << " pfx = s_prefix;\n"
+        << "#pragma unroll\n"
+        << "    for (int u = 0; u < " << U << "; u++) {\n"
+        << "      v[u][0] = " << cmb << "(pfx, v[u][0]); v[u][1] = " << cmb << "(pfx, v[u][1]);\n"
+        << "      v[u][2] = " << cmb << "(pfx, v[u][2]); v[u][3] = " << cmb << "(pfx, v[u][3]);\n"
+        << "    }\n"
+        << "  }\n";
+    }
+    k << "#pragma unroll\n"
+      << "  for (int u = 0; u < " << U << "; u++) {\n"
+      << "    const int e = threadIdx.x * 4 + 1024 * u;\n";
+    if (vec) {
+      k << "    if (e < tl) {\n"
+        << "      cc_v4<" << T << "> o;\n";
+      for (int c = 0; c < 4; c++) k << "      o." << comp[c] << " = v[u][" << c << "];\n";
+      k << "      *(cc_v4<" << T << ">*)(b" << out << " + base + e) = o;\n"
+        << "    }\n";
+    } else {
+      for (int c = 0; c < 4; c++)
+        k << "    if (e + " << c << " < tl) b" << out << "[base + e + " << c << "] = v[u][" << c << "];\n";
+    }
+    k << "  }\n"
+      << "}\n";
     src << k.str();
-    int kscan = add_kernel(kname, args, (int)tiles, 256, "scan_lookback");
-    return {kinit, kscan};
+    int kscan = add_kernel(kname, args, (int)tiles, 256, chained ? "scan_lookback" : "scan_tile");
+    if (chained) return {kinit, kscan};
+    return {kscan};
   }
 
   // ---- Scatter_add root (K9 zero fill + K10 atomics) ---------------------

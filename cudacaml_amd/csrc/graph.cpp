@@ -307,6 +307,42 @@ Graph parse_wire(const std::string &text) {
   return g;
 }
 
+// Dsl.transpose (dsl.ml:167-182) builds, for x : [m; n], the gather
+// out[k] = x[(k - (k/m)*m) * n + k/m] over iota [n; m]. Recognising that
+// exact shape lets the backend drop the bounds check (the index is in
+// range by construction) and load the operand of a matmul coalesced.
+static bool is_const_i32(const Graph &g, int x, int64_t v) {
+  const XNode &n = g.xs[x];
+  return n.kind == XK::Const && n.dt == DT::I32 && (int32_t)n.i == (int32_t)v;
+}
+
+static bool is_arg0(const Graph &g, int x) { return g.xs[x].kind == XK::Arg && g.xs[x].arg == 0; }
+
+static bool is_div_k_m(const Graph &g, int x, int64_t m) {
+  const XNode &n = g.xs[x];
+  return n.kind == XK::Bin && n.op == B_DIV && is_arg0(g, n.a) && is_const_i32(g, n.b, m);
+}
+
+int transpose_source(const Graph &g, int t) {
+  const TNode &n = g.ts[t];
+  if (n.kind != TK::Gather || n.shape.size() != 2) return -1;
+  const TNode &idx = g.ts[n.a];
+  const TNode &src = g.ts[n.b];
+  if (src.shape.size() != 2 || idx.kind != TK::Map || g.ts[idx.a].kind != TK::Iota) return -1;
+  int64_t m = src.shape[0], nn = src.shape[1];
+  if (n.shape[0] != nn || n.shape[1] != m) return -1;
+  // add(mul(sub(k, mul(div(k, m), m)), n), div(k, m))
+  const XNode &add = g.xs[idx.body];
+  if (add.kind != XK::Bin || add.op != B_ADD || !is_div_k_m(g, add.b, m)) return -1;
+  const XNode &mul = g.xs[add.a];
+  if (mul.kind != XK::Bin || mul.op != B_MUL || !is_const_i32(g, mul.b, nn)) return -1;
+  const XNode &sub = g.xs[mul.a];
+  if (sub.kind != XK::Bin || sub.op != B_SUB || !is_arg0(g, sub.a)) return -1;
+  const XNode &qm = g.xs[sub.b];
+  if (qm.kind != XK::Bin || qm.op != B_MUL || !is_div_k_m(g, qm.a, m) || !is_const_i32(g, qm.b, m)) return -1;
+  return n.b;
+}
+
 Plan fusion_plan(const Graph &g) {
   Plan p;
   p.materialized.assign(g.ts.size(), false);

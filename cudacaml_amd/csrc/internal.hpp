@@ -114,6 +114,10 @@ struct Plan {
 };
 Plan fusion_plan(const Graph &g);
 
+// Position of x if tensor t is Dsl.transpose x (a gather whose index is the
+// transpose map over iota), else -1.
+int transpose_source(const Graph &g, int t);
+
 // ---------------------------------------------------------------------------
 // Program: what the code generator produces and the executor runs
 // (Kernel_ir.program, lib/lower/kernel_ir.ml:124-141).

@@ -129,10 +129,14 @@ def test_s13_bs_greeks_f64(device):
     diff(g, bs.inputs(F64, seed=7), tolerance=1e-6)
 
 
-def test_config_rows_small(device):
-    g = C.rows(256, 8192)
-    x = C.uniform_pm1(3, (256, 8192))
-    assert_policy(g, [("x", x)])
+def test_config_rows_bit_exact(device):
+    """With >= 1024 rows each row is folded by one lane in the interpreter's
+    order: reduce_rows add/max and scan_rows add are bit-identical."""
+    g = C.rows(1024, 8192)
+    x = C.uniform_pm1(3, (1024, 8192))
+    exp, got = both(g, [("x", x)])
+    for (n, e), (_, v) in zip(exp, got):
+        np.testing.assert_array_equal(e, v, err_msg=n)
 
 
 def test_config_global_scan_bit_exact(device):

@@ -1,0 +1,146 @@
+"""Structure of what Backend_hip generates, read off its plan and source
+without a device: the fusion plan (Fusion.plan's four rules,
+fusion.ml:41-73), kernel counts and template choice per root, the host
+plan's shape (lower.ml:968-1012), the printer's integer-exactness
+spellings, and that generated modules compile for gfx950 with hiprtc.
+Mirrors test_fusion.ml, test_lower.ml, test_multikernel.ml, test_emit.ml,
+test_scatter.ml:50-70 and test_matmul.ml:105-139."""
+
+import pytest
+
+from cudacaml_amd import backend_hip as H
+from cudacaml_amd import dsl as D
+from cudacaml_amd import rng
+from cudacaml_amd import runtime
+from cudacaml_amd.examples import configs as C
+from cudacaml_amd.examples import programs as P
+from cudacaml_amd.examples import saxpy as sx
+from cudacaml_amd.ir import F32, F64, I32, I64, Graph
+
+
+def parse(plan):
+    bufs, kernels, ops = [], [], []
+    for line in plan.splitlines():
+        f = line.split()
+        if f[0] == "buffer":
+            bufs.append((f[2], f[3], int(f[4]), f[5]))
+        elif f[0] == "kernel":
+            kernels.append((f[1], f[2]))
+        elif f[0] in ("alloc", "upload", "launch", "download", "free"):
+            ops.append(tuple(f))
+    return bufs, kernels, ops
+
+
+def kernels_of(g):
+    return parse(H.plan(g))[1]
+
+
+def test_chain_is_one_kernel():
+    assert [t for _, t in kernels_of(P.chain(4096).graph())] == ["map"]
+
+
+def test_saxpy_is_map_then_reduce():
+    ks = kernels_of(sx.program(1 << 20, 2.0))
+    assert [t for _, t in ks] == ["map", "reduce_split"]
+
+
+def test_fanout_materialises_shared_node_once():
+    bufs, ks, _ = parse(H.plan(P.fanout(1000).graph()))
+    computed = [b for b in bufs if b[3] == "computed"]
+    # s = x*x (fan-out 3) plus the three outputs a, b, c
+    assert len(computed) == 4 and len(ks) == 4
+
+
+def test_transpose_fuses_into_rows_reduce():
+    x = D.param("x", F32, (8, 16))
+    r = D.reduce_rows(D.add, D.const(F32, 0.0), D.map(lambda e: D.mul(e, e), D.transpose(x)))
+    bufs, ks, _ = parse(H.plan(Graph.create("g", [("r", r)])))
+    assert len(ks) == 1 and [b[3] for b in bufs] == ["param", "computed"]
+
+
+def test_barriers_are_materialised():
+    idx, src = D.param("idx", I32, (6,)), D.param("src", F32, (6,))
+    s = D.scatter_add(idx, src, (4,))
+    bufs, ks, ops = parse(H.plan(Graph.create("h", [("r", D.map(D.neg, s))])))
+    assert [t for _, t in ks] == ["scatter_zero", "scatter_atomic", "map"]
+    launches = [o[1] for o in ops if o[0] == "launch"]
+    assert launches == [k for k, _ in ks]
+
+
+def test_matmul_barrier_fuses_operand_maps():
+    a, b = D.param("a", F64, (20, 30)), D.param("b", F64, (30, 10))
+    bufs, ks, _ = parse(H.plan(Graph.create("mm", [("c", D.matmul(D.map(D.exp, a), b))])))
+    assert len(ks) == 1 and ks[0][1].startswith("matmul")
+    assert [b[0] for b in bufs] == ["p_a", "p_b", bufs[2][0]]
+
+
+def test_host_plan_shape():
+    """Alloc params then computed, upload, launches, download, free in the
+    same order as alloc (lower.ml:977-1011)."""
+    bufs, ks, ops = parse(H.plan(sx.program(1024, 2.0)))
+    kinds = [o[0] for o in ops]
+    first_upload = kinds.index("upload")
+    assert all(k == "alloc" for k in kinds[:first_upload])
+    assert kinds[first_upload:first_upload + 2] == ["upload", "upload"]
+    assert [o[1] for o in ops if o[0] == "download"] == ["r", "s"]
+    allocs = [o[1] for o in ops if o[0] == "alloc"]
+    frees = [o[1] for o in ops if o[0] == "free"]
+    assert sorted(allocs) == sorted(frees)
+
+
+def test_uniform_graph_uploads_only_the_seed():
+    g = Graph.create("u", [("r", rng.uniform(F32, D.scalar("seed", I32), (16,)))])
+    _, _, ops = parse(H.plan(g))
+    assert [o for o in ops if o[0] == "upload"] == [("upload", "seed", "p_seed")]
+
+
+@pytest.mark.parametrize("rows,n,tpl", [(8192, 8192, "reduce_rowseq"), (1, 1 << 24, "reduce_split"),
+                                        (600, 4096, "reduce_block"), (64, 64, "reduce_wave")])
+def test_reduce_template_choice(rows, n, tpl):
+    x = D.param("x", F32, (rows, n))
+    assert [t for _, t in kernels_of(Graph.create("r", [("s", D.reduce_rows(D.add, D.const(F32, 0), x))]))] == [tpl]
+
+
+@pytest.mark.parametrize("rows,n,tpls", [(8192, 8192, ["scan_rowseq"]), (1, 1 << 28, ["scan_init", "scan_lookback"]),
+                                         (100, 5000, ["scan_tile"]), (100, 50, ["scan_wave"])])
+def test_scan_template_choice(rows, n, tpls):
+    x = D.param("x", I32, (rows, n))
+    assert [t for _, t in kernels_of(Graph.create("s", [("p", D.scan_rows(D.add, D.const(I32, 0), x))]))] == tpls
+
+
+def test_config_plans():
+    assert [t for _, t in kernels_of(C.rows())] == ["reduce_rowseq", "reduce_rowseq", "scan_rowseq"]
+    assert [t for _, t in kernels_of(C.scatter_gather())] == ["scatter_zero", "scatter_atomic", "map"]
+    ks = kernels_of(C.mc_paths())
+    assert "scan_rowseq" in [t for _, t in ks]
+
+
+def test_printer_integer_exactness():
+    """Wrapping through unsigned, masked logical shifts, OCaml min/max and
+    the f32-constant rule (emit.ml:60-135 and cudacaml_backend_interp.ml
+    :246)."""
+    x = D.param("x", I32, (4,))
+    src = H.source(Graph.create("g", [("r", D.map(lambda e: D.shr(D.mul(e, D.const(I32, 3)), D.const(I32, 3)), x))]))
+    assert "(cc_u32)" in src and "& 31" in src
+    y = D.param("y", I64, (4,))
+    src = H.source(Graph.create("g", [("r", D.map(lambda e: D.shl(e, D.const(I64, 3)), y))]))
+    assert "cc_u64" in src and "& 63" in src
+    z = D.param("z", F32, (4,))
+    src = H.source(Graph.create("g", [("r", D.map(lambda e: D.max(D.mul(e, D.const(F32, 0.1)), e), z))]))
+    assert "(float)(" in src and "(double)" in src and "cc_maxf" in src
+    src = H.source(Graph.create("g", [("r", D.map(lambda e: D.erfinv(D.sin(e)), z))]))
+    assert "erfinvf(" in src and "sinf(" in src
+    w = D.param("w", F64, (4,))
+    src = H.source(Graph.create("g", [("r", D.map(lambda e: D.erfinv(D.cos(e)), w))]))
+    assert "erfinv(" in src and "erfinvf(" not in src
+
+
+def test_generated_modules_compile_for_gfx950():
+    for g in [C.rows(2048, 1024), C.global_scan(1 << 16), C.scatter_gather(1 << 12, 1 << 8),
+              C.matmul(64), C.mc_paths(256, 16), P.bs_greeks(1024).graph()]:
+        assert runtime.Jit.check(g.name, H.source(g)) > 0
+
+
+def test_jit_reports_compile_errors():
+    with pytest.raises(RuntimeError, match="hiprtc"):
+        runtime.Jit.check("bad", "this is not HIP")
