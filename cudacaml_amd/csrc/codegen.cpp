@@ -136,7 +136,15 @@ struct ElemFn {
 
 class Gen {
  public:
-  Gen(const Graph &g, const Plan &p, const std::vector<int> &buf_of) : g_(g), p_(p), buf_of_(buf_of) {}
+  Gen(const Graph &g, const Plan &p, const std::vector<int> &buf_of) : g_(g), p_(p), buf_of_(buf_of) {
+    for (const XNode &n : g_.xs) {
+      int xa = -1, xb = -1;
+      if (n.kind == XK::Bin && n.dt == DT::I64 && n.op == B_MUL && zext32(n.a, &xa) && zext32(n.b, &xb)) {
+        wide_pairs_.insert({xa, xb});
+        wide_pairs_.insert({xb, xa});
+      }
+    }
+  }
 
   // f(i) = the value of tensor `t` at flat index i. If `inline_root`, t is
   // computed (inlined) even though it is materialised: it is the kernel's
@@ -198,6 +206,30 @@ class Gen {
   std::vector<int> ident_, ptrs_;
   bool uses_err_ = false;
   std::map<std::pair<int, std::string>, Val> tmemo_;
+  std::map<std::pair<std::string, std::string>, Val> wide_;  // 64-bit products by operand
+
+  std::set<std::pair<int, int>> wide_pairs_;  // I32 operand pairs of those products
+
+  Val wide_product(const Val &a, const Val &b) {
+    auto w = wide_.find({a.s, b.s});
+    if (w == wide_.end()) w = wide_.find({b.s, a.s});
+    if (w != wide_.end()) return w->second;
+    Val p = def(VC::I64, "((long long)((cc_u64)(cc_u32)(" + a.s + ") * (cc_u64)(cc_u32)(" + b.s + ")))");
+    wide_[{a.s, b.s}] = p;
+    return p;
+  }
+
+  // x is and(cast I64 (y : I32), 0xFFFFFFFF): *y is the I32 word.
+  bool zext32(int x, int *y) const {
+    const XNode &n = g_.xs[x];
+    if (n.kind != XK::Bin || n.op != B_AND || n.dt != DT::I64) return false;
+    const XNode &c = g_.xs[n.b];
+    const XNode &e = g_.xs[n.a];
+    if (c.kind != XK::Const || c.i != 0xFFFFFFFFLL) return false;
+    if (e.kind != XK::Cast || g_.xs[e.a].dt != DT::I32) return false;
+    *y = e.a;
+    return true;
+  }
 
   void reset(bool allow_ident) {
     body_.str("");
@@ -208,6 +240,7 @@ class Gen {
     ptrs_.clear();
     uses_err_ = false;
     tmemo_.clear();
+    wide_.clear();
   }
 
   Val def(VC c, const std::string &rhs) {
@@ -310,7 +343,20 @@ class Gen {
         if (n.arg >= (int)env.size()) throw Failure(strf("Lower: unbound Arg %d", n.arg));
         return env[n.arg];
       case XK::Index: return idx;
-      case XK::Bin: return binop(n, go(n.a), go(n.b));
+      case XK::Bin: {
+        // Rng's mulhilo (rng.ml:20-29): the I64 product of two zero-extended
+        // I32 words, and the I32 product of the same words. Both halves come
+        // from one 32x32->64 multiply (a single v_mad_u64_u32).
+        int xa = -1, xb = -1;
+        if (n.dt == DT::I64 && n.op == B_MUL && zext32(n.a, &xa) && zext32(n.b, &xb))
+          return wide_product(go(xa), go(xb));
+        Val a = go(n.a), b = go(n.b);
+        if (n.dt == DT::I32 && n.op == B_MUL && wide_pairs_.count({n.a, n.b})) {
+          Val p = wide_product(a, b);
+          return def(VC::I32, "((int)(cc_u32)(cc_u64)(" + p.s + "))");
+        }
+        return binop(n, a, b);
+      }
       case XK::Un: return unop(n, go(n.a));
       case XK::Cmp: {
         Val a = go(n.a), b = go(n.b);
@@ -459,6 +505,7 @@ const char *kPrelude = R"PRELUDE(// Generated by cchip (Backend_hip) for gfx950.
 typedef unsigned int cc_u32;
 typedef unsigned long long cc_u64;
 template <typename T> struct __attribute__((aligned(4 * sizeof(T)))) cc_v4 { T x, y, z, w; };
+template <typename T> struct __attribute__((aligned(2 * sizeof(T)))) cc_v2 { T x, y; };
 
 // Float.min / Float.max of OCaml: NaN if either operand is NaN, -0 below
 // +0. These are IEEE 754-2019 minimum/maximum, which gfx950 executes as
@@ -1327,6 +1374,234 @@ struct Lowering {
     return ks;
   }
 
+  // ---- Matmul on the matrix cores ------------------------------------------
+  // f32: v_mfma_f32_32x32x2f32, block tile 128x128x16, four waves of 64x64.
+  // f64: v_mfma_f64_16x16x4f64, block tile 64x64x16, four waves of 32x32.
+  // Within a 16-deep k tile, lane group g (of 64/MT groups) takes the k
+  // values g*S .. g*S+S-1 in order (A and B use the same permutation), so a
+  // lane's operands for the whole tile are one contiguous run along k.
+  // Each operand is staged in the LDS layout that matches its source:
+  // k-contiguous rows for A and for a transposed B, MN-contiguous rows for B
+  // and for a transposed A, so global loads stay coalesced either way;
+  // operands that are fused expressions are computed into the k-contiguous
+  // layout. Two LDS buffers, next tile prefetched into registers. Products
+  // accumulate on the matrix cores, so f32 sums are not in the
+  // interpreter's order: results match it to rounding, not bit for bit.
+  std::vector<int> lower_matmul_mfma(int t, int64_t M, int64_t N, int64_t K) {
+    const TNode &n = g.ts[t];
+    std::string id = std::to_string(n.id);
+    std::string kname = "k_" + id;
+    bool f64 = n.dt == DT::F64;
+    std::string T = dt_ctype(n.dt);
+    int out = buf_of[t];
+    const int64_t BM = f64 ? 64 : 128, BK = 16, MT = f64 ? 16 : 32;
+    const int64_t G = 64 / MT;    // lane groups along k
+    const int64_t S = BK / G;     // k steps per tile held by one lane
+    const int64_t WT = BM / 2;    // wave tile
+    const int64_t RT = WT / MT;   // instruction tiles per wave side
+    const int64_t VEC = 16 / dt_size(n.dt);        // elements per 16-byte access
+    const int64_t PER = BM * BK / 256;             // elements per thread per operand tile
+    const int64_t KP = BK + VEC;                   // k-contiguous row stride (keeps 16-byte alignment)
+    const int64_t MP = BM + VEC;                   // mn-contiguous row stride
+    // Operand modes: 0 direct buffer, 1 transpose of a buffer, 2 fused expression.
+    struct Opnd {
+      int mode;
+      int buf;
+      bool kcontig;
+      ElemFn fn;
+    };
+    auto classify = [&](int op, bool is_a) {
+      Opnd o;
+      o.buf = -1;
+      if (plan.materialized[op]) {
+        o.mode = 0;
+        o.buf = buf_of[op];
+        o.kcontig = is_a;  // A[m][k] rows are k-contiguous; B[k][n] rows are n-contiguous
+      } else if (transpose_source(g, op) >= 0 && plan.materialized[transpose_source(g, op)] &&
+                 !plan.materialized[g.ts[op].a]) {
+        o.mode = 1;
+        o.buf = buf_of[transpose_source(g, op)];
+        o.kcontig = !is_a;
+      } else {
+        o.mode = 2;
+        o.kcontig = true;
+        o.fn = gen.element_fn(std::string(is_a ? "fa_" : "fb_") + id, op, false, false);
+        src << o.fn.code;
+      }
+      return o;
+    };
+    Opnd A = classify(n.a, true), B = classify(n.b, false);
+    Params p;
+    for (Opnd *o : {&A, &B}) {
+      if (o->mode == 2) add_in(p, o->fn);
+      else {
+        bool dup = false;
+        for (int x : p.in) dup |= x == o->buf;
+        if (!dup) p.in.push_back(o->buf);
+      }
+    }
+    p.out.push_back(out);
+    std::vector<int> args;
+    std::string params = param_list(p, args);
+    const int64_t ALDS = A.kcontig ? BM * KP : BK * MP;
+    const int64_t BLDS = B.kcontig ? BM * KP : BK * MP;
+    std::string V = f64 ? "cc_v2<double>" : "cc_v4<float>";  // one 16-byte access
+    std::ostringstream k;
+    // Global -> registers for one operand tile. `base` is the tile's first
+    // row (m for A, n for B) along MN; kt the tile's first k.
+    auto gload = [&](const Opnd &o, bool is_a, const std::string &reg) {
+      std::ostringstream l;
+      std::string mnb = is_a ? "bm" : "bn";
+      int64_t MNtot = is_a ? M : N;
+      if (o.kcontig) {
+        // thread -> (row r, k offset kk) with PER consecutive k
+        l << "    { const int r = threadIdx.x / " << BK / PER << ", kk = (threadIdx.x % " << BK / PER << ") * " << PER
+          << ";\n";
+        if (o.mode == 2) {
+          for (int64_t c = 0; c < PER; c++) {
+            std::string idx = is_a ? "(" + mnb + " + r) * " + std::to_string(K) + " + kt + kk + " + std::to_string(c)
+                                   : "(kt + kk + " + std::to_string(c) + ") * " + std::to_string(N) + " + " + mnb +
+                                         " + r";
+            l << "      " << reg << "[" << c << "] = " << o.fn.call_scalar(idx) << ";\n";
+          }
+        } else {
+          // direct A ([M][K]) or transposed B (source [N][K]): row length K
+          l << "      const " << T << "* s = b" << o.buf << " + (size_t)(" << mnb << " + r) * " << K << " + kt + kk;\n";
+          for (int64_t c = 0; c < PER; c += VEC)
+            l << "      *(" << V << "*)&" << reg << "[" << c << "] = *(const " << V << "*)(s + " << c << ");\n";
+        }
+        l << "    }\n";
+      } else {
+        // thread -> (k row kk, MN offset c0) with PER consecutive MN
+        l << "    { const int kk = threadIdx.x / " << BM / PER << ", c0 = (threadIdx.x % " << BM / PER << ") * " << PER
+          << ";\n"
+          << "      const " << T << "* s = b" << o.buf << " + (size_t)(kt + kk) * " << MNtot << " + " << mnb
+          << " + c0;\n";
+        for (int64_t c = 0; c < PER; c += VEC)
+          l << "      *(" << V << "*)&" << reg << "[" << c << "] = *(const " << V << "*)(s + " << c << ");\n";
+        l << "    }\n";
+      }
+      return l.str();
+    };
+    auto lstore = [&](const Opnd &o, const std::string &lds, const std::string &reg) {
+      std::ostringstream l;
+      if (o.kcontig)
+        l << "    { const int r = threadIdx.x / " << BK / PER << ", kk = (threadIdx.x % " << BK / PER << ") * " << PER
+          << ";\n"
+          << "      " << T << "* d = " << lds << " + r * " << KP << " + kk;\n";
+      else
+        l << "    { const int kk = threadIdx.x / " << BM / PER << ", c0 = (threadIdx.x % " << BM / PER << ") * "
+          << PER << ";\n"
+          << "      " << T << "* d = " << lds << " + kk * " << MP << " + c0;\n";
+      for (int64_t c = 0; c < PER; c += VEC)
+        l << "      *(" << V << "*)(d + " << c << ") = *(const " << V << "*)&" << reg << "[" << c << "];\n";
+      l << "    }\n";
+      return l.str();
+    };
+    // LDS -> fragment registers: lane's S consecutive k for instruction tile rt
+    auto fragload = [&](const Opnd &o, const std::string &lds, const std::string &frag, const std::string &mn0) {
+      std::ostringstream l;
+      l << "#pragma unroll\n"
+        << "      for (int rt = 0; rt < " << RT << "; rt++) {\n"
+        << "        const int mn = " << mn0 << " + rt * " << MT << " + (lane % " << MT << ");\n"
+        << "        const int k0 = (lane / " << MT << ") * " << S << ";\n";
+      if (o.kcontig) {
+        for (int64_t c = 0; c < S; c += VEC)
+          l << "        *(" << V << "*)&" << frag << "[rt][" << c << "] = *(const " << V << "*)(" << lds << " + mn * "
+            << KP << " + k0 + " << c << ");\n";
+      } else {
+        l << "#pragma unroll\n"
+          << "        for (int s2 = 0; s2 < " << S << "; s2++) " << frag << "[rt][s2] = " << lds << "[(k0 + s2) * " << MP
+          << " + mn];\n";
+      }
+      l << "      }\n";
+      return l.str();
+    };
+    std::string accT = f64 ? "cc_f64x4" : "cc_f32x16";
+    int64_t NACC = f64 ? 4 : 16;
+    std::string mfma = f64 ? "__builtin_amdgcn_mfma_f64_16x16x4f64" : "__builtin_amdgcn_mfma_f32_32x32x2f32";
+    int64_t tiles_m = M / BM, tiles_n = N / BM, ntiles = tiles_m * tiles_n;
+    k << "typedef " << T << " " << accT << " __attribute__((ext_vector_type(" << NACC << ")));\n"
+      << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
+      << "  __shared__ __attribute__((aligned(16))) " << T << " As[2][" << ALDS << "];\n"
+      << "  __shared__ __attribute__((aligned(16))) " << T << " Bs[2][" << BLDS << "];\n"
+      << "  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;\n"
+      << "  const int wm = (wid >> 1) * " << WT << ", wn = (wid & 1) * " << WT << ";\n"
+      // blocks are dispatched round-robin over the 8 XCDs; give each XCD a
+      // contiguous run of tiles so its L2 sees shared A row panels.
+      << "  int tile = blockIdx.x;\n";
+    if (ntiles % 8 == 0) k << "  tile = (tile % 8) * " << ntiles / 8 << " + tile / 8;\n";
+    k << "  const int bm = (tile / " << tiles_n << ") * " << BM << ", bn = (tile % " << tiles_n << ") * " << BM << ";\n"
+      << "  " << accT << " acc[" << RT << "][" << RT << "];\n"
+      << "#pragma unroll\n"
+      << "  for (int i = 0; i < " << RT << "; i++)\n"
+      << "#pragma unroll\n"
+      << "    for (int j = 0; j < " << RT << "; j++) acc[i][j] = (" << accT << ")(0);\n"
+      << "  __attribute__((aligned(16))) " << T << " ra[" << PER << "], rb[" << PER << "];\n";
+    // Two-level accumulation (f32): the matrix cores sum KC-deep chunks into
+    // `acc`, which is folded into `tot` with plain adds and cleared. Error
+    // then grows with sqrt(KC) + sqrt(K / KC) instead of sqrt(K).
+    int64_t KCT = f64 ? 0 : tune("mm_chunk_tiles", 4);
+    if (KCT > 0 && (K / BK) % KCT != 0) KCT = 0;
+    if (KCT > 0)
+      k << "  " << accT << " tot[" << RT << "][" << RT << "];\n"
+        << "#pragma unroll\n"
+        << "  for (int i = 0; i < " << RT << "; i++)\n"
+        << "#pragma unroll\n"
+        << "    for (int j = 0; j < " << RT << "; j++) tot[i][j] = (" << accT << ")(0);\n";
+    k << "  int kt = 0;\n"
+      << gload(A, true, "ra") << gload(B, false, "rb") << lstore(A, "As[0]", "ra") << lstore(B, "Bs[0]", "rb")
+      << "  __syncthreads();\n"
+      << "  for (int it = 0; it < " << K / BK << "; it++) {\n"
+      << "    const int buf = it & 1;\n"
+      << "    kt = (it + 1) * " << BK << ";\n"
+      << "    if (it + 1 < " << K / BK << ") {\n"
+      << gload(A, true, "ra") << gload(B, false, "rb") << "    }\n"
+      << "    {\n"
+      << "      __attribute__((aligned(16))) " << T << " fa[" << RT << "][" << S << "], fb[" << RT << "][" << S << "];\n"
+      << "      const " << T << "* const al = As[buf];\n"
+      << "      const " << T << "* const bl = Bs[buf];\n"
+      << fragload(A, "al", "fa", "wm") << fragload(B, "bl", "fb", "wn") << "#pragma unroll\n"
+      << "      for (int s2 = 0; s2 < " << S << "; s2++)\n"
+      << "#pragma unroll\n"
+      << "        for (int i = 0; i < " << RT << "; i++)\n"
+      << "#pragma unroll\n"
+      << "          for (int j = 0; j < " << RT << "; j++) acc[i][j] = " << mfma
+      << "(fa[i][s2], fb[j][s2], acc[i][j], 0, 0, 0);\n"
+      << "    }\n"
+      << "    if (it + 1 < " << K / BK << ") {\n"
+      << lstore(A, "As[buf ^ 1]", "ra") << lstore(B, "Bs[buf ^ 1]", "rb") << "    }\n";
+    if (KCT > 0)
+      k << "    if ((it + 1) % " << KCT << " == 0) {\n"
+        << "#pragma unroll\n"
+        << "      for (int i = 0; i < " << RT << "; i++)\n"
+        << "#pragma unroll\n"
+        << "        for (int j = 0; j < " << RT << "; j++) { tot[i][j] += acc[i][j]; acc[i][j] = (" << accT << ")(0); }\n"
+        << "    }\n";
+    k << "    __syncthreads();\n"
+      << "  }\n"
+      // epilogue: the accumulator layout of the instruction
+      << "#pragma unroll\n"
+      << "  for (int i = 0; i < " << RT << "; i++)\n"
+      << "#pragma unroll\n"
+      << "    for (int j = 0; j < " << RT << "; j++) {\n"
+      << "      const int col = bn + wn + j * " << MT << " + (lane % " << MT << ");\n"
+      << "#pragma unroll\n"
+      << "      for (int r = 0; r < " << NACC << "; r++) {\n";
+    if (f64)
+      k << "        const int row = bm + wm + i * 16 + (lane / 16) * 4 + r;\n";
+    else
+      k << "        const int row = bm + wm + i * 32 + (r / 4) * 8 + (lane / 32) * 4 + (r % 4);\n";
+    k << "        b" << out << "[(size_t)row * " << N << " + col] = " << (KCT > 0 ? "tot" : "acc") << "[i][j][r];\n"
+      << "      }\n"
+      << "    }\n"
+      << "}\n";
+    src << k.str();
+    std::string role = std::string("matmul_mfma_") + (f64 ? "f64" : "f32") + "_" + "a" + std::to_string(A.mode) +
+                       "b" + std::to_string(B.mode);
+    return {add_kernel(kname, args, (int)ntiles, 256, role)};
+  }
+
   // ---- Matmul root (K11) --------------------------------------------------
   // Generic tiled product: one output per thread, k ascending, each product
   // and sum rounded separately, zero-padded edge tiles. For float dtypes
@@ -1340,6 +1615,10 @@ struct Lowering {
     int64_t M = n.shape[0], N = n.shape[1];
     int64_t K = g.ts[n.a].shape[1];
     if (M == 0 || N == 0) return {};
+    if (dt_is_float(n.dt) && K > 0 && tune("mm_mfma", 1)) {
+      int64_t BM = n.dt == DT::F32 ? 128 : 64;
+      if (M % BM == 0 && N % BM == 0 && K % 16 == 0) return lower_matmul_mfma(t, M, N, K);
+    }
     ElemFn fa = gen.element_fn("fa_" + id, n.a, false, false);
     ElemFn fb = gen.element_fn("fb_" + id, n.b, false, false);
     src << fa.code << fb.code;

@@ -157,3 +157,69 @@ def test_config_scatter_gather(device):
 def test_config_mc_paths_small(device):
     g = C.mc_paths(4096, 64, F32)
     assert_policy(g, bs.inputs(F32, seed=7))
+
+
+def _plan_roles(g):
+    return [l.split()[2] for l in H.plan(g).splitlines() if l.startswith("kernel")]
+
+
+@pytest.mark.parametrize("dtype,m,k,n", [(F32, 256, 1024, 384), (F64, 128, 256, 192), (F32, 128, 16, 128),
+                                         (F64, 64, 48, 64)])
+def test_matmul_mfma_vs_oracle(device, dtype, m, k, n):
+    """Aligned sizes take the matrix-core kernel; the accumulation-policy
+    band (1e-4 f32, 1e-12 f64, relative) against the sequential oracle."""
+    g = C.matmul(n, dtype, k=k, m=m)
+    assert any(r.startswith("matmul_mfma") for r in _plan_roles(g))
+    inputs = [("a", C.uniform_pm1(11, (m, k)).astype(dtype.np)), ("b", C.uniform_pm1(12, (k, n)).astype(dtype.np))]
+    assert_policy(g, inputs)
+
+
+def test_matmul_mfma_fused_operand(device):
+    """An operand that is a map over a param is computed while staging the
+    tile (expression mode), not materialised."""
+    a, b = D.param("a", F32, (128, 64)), D.param("b", F32, (64, 256))
+    g = Graph.create("mmx", [("c", D.matmul(D.map(lambda e: D.mul(e, e), a), D.map(D.exp, b)))])
+    assert [r for r in _plan_roles(g)] == ["matmul_mfma_f32_a2b2"]
+    assert_policy(g, [("a", C.uniform_pm1(1, (128, 64))), ("b", C.uniform_pm1(2, (64, 256)))])
+
+
+@pytest.mark.parametrize("dtype", [F32, F64])
+def test_matmul_grad_transposed_operands(device, dtype):
+    """Grad of sum(A@B): dA = 1 @ B^T and dB = A^T @ 1 use the transposed
+    operand modes; every row of dA is the row sums of B, every column of dB
+    the column sums of A."""
+    n = 256
+    g = C.matmul_grad(n, dtype)
+    roles = _plan_roles(g)
+    assert {"matmul_mfma_%s_a0b1" % dtype.name, "matmul_mfma_%s_a1b0" % dtype.name} <= set(roles), roles
+    inputs = [("a", C.uniform_pm1(3, (n, n)).astype(dtype.np)), ("b", C.uniform_pm1(4, (n, n)).astype(dtype.np))]
+    exp, got = assert_policy(g, inputs)
+    out = dict(got)
+    a64, b64 = inputs[0][1].astype(np.float64), inputs[1][1].astype(np.float64)
+    tol = 1e-4 if dtype is F32 else 1e-12
+    da = out["ds/da"].astype(np.float64)
+    db = out["ds/db"].astype(np.float64)
+    np.testing.assert_allclose(da, np.broadcast_to(b64.sum(1), (n, n)), rtol=tol, atol=tol)
+    np.testing.assert_allclose(db, np.broadcast_to(a64.sum(0)[:, None], (n, n)), rtol=tol, atol=tol)
+
+
+def test_matmul_unaligned_takes_generic_kernel(device):
+    g = C.matmul(100, F32, k=37, m=130)
+    assert not any(r.startswith("matmul_mfma") for r in _plan_roles(g))
+    assert_policy(g, [("a", C.uniform_pm1(5, (130, 37))), ("b", C.uniform_pm1(6, (37, 100)))])
+
+
+def test_matmul_f32_full_size_vs_exact(device):
+    """At the benchmark's 4096^3 the device result is within the f32 band of
+    the exact (float64) product of the same f32 inputs."""
+    n = 4096
+    g = C.matmul(n, F32)
+    a, b = C.uniform_pm1(7, (n, n)), C.uniform_pm1(8, (n, n))
+    c = H.compile(g)
+    try:
+        got = dict(H.run(c, [("a", a), ("b", b)]))["c"].astype(np.float64)
+    finally:
+        c.release()
+    exact = a.astype(np.float64) @ b.astype(np.float64)
+    err = np.abs(got - exact) / (1.0 + np.abs(exact))
+    assert err.max() <= 1e-4, err.max()
