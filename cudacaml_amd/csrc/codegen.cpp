@@ -1588,8 +1588,8 @@ struct Lowering {
       << "      const int col = bn + wn + j * " << MT << " + (lane % " << MT << ");\n"
       << "#pragma unroll\n"
       << "      for (int r = 0; r < " << NACC << "; r++) {\n";
-    if (f64)
-      k << "        const int row = bm + wm + i * 16 + (lane / 16) * 4 + r;\n";
+    if (f64)  // the f64 instruction interleaves rows: lane group g holds rows g, g+4, g+8, g+12
+      k << "        const int row = bm + wm + i * 16 + (lane / 16) + 4 * r;\n";
     else
       k << "        const int row = bm + wm + i * 32 + (r / 4) * 8 + (lane / 32) * 4 + (r % 4);\n";
     k << "        b" << out << "[(size_t)row * " << N << " + col] = " << (KCT > 0 ? "tot" : "acc") << "[i][j][r];\n"
