@@ -110,6 +110,14 @@ def build_workload(name, H, C):
         return Workload(name, progs, "GB/s", "f32/i32",
                         "config2: reduce_rows add+max and scan_rows add over f32[8192,8192]; "
                         "inclusive scan over i32[2^28]")
+    if name == "copy":
+        # calibration: one plain copy kernel of known size (1 GiB read, 1 GiB written)
+        from cudacaml_amd import dsl as Dsl
+        from cudacaml_amd.ir import Graph
+
+        x = device_inputs(H, C.gen_uniform_pm1((1 << 28,)), 1)
+        add(Graph.create("copy", [("r", Dsl.map(lambda e: e, Dsl.param("x", F32, (1 << 28,))))]), [("x", x)])
+        return Workload(name, progs, "GB/s", "f32", "calibration: copy of f32[2^28]")
     if name in ("saxpy", "chain"):
         x = device_inputs(H, C.gen_uniform_pm1((C.N1,)), 1)
         if name == "saxpy":
@@ -166,8 +174,8 @@ def cpu_baseline(name, C, H=None):
     import oracle
 
     if name == "rows":
-        r = 4096
-        n = 1 << 27
+        r = C.ROWS2
+        n = C.SCAN2
         if H is not None:
             x = H.download(device_inputs(H, C.gen_uniform_pm1((r, C.ROWS2)), 3))
             v = H.download(device_inputs(H, C.gen_small_ints((n,)), 4))
@@ -181,8 +189,118 @@ def cpu_baseline(name, C, H=None):
         oracle.Interp.run(c2, [("v", v)])
         dt = time.perf_counter() - t0
         nbytes = 3 * x.nbytes + 2 * r * 4 + x.nbytes + 2 * v.nbytes
-        return nbytes / dt / 1e9, "GB/s", "rows graph on f32[4096,8192] + global scan on i32[2^27]", dt
+        return nbytes / dt / 1e9, "GB/s", "the whole workload: rows graph on f32[8192,8192] + global scan on i32[2^28]", dt
     raise SystemExit("no CPU baseline for %s" % name)
+
+
+def pmc_child(args):
+    """Child of a counter pass: the workload's warm-up and steps, then the
+    copy calibration kernel; prints the two kernel names as JSON."""
+    from cudacaml_amd import backend_hip as H
+    from cudacaml_amd.examples import configs as C
+
+    w = build_workload(args.config, H, C)
+    dom = dominant(H, w, args.config)[0]
+    cal = build_workload("copy", H, C)
+    copy_name = list(plan_bytes(H, cal.programs[0][0]))[0]
+    for _ in range(1 + args.steps):
+        step(H, w)
+    for _ in range(2):
+        step(H, cal)
+    from cudacaml_amd.runtime import Device
+
+    Device.synchronize()
+    print(json.dumps({"dom": dom, "copy": copy_name}), flush=True)
+
+
+COPY_BYTES = (1 << 28) * 4  # read once and written once by the calibration kernel
+
+
+def measure_traffic(config, steps=2):
+    """HBM bytes per launch of the dominant kernel from two rocprofv3 counter
+    passes (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by
+    what the same counter reads for a plain copy kernel of known size. Runs
+    as child processes, before this process touches the GPU. Returns
+    (traffic_bytes, detail) or (None, reason)."""
+    import csv
+    import glob
+    import shutil
+    import statistics
+    import subprocess
+    import tempfile
+
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        return None, "rocprofv3 not found"
+    vals = {}
+    names = None
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        out = tempfile.mkdtemp(prefix="cchip_pmc_", dir="/tmp")
+        cmd = [exe, "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "p", "--",
+               sys.executable, os.path.abspath(__file__), "--config", config, "--steps", str(steps),
+               "--pmc-child"]
+        env = dict(os.environ, TMPDIR="/tmp")
+        log("traffic: %s pass" % counter)
+        try:
+            r = subprocess.run(cmd, cwd="/tmp", env=env, stdout=subprocess.PIPE, stderr=subprocess.PIPE,
+                               timeout=180, start_new_session=True)
+        except subprocess.TimeoutExpired:
+            return None, "rocprofv3 %s pass timed out" % counter
+        lines = [l for l in r.stdout.decode(errors="replace").splitlines() if l.startswith("{")]
+        if r.returncode != 0 or not lines:
+            return None, "rocprofv3 %s pass failed (rc %d)" % (counter, r.returncode)
+        names = json.loads(lines[-1])
+        files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
+        if not files:
+            return None, "no counter file from the %s pass" % counter
+        per = {"dom": [], "copy": []}
+        with open(files[0]) as f:
+            for row in csv.DictReader(f):
+                if row["Counter_Name"] != counter:
+                    continue
+                for key in per:
+                    if row["Kernel_Name"] == names[key]:
+                        per[key].append(float(row["Counter_Value"]))
+        shutil.rmtree(out, ignore_errors=True)
+        if not per["dom"] or not per["copy"]:
+            return None, "kernel rows missing from the %s pass" % counter
+        vals[counter] = (statistics.median(per["dom"]), statistics.median(per["copy"]))
+    fetch_scale = COPY_BYTES / (vals["FETCH_SIZE"][1] * 1024)
+    write_scale = COPY_BYTES / (vals["WRITE_SIZE"][1] * 1024)
+    fetch = vals["FETCH_SIZE"][0] * 1024 * fetch_scale
+    write = vals["WRITE_SIZE"][0] * 1024 * write_scale
+    detail = {"kernel": names["dom"], "fetch_kib": vals["FETCH_SIZE"][0], "write_kib": vals["WRITE_SIZE"][0],
+              "fetch_scale": round(fetch_scale, 4), "write_scale": round(write_scale, 4),
+              "fetch_bytes": int(fetch), "write_bytes": int(write)}
+    return int(fetch + write), detail
+
+
+def dominant(H, w, config):
+    """The kernel with the most algorithmic bytes (the matmul, for flops):
+    (name, role, bytes, compiled) plus every kernel's (role, bytes)."""
+    kinfo = {}
+    for g, c, _, _ in w.programs:
+        for k, (role, b) in plan_bytes(H, g).items():
+            kinfo[k] = (role, b, c)
+    dom = max(kinfo.items(), key=lambda kv: kv[1][1])[0]
+    if config.startswith("matmul"):
+        dom = [k for k, v in kinfo.items() if v[0].startswith("matmul")][0]
+    return (dom,) + kinfo[dom] + (kinfo,)
+
+
+def whole_run_ms(H, w, reps=3):
+    """Median time of a synchronous run from host arrays: upload, launches,
+    download (pageable host memory, as Executor.run)."""
+    import statistics
+
+    hosts = [(c, [(n, H.download(r)) for n, r in ins]) for _, c, ins, _ in w.programs]
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        for c, ins in hosts:
+            H.run(c, ins)
+        ts.append((time.perf_counter() - t0) * 1e3)
+    return statistics.median(ts)
 
 
 def main():
@@ -191,12 +309,27 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="rows")
-    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
+    ap.add_argument("--no-whole-run", action="store_true", help="skip the host-to-host run timing")
+    ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this backend runs on one GPU; multi-GPU runs (Multi) are out of scope. Use --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
+    if args.pmc_child:
+        pmc_child(args)
+        return
+    # Counter passes first: they are child processes, started before this
+    # process initialises the GPU.
+    traffic, traffic_detail = (None, "skipped (--no-traffic)")
+    if not args.no_traffic:
+        traffic, traffic_detail = measure_traffic(args.config)
+        log("traffic:", traffic, traffic_detail)
+
+    import statistics
+
     from cudacaml_amd import backend_hip as H
     from cudacaml_amd.examples import configs as C
     from cudacaml_amd.runtime import Device
@@ -209,16 +342,7 @@ def main():
     w = build_workload(args.config, H, C)
     log("compiled and generated inputs in %.1fs" % (time.perf_counter() - t0))
 
-    # Per-kernel algorithmic bytes; the dominant kernel is the one with the
-    # most bytes (or the matmul, for flops).
-    kinfo = {}
-    for g, c, _, _ in w.programs:
-        for k, (role, b) in plan_bytes(H, g).items():
-            kinfo[k] = (role, b, c)
-    dom = max(kinfo.items(), key=lambda kv: kv[1][1])[0]
-    if args.config.startswith("matmul"):
-        dom = [k for k, v in kinfo.items() if v[0].startswith("matmul")][0]
-    dom_role, dom_bytes, dom_c = kinfo[dom]
+    dom, dom_role, dom_bytes, dom_c, kinfo = dominant(H, w, args.config)
 
     for _ in range(args.warmup):
         step(H, w)
@@ -230,7 +354,7 @@ def main():
         step(H, w)
     Device.synchronize()
     elapsed = time.perf_counter() - t0
-    launches, dom_ms = H.timing(dom_c)
+    each = H.timing_each(dom_c)
     H.time_kernel(dom_c, None)
     step(H, w, sync=True)  # surfaces any device-side error of the timed runs
 
@@ -247,7 +371,7 @@ def main():
         value = flops * args.steps / elapsed / 1e12
     else:
         value = C.PATHS5 * args.steps / elapsed
-    dom_avg_ms = dom_ms / max(1, launches)
+    dom_avg_ms = sum(each) / max(1, len(each))
     if w.unit == "TFLOP/s":
         g = w.programs[0][0]
         mm = [t for t in g.order if t.kind == "matmul"][0]
@@ -255,21 +379,31 @@ def main():
         peak = FP64_MFMA_TFLOPS if w.dtype == "f64" else FP32_MFMA_TFLOPS
         achieved = fl / (dom_avg_ms * 1e-3) / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
-                "frac": round(achieved / peak, 4), "traffic": None}
+                "frac": round(achieved / peak, 4), "traffic": traffic, "flops_per_launch": fl}
     else:
         achieved = dom_bytes / (dom_avg_ms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None}
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic}
     roof["kernel"] = dom
     roof["template"] = dom_role
-    roof["launch_ms"] = round(dom_avg_ms, 4)
     roof["algorithmic_bytes"] = dom_bytes
+    roof["launches"] = len(each)
+    roof["launch_ms"] = round(dom_avg_ms, 4)
+    if each:
+        roof["launch_ms_best"] = round(min(each), 4)
+        roof["launch_ms_median"] = round(statistics.median(each), 4)
+    roof["traffic_detail"] = traffic_detail
+
+    whole = None
+    if not args.no_whole_run:
+        whole = {"ms": round(whole_run_ms(H, w), 2),
+                 "what": "host arrays in, host arrays out: upload + kernels + download, pageable memory"}
 
     cpu = None
     if not args.no_cpu and args.config == "rows":
         v, unit, sample, secs = cpu_baseline(args.config, C, H)
         cpu = {"value": round(v, 3), "unit": unit, "cores": 1, "kind": "port",
-               "sample": sample + " (%.1fs, C restatement of the OCaml interpreter)" % secs}
+               "sample": sample + " (%.1fs, C restatement of the OCaml interpreter, one thread)" % secs}
 
     line = {
         "metric": "HBM GB/s & % peak (fused map/reduce/scan); matmul TFLOP/s; MC paths/s",
@@ -287,6 +421,7 @@ def main():
         "config": {"workload": w.describe, "parallelism": "single GPU", "algorithmic_bytes_per_step": total_bytes},
         "roofline": roof,
         "cpu_baseline": cpu,
+        "whole_run": whole,
     }
     print(json.dumps(line), flush=True)
 

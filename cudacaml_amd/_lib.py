@@ -85,6 +85,7 @@ SIGNATURES = {
     "cchip_program_stream": (c_int, [c_vp, c_int, P(c_vp)]),
     "cchip_program_time_kernel": (c_int, [c_vp, c_cp]),
     "cchip_program_timing": (c_int, [c_vp, P(c_int), P(ctypes.c_double)]),
+    "cchip_program_timing_each": (c_int, [c_vp, c_int, P(ctypes.c_double), P(c_int), P(ctypes.c_double)]),
 }
 
 _lib = None

@@ -318,4 +318,14 @@ def timing(c):
     return n.value, ms.value
 
 
+def timing_each(c, capacity=4096):
+    """Per-launch milliseconds of the timed kernel since the last read, in
+    launch order."""
+    buf = (ctypes.c_double * capacity)()
+    n = ctypes.c_int()
+    ms = ctypes.c_double()
+    check(lib().cchip_program_timing_each(c.handle, capacity, buf, ctypes.byref(n), ctypes.byref(ms)))
+    return list(buf[:min(n.value, capacity)])
+
+
 available = Device.available

@@ -454,22 +454,29 @@ int cchip_program_time_kernel(cchip_program *p, const char *name) {
   });
 }
 
-int cchip_program_timing(cchip_program *p, int *launches, double *total_ms) {
+int cchip_program_timing_each(cchip_program *p, int capacity, double *each_ms, int *launches, double *total_ms) {
   return guarded([&] {
     std::lock_guard<std::mutex> lk(p->mu);
     DeviceGuard dg(p->device);
     double tot = 0;
+    int i = 0;
     for (auto &e : p->ev_used) {
       check_hip(hipEventSynchronize(e.second), "hipEventSynchronize");
       float ms = 0;
       check_hip(hipEventElapsedTime(&ms, e.first, e.second), "hipEventElapsedTime");
       tot += ms;
+      if (each_ms && i < capacity) each_ms[i] = ms;
+      i++;
     }
     *launches = (int)p->ev_used.size();
     *total_ms = tot;
     for (auto &e : p->ev_used) p->ev_free.push_back(e);
     p->ev_used.clear();
   });
+}
+
+int cchip_program_timing(cchip_program *p, int *launches, double *total_ms) {
+  return cchip_program_timing_each(p, 0, nullptr, launches, total_ms);
 }
 
 }  // extern "C"

@@ -106,6 +106,10 @@ int cchip_program_stream(const cchip_program *program, int lane, void **stream);
    device time. Synchronise the stream before reading. */
 int cchip_program_time_kernel(cchip_program *program, const char *name);
 int cchip_program_timing(cchip_program *program, int *launches, double *total_ms);
+/* As cchip_program_timing, also writing the first `capacity` per-launch
+   durations (ms, launch order) to `each_ms`. */
+int cchip_program_timing_each(cchip_program *program, int capacity, double *each_ms, int *launches,
+                              double *total_ms);
 
 #ifdef __cplusplus
 }
