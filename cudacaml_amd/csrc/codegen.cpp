@@ -505,6 +505,18 @@ const char *kPrelude = R"PRELUDE(// Generated by cchip (Backend_hip) for gfx950.
 typedef unsigned int cc_u32;
 typedef unsigned long long cc_u64;
 template <typename T> struct __attribute__((aligned(4 * sizeof(T)))) cc_v4 { T x, y, z, w; };
+// Streaming (non-temporal) 4-wide accesses: they do not displace the lines
+// that random-access loads of the same kernel reuse.
+template <typename T> __device__ __forceinline__ cc_v4<T> cc_ld4_nt(const T* p) {
+  typedef T v4 __attribute__((ext_vector_type(4)));
+  const v4 v = __builtin_nontemporal_load((const v4*)p);
+  return {v.x, v.y, v.z, v.w};
+}
+template <typename T> __device__ __forceinline__ void cc_st4_nt(T* p, const cc_v4<T>& r) {
+  typedef T v4 __attribute__((ext_vector_type(4)));
+  const v4 v = {r.x, r.y, r.z, r.w};
+  __builtin_nontemporal_store(v, (v4*)p);
+}
 template <typename T> struct __attribute__((aligned(2 * sizeof(T)))) cc_v2 { T x, y; };
 
 // Float.min / Float.max of OCaml: NaN if either operand is NaN, -0 below
@@ -535,6 +547,56 @@ __device__ __forceinline__ void cc_flag(int* err, int code) {
 __device__ __forceinline__ void cc_atomic_add(float* p, float v) { unsafeAtomicAdd(p, v); }
 __device__ __forceinline__ void cc_atomic_add(double* p, double v) { unsafeAtomicAdd(p, v); }
 __device__ __forceinline__ void cc_atomic_add(int* p, int v) { atomicAdd(p, v); }
+// LDS accumulation. The native float LDS atomic add runs about four times
+// slower than a compare-and-swap loop on gfx950, so floats use the loop;
+// every round at least one contending lane succeeds, so it terminates.
+__device__ __forceinline__ void cc_lds_add(int* p, int v) {
+  __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void cc_lds_add(float* p, float v) {
+  unsigned* const q = (unsigned*)p;
+  unsigned seen = *q;
+  while (true) {
+    unsigned cur = seen;
+    if (__hip_atomic_compare_exchange_strong(q, &cur, __float_as_uint(__uint_as_float(seen) + v), __ATOMIC_RELAXED,
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) break;
+    seen = cur;
+  }
+}
+__device__ __forceinline__ void cc_lds_add(double* p, double v) {
+  unsigned long long* const q = (unsigned long long*)p;
+  unsigned long long seen = *q;
+  while (true) {
+    unsigned long long cur = seen;
+    if (__hip_atomic_compare_exchange_strong(q, &cur,
+                                             (unsigned long long)__double_as_longlong(__longlong_as_double((long long)seen) + v),
+                                             __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) break;
+    seen = cur;
+  }
+}
+// Exclusive prefix of v over a 256-thread workgroup; *total gets the sum.
+// ws: 4 ints of LDS. Every thread of the workgroup must call it.
+__device__ __forceinline__ int cc_wg_exscan(int v, int* ws, int* total) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  int incl = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(incl, off);
+    if (lane >= off) incl += o;
+  }
+  if (lane == 63) ws[wv] = incl;
+  __syncthreads();
+  int base = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < 4; w++) {
+    const int t = ws[w];
+    if (w < wv) base += t;
+    tot += t;
+  }
+  *total = tot;
+  __syncthreads();
+  return base + incl - v;
+}
 __device__ __forceinline__ cc_u64 cc_bits(float v) { return (cc_u64)__float_as_uint(v); }
 __device__ __forceinline__ cc_u64 cc_bits(int v) { return (cc_u64)(cc_u32)v; }
 __device__ __forceinline__ cc_u64 cc_bits(double v) { return (cc_u64)__double_as_longlong(v); }
@@ -677,11 +739,16 @@ struct Lowering {
 
   // Loads of the identity-indexed buffers of `f` as 4-wide vectors at `i`.
   static std::string vec_loads(const ElemFn &f, const std::string &i, const std::string &indent,
-                               const std::function<std::string(int)> &tyof) {
+                               const std::function<std::string(int)> &tyof, bool nt = false) {
     std::string s;
-    for (int b : f.ident)
-      s += indent + "const cc_v4<" + tyof(b) + "> l" + std::to_string(b) + " = *(const cc_v4<" + tyof(b) +
-           ">*)(b" + std::to_string(b) + " + " + i + ");\n";
+    for (int b : f.ident) {
+      std::string bb = "b" + std::to_string(b);
+      if (nt)
+        s += indent + "const cc_v4<" + tyof(b) + "> l" + std::to_string(b) + " = cc_ld4_nt(" + bb + " + " + i + ");\n";
+      else
+        s += indent + "const cc_v4<" + tyof(b) + "> l" + std::to_string(b) + " = *(const cc_v4<" + tyof(b) + ">*)(" +
+             bb + " + " + i + ");\n";
+    }
     return s;
   }
 
@@ -710,16 +777,26 @@ struct Lowering {
     int64_t N = n.numel;
     if (N == 0) return {};
     std::string T = dt_ctype(n.dt);
+    // Non-temporal streaming accesses when the kernel also gathers (mode 1),
+    // always (2) or never (0).
+    int64_t nt_mode = tune("map_nt", 1);
+    bool nt = nt_mode == 2 || (nt_mode == 1 && !f.ptrs.empty());
+    if (n.dt == DT::BOOL) nt = false;
+    for (int b : f.ident) nt = nt && prog.bufs[b].dt != DT::BOOL;
     std::ostringstream k;
     k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
       << "  const int stride = gridDim.x * 256;\n"
       << "  const int nvec = " << N / 4 << ";\n"
       << "  for (int v = blockIdx.x * 256 + threadIdx.x; v < nvec; v += stride) {\n"
       << "    const int i = v * 4;\n"
-      << vec_loads(f, "i", "    ", tyof()) << "    cc_v4<" << T << "> r;\n";
+      << vec_loads(f, "i", "    ", tyof(), nt) << "    cc_v4<" << T << "> r;\n";
     static const char *comp[] = {"x", "y", "z", "w"};
     for (int u = 0; u < 4; u++) k << "    r." << comp[u] << " = " << lane_call(f, "i", u) << ";\n";
-    k << "    *(cc_v4<" << T << ">*)(b" << out << " + i) = r;\n"
+    if (nt)
+      k << "    cc_st4_nt(b" << out << " + i, r);\n";
+    else
+      k << "    *(cc_v4<" << T << ">*)(b" << out << " + i) = r;\n";
+    k
       << "  }\n"
       << "  for (int i = nvec * 4 + blockIdx.x * 256 + threadIdx.x; i < " << N << "; i += stride)\n"
       << "    b" << out << "[i] = " << f.call_scalar("i") << ";\n"
@@ -1316,6 +1393,347 @@ struct Lowering {
   }
 
   // ---- Scatter_add root (K9 zero fill + K10 atomics) ---------------------
+  // ---- Scatter_add without global atomics -----------------------------------
+  // Device-wide atomics run at roughly one per clock per XCD whatever the
+  // table size, so collisions are resolved in LDS instead. The bins are cut
+  // into P slices of S bins (S a power of two, S * sizeof(T) <= 64 KiB):
+  //   count     chunk g counts its elements per slice      -> cnt[g][p]
+  //   colscan   cnt[g][p] becomes the offset of chunk g within slice p,
+  //             start[p] the slice's total
+  //   bscan     start[] becomes the exclusive prefix of the totals
+  //   partition chunk g writes (bin within slice, value) pairs into slice
+  //             order at start[p] + cnt[g][p] + (rank within the chunk)
+  //   accumulate W workgroups per slice fold the slice's pairs into an LDS
+  //             table with LDS atomics and store it (W = 1) or a partial
+  //   reduce    out[b] = sum over w of the partials, w ascending
+  // With one slice (B <= 4096) the partition is skipped and the workgroups
+  // fold contiguous input chunks directly. Out-of-range indices are skipped
+  // and flag error 2, as the atomic path does. Within a slice the order of
+  // the additions depends on LDS atomic order, so float sums are not
+  // bit-reproducible (the atomic path's are not either).
+  std::vector<int> lower_scatter_lds(int t, int64_t B, int64_t N, int64_t S, int64_t P) {
+    const TNode &n = g.ts[t];
+    std::string id = std::to_string(n.id);
+    std::string kname = "k_" + id;
+    std::string T = dt_ctype(n.dt);
+    const int64_t ES = dt_size(n.dt);
+    int out = buf_of[t];
+    int shift = 0;
+    while ((int64_t(1) << shift) < S) shift++;
+    ElemFn fi = gen.element_fn("fi_" + id, n.a, false, false);
+    ElemFn fs = gen.element_fn("fs_" + id, n.b, false, false);
+    src << fi.code << fs.code;
+    std::string acc = n.dt == DT::I32 ? "cc_u32" : T;  // partial sums wrap for i32
+    std::vector<int> ks;
+    // Loop over [lo, hi) four strides at a time, loads issued first. The
+    // clamped index keeps every load in range.
+    auto chunk_loop = [&](bool with_val, const std::string &body) {
+      std::ostringstream l;
+      l << "  for (int i0 = lo + (int)threadIdx.x; i0 < hi; i0 += 1024) {\n"
+        << "    int jj[4];\n";
+      if (with_val) l << "    " << T << " xx[4];\n";
+      l << "#pragma unroll\n"
+        << "    for (int u = 0; u < 4; u++) {\n"
+        << "      const int i = i0 + u * 256 < hi ? i0 + u * 256 : lo;\n"
+        << "      jj[u] = " << fi.call_scalar("i") << ";\n";
+      if (with_val) l << "      xx[u] = " << fs.call_scalar("i") << ";\n";
+      l << "    }\n"
+        << "#pragma unroll\n"
+        << "    for (int u = 0; u < 4; u++) {\n"
+        << "      if (i0 + u * 256 >= hi) break;\n"
+        << "      const int j = jj[u];\n"
+        << body << "    }\n"
+        << "  }\n";
+      return l.str();
+    };
+    auto finish = [&](int64_t W, int64_t nslices, int64_t part_bins) {
+      // partial tables, then the fixed-order sum
+      if (W == 1) return -1;
+      int part = add_buf("t" + id + "_part", n.dt, W * part_bins, BufRole::Scratch);
+      (void)nslices;
+      return part;
+    };
+    if (P == 1) {
+      // One slice: fold input chunks straight into LDS.
+      int64_t W = std::min<int64_t>(tune("scatter_direct_wgs", 1024), cdiv(N, 8192));
+      W = std::max<int64_t>(1, W);
+      int64_t C = cdiv(cdiv(N, W), 256) * 256;
+      W = cdiv(N, C);
+      int part = finish(W, 1, B);
+      Params p;
+      add_in(p, fi);
+      add_in(p, fs);
+      p.out.push_back(part >= 0 ? part : out);
+      p.err = true;
+      std::vector<int> args;
+      std::string params = param_list(p, args);
+      int dst = part >= 0 ? part : out;
+      std::ostringstream k;
+      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_direct(" << params << ") {\n"
+        << "  __shared__ " << T << " h[" << B << "];\n"
+        << "  for (int b = threadIdx.x; b < " << B << "; b += 256) h[b] = " << zero_of(n.dt) << ";\n"
+        << "  __syncthreads();\n"
+        << "  const int lo = blockIdx.x * " << C << ";\n"
+        << "  const int hi = lo + " << C << " < " << N << " ? lo + " << C << " : " << N << ";\n"
+        << chunk_loop(true, "      if ((unsigned)j < " + std::to_string(B) + "u) cc_lds_add(&h[j], xx[u]); else cc_flag(err, 2);\n")
+        << "  __syncthreads();\n"
+        << "  for (int b = threadIdx.x; b < " << B << "; b += 256) b" << dst << "[(size_t)blockIdx.x * " << B
+        << " + b] = h[b];\n"
+        << "}\n";
+      src << k.str();
+      ks.push_back(add_kernel(kname + "_direct", args, (int)W, 256, "scatter_direct"));
+      if (part >= 0) ks.push_back(scatter_reduce(kname, T, acc, part, out, W, B, B));
+      return ks;
+    }
+    int64_t G = std::min<int64_t>(tune("scatter_chunks", 1024), cdiv(N, 4096));
+    G = std::max<int64_t>(1, G);
+    int64_t C = cdiv(cdiv(N, G), 256) * 256;
+    G = cdiv(N, C);
+    int64_t W = std::max<int64_t>(1, std::min<int64_t>(16, tune("scatter_slice_wgs", 2048) / P));
+    while (W > 1 && W * P * S * ES > (int64_t(256) << 20)) W--;
+    int cnt = add_buf("t" + id + "_cnt", DT::I32, G * P, BufRole::Scratch);
+    int start = add_buf("t" + id + "_start", DT::I32, P + 1, BufRole::Scratch);
+    int key = add_buf("t" + id + "_key", DT::I32, cdiv(N, 2), BufRole::Scratch);  // 16-bit keys
+    int val = add_buf("t" + id + "_val", n.dt, N, BufRole::Scratch);
+    int part = finish(W, P, P * S);
+    std::string sS = std::to_string(S), sB = std::to_string(B), sP = std::to_string(P);
+    std::string bounds = "(unsigned)j < " + sB + "u";
+    auto bounds_of = [&](const std::string &v) { return "(unsigned)" + v + " < " + sB + "u"; };
+    {  // count
+      Params p;
+      add_in(p, fi);
+      p.out.push_back(cnt);
+      std::vector<int> args;
+      std::string params = param_list(p, args);
+      std::ostringstream k;
+      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_count(" << params << ") {\n"
+        << "  __shared__ int lc[" << P << "];\n"
+        << "  for (int q = threadIdx.x; q < " << P << "; q += 256) lc[q] = 0;\n"
+        << "  __syncthreads();\n"
+        << "  const int lo = blockIdx.x * " << C << ";\n"
+        << "  const int hi = lo + " << C << " < " << N << " ? lo + " << C << " : " << N << ";\n"
+        << chunk_loop(false, "      if (" + bounds + ") cc_lds_add(&lc[j >> " + std::to_string(shift) + "], 1);\n")
+        << "  __syncthreads();\n"
+        << "  for (int q = threadIdx.x; q < " << P << "; q += 256) b" << cnt << "[(size_t)blockIdx.x * " << P
+        << " + q] = lc[q];\n"
+        << "}\n";
+      src << k.str();
+      ks.push_back(add_kernel(kname + "_count", args, (int)G, 256, "scatter_count"));
+    }
+    {  // colscan: per slice, running offsets over the chunks
+      std::ostringstream k;
+      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_colscan(int* __restrict__ b" << cnt
+        << ", int* __restrict__ b" << start << ") {\n"
+        << "  const int q = blockIdx.x * 256 + threadIdx.x;\n"
+        << "  if (q >= " << P << ") return;\n"
+        << "  int run = 0;\n"
+        << "  for (int c = 0; c < " << G << "; c++) {\n"
+        << "    const int v = b" << cnt << "[(size_t)c * " << P << " + q];\n"
+        << "    b" << cnt << "[(size_t)c * " << P << " + q] = run;\n"
+        << "    run += v;\n"
+        << "  }\n"
+        << "  b" << start << "[q] = run;\n"
+        << "}\n";
+      src << k.str();
+      ks.push_back(add_kernel(kname + "_colscan", {cnt, start}, (int)cdiv(P, 256), 256, "scatter_colscan"));
+    }
+    {  // bscan: one workgroup, exclusive prefix of the slice totals
+      int64_t per = cdiv(P, 256);
+      std::ostringstream k;
+      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_bscan(int* __restrict__ b" << start
+        << ") {\n"
+        << "  __shared__ int ps[257];\n"
+        << "  const int lo = threadIdx.x * " << per << ";\n"
+        << "  int s = 0;\n"
+        << "  for (int q = lo; q < lo + " << per << " && q < " << P << "; q++) s += b" << start << "[q];\n"
+        << "  ps[threadIdx.x] = s;\n"
+        << "  __syncthreads();\n"
+        << "  if (threadIdx.x == 0) {\n"
+        << "    int run = 0;\n"
+        << "    for (int w = 0; w < 256; w++) { const int v = ps[w]; ps[w] = run; run += v; }\n"
+        << "    ps[256] = run;\n"
+        << "  }\n"
+        << "  __syncthreads();\n"
+        << "  int run = ps[threadIdx.x];\n"
+        << "  for (int q = lo; q < lo + " << per << " && q < " << P << "; q++) { const int v = b" << start
+        << "[q]; b" << start << "[q] = run; run += v; }\n"
+        << "  if (threadIdx.x == 0) b" << start << "[" << P << "] = ps[256];\n"
+        << "}\n";
+      src << k.str();
+      ks.push_back(add_kernel(kname + "_bscan", {start}, 1, 256, "scatter_bscan"));
+    }
+    const int64_t STAGE_P = tune("scatter_stage_p", 512), TILE = 4096, E = TILE / 256;
+    if (P <= STAGE_P) {  // partition, staged: each 4096-element tile is grouped by slice in LDS
+      Params p;
+      add_in(p, fi);
+      add_in(p, fs);
+      for (int b : {cnt, start}) p.in.push_back(b);
+      p.out.push_back(key);
+      p.out.push_back(val);
+      p.err = true;
+      std::vector<int> args;
+      std::string params = param_list(p, args);
+      int64_t PP = cdiv(P, 256);
+      std::string sh = std::to_string(shift);
+      std::ostringstream k;
+      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_partition(" << params << ") {\n"
+        << "  __shared__ int cur[" << P << "];\n"
+        << "  __shared__ int tc[" << P + 1 << "];\n"
+        << "  __shared__ int sj[" << TILE << "];\n"
+        << "  __shared__ " << T << " sx[" << TILE << "];\n"
+        << "  __shared__ int ws[4];\n"
+        << "  for (int q = threadIdx.x; q < " << P << "; q += 256) cur[q] = b" << start << "[q] + b" << cnt
+        << "[(size_t)blockIdx.x * " << P << " + q];\n"
+        << "  unsigned short* const keys = (unsigned short*)b" << key << ";\n"
+        << "  const int lo = blockIdx.x * " << C << ";\n"
+        << "  const int hi = lo + " << C << " < " << N << " ? lo + " << C << " : " << N << ";\n"
+        << "  for (int t0 = lo; t0 < hi; t0 += " << TILE << ") {\n"
+        << "    for (int q = threadIdx.x; q < " << P << "; q += 256) tc[q] = 0;\n"
+        << "    int jj[" << E << "], rk[" << E << "];\n"
+        << "    " << T << " xx[" << E << "];\n"
+        << "#pragma unroll\n"
+        << "    for (int u = 0; u < " << E << "; u++) {\n"
+        << "      const int i = t0 + u * 256 + (int)threadIdx.x < hi ? t0 + u * 256 + (int)threadIdx.x : lo;\n"
+        << "      jj[u] = " << fi.call_scalar("i") << ";\n"
+        << "      xx[u] = " << fs.call_scalar("i") << ";\n"
+        << "    }\n"
+        << "    __syncthreads();\n"
+        << "#pragma unroll\n"
+        << "    for (int u = 0; u < " << E << "; u++) {\n"
+        << "      rk[u] = 0;\n"
+        << "      if (t0 + u * 256 + (int)threadIdx.x >= hi) { jj[u] = -1; continue; }\n"
+        << "      if (" << bounds_of("jj[u]") << ") rk[u] = atomicAdd(&tc[jj[u] >> " << sh << "], 1);\n"
+        << "      else { cc_flag(err, 2); jj[u] = -1; }\n"
+        << "    }\n"
+        << "    __syncthreads();\n"
+        << "    {\n"
+        << "      int loc[" << PP << "], s = 0;\n"
+        << "#pragma unroll\n"
+        << "      for (int c = 0; c < " << PP << "; c++) {\n"
+        << "        const int q = threadIdx.x * " << PP << " + c;\n"
+        << "        loc[c] = s;\n"
+        << "        s += q < " << P << " ? tc[q] : 0;\n"
+        << "      }\n"
+        << "      int tot;\n"
+        << "      const int base = cc_wg_exscan(s, ws, &tot);\n"
+        << "#pragma unroll\n"
+        << "      for (int c = 0; c < " << PP << "; c++) {\n"
+        << "        const int q = threadIdx.x * " << PP << " + c;\n"
+        << "        if (q < " << P << ") tc[q] = base + loc[c];\n"
+        << "      }\n"
+        << "      if (threadIdx.x == 0) tc[" << P << "] = tot;\n"
+        << "    }\n"
+        << "    __syncthreads();\n"
+        << "#pragma unroll\n"
+        << "    for (int u = 0; u < " << E << "; u++)\n"
+        << "      if (jj[u] >= 0) {\n"
+        << "        const int slot = tc[jj[u] >> " << sh << "] + rk[u];\n"
+        << "        sj[slot] = jj[u];\n"
+        << "        sx[slot] = xx[u];\n"
+        << "      }\n"
+        << "    __syncthreads();\n"
+        << "    for (int s = threadIdx.x; s < tc[" << P << "]; s += 256) {\n"
+        << "      const int j = sj[s], q = j >> " << sh << ";\n"
+        << "      const int pos = cur[q] + (s - tc[q]);\n"
+        << "      keys[pos] = (unsigned short)(j & " << S - 1 << ");\n"
+        << "      b" << val << "[pos] = sx[s];\n"
+        << "    }\n"
+        << "    __syncthreads();\n"
+        << "    for (int q = threadIdx.x; q < " << P << "; q += 256) cur[q] += tc[q + 1] - tc[q];\n"
+        << "    __syncthreads();\n"
+        << "  }\n"
+        << "}\n";
+      src << k.str();
+      ks.push_back(add_kernel(kname + "_partition", args, (int)G, 256, "scatter_partition"));
+    } else {  // partition
+      Params p;
+      add_in(p, fi);
+      add_in(p, fs);
+      for (int b : {cnt, start}) p.in.push_back(b);
+      p.out.push_back(key);
+      p.out.push_back(val);
+      p.err = true;
+      std::vector<int> args;
+      std::string params = param_list(p, args);
+      std::ostringstream k;
+      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_partition(" << params << ") {\n"
+        << "  __shared__ int cur[" << P << "];\n"
+        << "  for (int q = threadIdx.x; q < " << P << "; q += 256) cur[q] = b" << start << "[q] + b" << cnt
+        << "[(size_t)blockIdx.x * " << P << " + q];\n"
+        << "  __syncthreads();\n"
+        << "  unsigned short* const keys = (unsigned short*)b" << key << ";\n"
+        << "  const int lo = blockIdx.x * " << C << ";\n"
+        << "  const int hi = lo + " << C << " < " << N << " ? lo + " << C << " : " << N << ";\n"
+        << chunk_loop(true, "      if (" + bounds + ") {\n"
+                            "        const int pos = atomicAdd(&cur[j >> " + std::to_string(shift) + "], 1);\n"
+                            "        keys[pos] = (unsigned short)(j & " + std::to_string(S - 1) + ");\n"
+                            "        b" + std::to_string(val) + "[pos] = xx[u];\n"
+                            "      } else cc_flag(err, 2);\n")
+        << "}\n";
+      src << k.str();
+      ks.push_back(add_kernel(kname + "_partition", args, (int)G, 256, "scatter_partition"));
+    }
+    {  // accumulate
+      int dst = part >= 0 ? part : out;
+      std::ostringstream k;
+      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_accumulate(const int* __restrict__ b"
+        << start << ", const int* __restrict__ b" << key << ", const " << T << "* __restrict__ b" << val << ", " << T
+        << "* __restrict__ b" << dst << ") {\n"
+        << "  __shared__ " << T << " h[" << S << "];\n"
+        << "  const int q = blockIdx.x / " << W << ", w = blockIdx.x % " << W << ";\n"
+        << "  for (int b = threadIdx.x; b < " << S << "; b += 256) h[b] = " << zero_of(n.dt) << ";\n"
+        << "  __syncthreads();\n"
+        << "  const int s0 = b" << start << "[q], len = b" << start << "[q + 1] - s0;\n"
+        << "  const int lo = s0 + (int)((long long)len * w / " << W << ");\n"
+        << "  const int hi = s0 + (int)((long long)len * (w + 1) / " << W << ");\n"
+        << "  const unsigned short* const keys = (const unsigned short*)b" << key << ";\n"
+        << "  for (int i0 = lo + (int)threadIdx.x; i0 < hi; i0 += 1024) {\n"
+        << "    int kk[4];\n"
+        << "    " << T << " xx[4];\n"
+        << "#pragma unroll\n"
+        << "    for (int u = 0; u < 4; u++) {\n"
+        << "      const int i = i0 + u * 256 < hi ? i0 + u * 256 : lo;\n"
+        << "      kk[u] = keys[i];\n"
+        << "      xx[u] = b" << val << "[i];\n"
+        << "    }\n"
+        << "#pragma unroll\n"
+        << "    for (int u = 0; u < 4; u++)\n"
+        << "      if (i0 + u * 256 < hi) cc_lds_add(&h[kk[u]], xx[u]);\n"
+        << "  }\n"
+        << "  __syncthreads();\n";
+      if (part >= 0)
+        k << "  for (int b = threadIdx.x; b < " << S << "; b += 256) b" << dst << "[(size_t)w * " << P * S
+          << " + (size_t)q * " << S << " + b] = h[b];\n";
+      else
+        k << "  const int nb = " << B << " - q * " << S << " < " << S << " ? " << B << " - q * " << S << " : " << S
+          << ";\n"
+          << "  for (int b = threadIdx.x; b < nb; b += 256) b" << dst << "[(size_t)q * " << S << " + b] = h[b];\n";
+      k << "}\n";
+      src << k.str();
+      ks.push_back(add_kernel(kname + "_accumulate", {start, key, val, dst}, (int)(P * W), 256, "scatter_accumulate"));
+    }
+    if (part >= 0) ks.push_back(scatter_reduce(kname, T, acc, part, out, W, B, P * S));
+    return ks;
+  }
+
+  // out[b] = sum over w of part[w * stride + b], w ascending.
+  int scatter_reduce(const std::string &kname, const std::string &T, const std::string &acc, int part, int out,
+                     int64_t W, int64_t B, int64_t stride) {
+    std::ostringstream k;
+    k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_reduce(const " << T
+      << "* __restrict__ b" << part << ", " << T << "* __restrict__ b" << out << ") {\n"
+      << "  for (int b = blockIdx.x * 256 + threadIdx.x; b < " << B << "; b += gridDim.x * 256) {\n"
+      << "    " << acc << " s = (" << acc << ")b" << part << "[b];\n"
+      << "    for (int w = 1; w < " << W << "; w++) s += (" << acc << ")b" << part << "[(size_t)w * " << stride
+      << " + b];\n"
+      << "    b" << out << "[b] = (" << T << ")s;\n"
+      << "  }\n"
+      << "}\n";
+    src << k.str();
+    return add_kernel(kname + "_reduce", {part, out}, (int)std::min<int64_t>(cdiv(B, 256), 4096), 256,
+                      "scatter_reduce");
+  }
+
   std::vector<int> lower_scatter(int t) {
     const TNode &n = g.ts[t];
     std::string id = std::to_string(n.id);
@@ -1324,6 +1742,16 @@ struct Lowering {
     int out = buf_of[t];
     int64_t M = n.numel;
     int64_t N = g.ts[n.a].numel;
+    if (M > 0 && N > 0 && tune("scatter_lds", 1)) {
+      const int64_t ES = dt_size(n.dt);
+      int64_t S = 4096;
+      const int64_t want = tune("scatter_slice_bins", 8192);
+      while (S < want && S * 2 * ES <= 65536) S *= 2;
+      while (cdiv(M, S) > 4096 && S * ES < 65536) S *= 2;
+      int64_t P = cdiv(M, S);
+      if (P == 1) return lower_scatter_lds(t, M, N, M, 1);
+      if (P <= 4096) return lower_scatter_lds(t, M, N, S, P);
+    }
     std::vector<int> ks;
     if (M > 0) {
       std::ostringstream z;

@@ -120,14 +120,93 @@ def test_map_ragged(device, n):
     check(g, [("x", data(F32, (n,), 1)), ("y", data(I32, (n,), 2))], [] if n == 0 else ["map"])
 
 
-@pytest.mark.parametrize("dtype", [F32, F64, I32])
-def test_scatter_dtypes(device, dtype):
-    n, bins = 100003, 1000
+def scatter_graph(n, bins, dtype):
     idx = D.param("idx", I32, (n,))
     src = D.param("src", dtype, (n,))
-    g = Graph.create("h", [("h", D.scatter_add(idx, src, (bins,)))])
-    check(g, [("idx", C.bin_indices(3, n, bits=10) % bins), ("src", data(dtype, (n,), 4))],
+    return Graph.create("h", [("h", D.scatter_add(idx, src, (bins,)))])
+
+
+def scatter_idx(seed, n, bins):
+    v = C.philox_w0(seed, n).astype(np.int64) % bins
+    if n >= 2:
+        v[0], v[-1] = 0, bins - 1
+    return v.astype(np.int32)
+
+
+SCATTER_CASES = [
+    # (n, bins, dtype, templates): one slice folded directly (with and
+    # without partials), partitioned slices (with partials, and W = 1 where
+    # each slice's table is stored straight to the output)
+    (100003, 1000, F32, ["scatter_direct", "scatter_reduce"]),
+    (100003, 1000, F64, ["scatter_direct", "scatter_reduce"]),
+    (100003, 1000, I32, ["scatter_direct", "scatter_reduce"]),
+    (5000, 4096, I32, ["scatter_direct"]),
+    (300001, 50000, F32, ["scatter_partition", "scatter_accumulate", "scatter_reduce"]),
+    (300001, 50000, F64, ["scatter_partition", "scatter_accumulate", "scatter_reduce"]),
+    (300001, 50001, I32, ["scatter_partition", "scatter_accumulate", "scatter_reduce"]),
+    (1 << 20, (1 << 24) + 5, F32, ["scatter_partition", "scatter_accumulate"]),
+    (1 << 20, 1 << 24, I32, ["scatter_partition", "scatter_accumulate"]),
+]
+
+
+@pytest.mark.parametrize("n,bins,dtype,tpl", SCATTER_CASES, ids=lambda v: str(v))
+def test_scatter_paths(device, n, bins, dtype, tpl):
+    g = scatter_graph(n, bins, dtype)
+    if "scatter_reduce" not in tpl:
+        assert "scatter_reduce" not in templates(g)
+    check(g, [("idx", scatter_idx(3, n, bins)), ("src", data(dtype, (n,), 4))], tpl)
+
+
+@pytest.mark.parametrize("dtype", [F32, I32])
+def test_scatter_atomic_path(device, dtype, monkeypatch):
+    """The global-atomic template, still used where the slices would not
+    fit (and selectable with scatter_lds=0)."""
+    monkeypatch.setenv("CCHIP_TUNE", "scatter_lds=0")
+    n, bins = 100003, 50000
+    check(scatter_graph(n, bins, dtype), [("idx", scatter_idx(5, n, bins)), ("src", data(dtype, (n,), 6))],
           ["scatter_zero", "scatter_atomic"])
+
+
+@pytest.mark.parametrize("bins", [3000, 70000])
+def test_scatter_one_hot_bin(device, bins):
+    """Every element in one bin: one slice takes all the work."""
+    n = 200000
+    idx = np.full(n, bins // 2, np.int32)
+    check(scatter_graph(n, bins, I32), [("idx", idx), ("src", data(I32, (n,), 7))], [])
+    check(scatter_graph(n, bins, F32), [("idx", idx), ("src", data(F32, (n,), 8))], [])
+
+
+def test_scatter_empty_source(device):
+    check(scatter_graph(0, 10, F32), [("idx", np.zeros(0, np.int32)), ("src", np.zeros(0, np.float32))],
+          ["scatter_zero"])
+
+
+def test_scatter_fused_operands(device):
+    """Index and source are fused expressions, evaluated in both the count
+    and the partition pass."""
+    n, bins = 200000, 30000
+    i = D.param("i", I32, (n,))
+    x = D.param("x", F32, (n,))
+    idx = D.map(lambda e: D.sub(D.const(I32, bins - 1), D.mul(e, D.const(I32, 1))), i)
+    g = Graph.create("h", [("h", D.scatter_add(idx, D.map(D.exp, x), (bins,)))])
+    check(g, [("i", scatter_idx(9, n, bins)), ("x", data(F32, (n,), 10))], ["scatter_partition"])
+
+
+@pytest.mark.parametrize("bins", [4, 50000])
+def test_scatter_partition_out_of_range_raises(device, bins):
+    n = 20000
+    idx = scatter_idx(11, n, bins)
+    idx[777] = bins
+    idx[12345] = -1
+    c = H.compile(scatter_graph(n, bins, I32))
+    try:
+        with pytest.raises(ValueError, match="scatter_add index out of bounds"):
+            H.run(c, [("idx", idx), ("src", np.ones(n, np.int32))])
+        idx[777], idx[12345] = 0, 1
+        got = dict(H.run(c, [("idx", idx), ("src", np.ones(n, np.int32))]))["h"]
+        np.testing.assert_array_equal(got, np.bincount(idx, minlength=bins).astype(np.int32))
+    finally:
+        c.release()
 
 
 def test_gather_out_of_range_raises(device):

@@ -62,9 +62,25 @@ def test_barriers_are_materialised():
     idx, src = D.param("idx", I32, (6,)), D.param("src", F32, (6,))
     s = D.scatter_add(idx, src, (4,))
     bufs, ks, ops = parse(H.plan(Graph.create("h", [("r", D.map(D.neg, s))])))
-    assert [t for _, t in ks] == ["scatter_zero", "scatter_atomic", "map"]
+    assert [t for _, t in ks] == ["scatter_direct", "map"]
     launches = [o[1] for o in ops if o[0] == "launch"]
     assert launches == [k for k, _ in ks]
+
+
+def test_scatter_template_choice(monkeypatch):
+    """One slice (8192 bins by default): direct LDS fold; more: partitioned
+    slices; tables too
+    large for the slice limit (or scatter_lds=0): global atomics."""
+    def ks(n, bins):
+        i, s = D.param("i", I32, (n,)), D.param("s", F32, (n,))
+        return [t for _, t in kernels_of(Graph.create("h", [("h", D.scatter_add(i, s, (bins,)))]))]
+
+    assert ks(1000, 8192) == ["scatter_direct"]
+    assert ks(100000, 8192) == ["scatter_direct", "scatter_reduce"]
+    assert ks(100000, 8193)[:4] == ["scatter_count", "scatter_colscan", "scatter_bscan", "scatter_partition"]
+    assert ks(1 << 22, 1 << 28) == ["scatter_zero", "scatter_atomic"]
+    monkeypatch.setenv("CCHIP_TUNE", "scatter_lds=0")
+    assert ks(1000, 4096) == ["scatter_zero", "scatter_atomic"]
 
 
 def test_matmul_barrier_fuses_operand_maps():
@@ -110,7 +126,11 @@ def test_scan_template_choice(rows, n, tpls):
 
 def test_config_plans():
     assert [t for _, t in kernels_of(C.rows())] == ["reduce_rowseq", "reduce_rowseq", "scan_rowseq"]
-    assert [t for _, t in kernels_of(C.scatter_gather())] == ["scatter_zero", "scatter_atomic", "map"]
+    assert [t for _, t in kernels_of(C.scatter_gather())] == ["scatter_count", "scatter_colscan", "scatter_bscan",
+                                                               "scatter_partition", "scatter_accumulate",
+                                                               "scatter_reduce", "map"]
+    # 2^26 bins: one workgroup per slice stores its table, no partials
+    assert "scatter_reduce" not in [t for _, t in kernels_of(C.scatter_gather(C.N3, C.N3))]
     ks = kernels_of(C.mc_paths())
     assert "scan_rowseq" in [t for _, t in ks]
 
