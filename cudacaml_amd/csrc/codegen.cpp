@@ -646,6 +646,29 @@ int64_t tune(const char *key, int64_t dflt) {
   return dflt;
 }
 
+// Accumulation with an empty flag (`acc`, `has` in scope): x is folded in on
+// the right; the first value is taken as is.
+std::string fold_in(const std::string &cmb, const std::string &T, const std::string &x) {
+  return "{ const " + T + " x_ = " + x + "; acc = has ? " + cmb + "(acc, x_) : x_; has = true; }";
+}
+
+// One butterfly step over (acc, has): the lower lane's value stays on the left.
+std::string xor_combine(const std::string &cmb, const std::string &T, const std::string &off) {
+  return "{ const " + T + " o_ = __shfl_xor(acc, " + off + "); const bool oh_ = __shfl_xor((int)has, " + off +
+         ") != 0; if (oh_) { acc = has ? " + cmb + "(acc, o_) : o_; has = true; } }";
+}
+
+// Look-back fold over lanes (`w`, `hw` in scope; lane 0 is the nearest
+// tile): lanes further away are earlier in the row, so they go on the left.
+std::string lookback_tree(const std::string &cmb, const std::string &T) {
+  std::string r;
+  for (int off = 1; off < 64; off *= 2)
+    r += "        { const " + T + " o = __shfl_down(w, " + std::to_string(off) + "); const bool oh = __shfl_down((int)hw, " +
+         std::to_string(off) + ") != 0;\n          if ((lane & " + std::to_string(2 * off - 1) +
+         ") == 0 && oh) { w = hw ? " + cmb + "(o, w) : o; hw = true; } }\n";
+  return r;
+}
+
 // ---------------------------------------------------------------------------
 // The lowering proper
 // ---------------------------------------------------------------------------
@@ -1001,37 +1024,43 @@ struct Lowering {
         << "  for (int rb = wave * " << rpw << "; rb < " << rows << "; rb += nwaves * " << rpw << ") {\n"
         << "    const int r = rb + seg;\n"
         << "    " << T << " acc = " << ini << "();\n"
+        << "    bool has = false;\n"
         << "    if (r < " << rows << ") {\n"
         << "      for (int j = sl; j < " << len << "; j += " << S << ") {\n"
         << "        const int i = r * " << len << " + j;\n"
-        << "        acc = " << cmb << "(acc, " << f.call_scalar("i") << ");\n"
+        << "        " << fold_in(cmb, T, f.call_scalar("i")) << "\n"
         << "      }\n"
         << "    }\n";
-      for (int64_t off = S / 2; off > 0; off /= 2) k << "    acc = " << cmb << "(acc, __shfl_xor(acc, " << off << "));\n";
-      k << "    if (r < " << rows << " && sl == 0) b" << out << "[r] = acc;\n"
+      for (int64_t off = S / 2; off > 0; off /= 2) k << "    " << xor_combine(cmb, T, std::to_string(off)) << "\n";
+      k << "    if (r < " << rows << " && sl == 0) b" << out << "[r] = has ? " << cmb << "(" << ini << "(), acc) : " << ini
+        << "();\n"
         << "  }\n}\n";
       src << k.str();
       int64_t waves = cdiv(rows, rpw);
       int grid = (int)std::min<int64_t>(cdiv(waves, 4), 16384);
       return {add_kernel(kname, args, grid, 256, "reduce_wave")};
     }
-    std::string block_reduce =
-        "    for (int off = 32; off > 0; off >>= 1) acc = " + cmb +
-        "(acc, __shfl_xor(acc, off));\n"
-        "    if (lane == 0) wpart[wid] = acc;\n"
-        "    __syncthreads();\n";
+    // Accumulators carry an empty flag, so init is applied exactly once, to
+    // the row's total (init is not assumed to be the combine's identity).
+    std::string block_reduce = "    for (int off = 32; off > 0; off >>= 1) " + xor_combine(cmb, T, "off") +
+                               "\n"
+                               "    if (lane == 0) { wpart[wid] = acc; whas[wid] = has; }\n"
+                               "    __syncthreads();\n";
+    std::string wave_parts = "      " + T + " t = " + ini + "();\n      bool th = false;\n"
+                             "      for (int w = 0; w < 4; w++) if (whas[w]) { t = th ? " + cmb +
+                             "(t, wpart[w]) : wpart[w]; th = true; }\n";
     auto fold_loop = [&](const std::string &lo, const std::string &hi) {
       std::ostringstream l;
       if (vec) {
         l << "    for (int j = " << lo << " + threadIdx.x * 4; j < " << hi << "; j += 1024) {\n"
           << "      const int i = base + j;\n"
           << vec_loads(f, "i", "      ", tyof());
-        for (int u = 0; u < 4; u++) l << "      acc = " << cmb << "(acc, " << lane_call(f, "i", u) << ");\n";
+        for (int u = 0; u < 4; u++) l << "      " << fold_in(cmb, T, lane_call(f, "i", u)) << "\n";
         l << "    }\n";
       } else {
         l << "    for (int j = " << lo << " + threadIdx.x; j < " << hi << "; j += 256) {\n"
           << "      const int i = base + j;\n"
-          << "      acc = " << cmb << "(acc, " << f.call_scalar("i") << ");\n"
+          << "      " << fold_in(cmb, T, f.call_scalar("i")) << "\n"
           << "    }\n";
       }
       return l.str();
@@ -1046,16 +1075,15 @@ struct Lowering {
       std::ostringstream k;
       k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
         << "  __shared__ " << T << " wpart[4];\n"
+        << "  __shared__ bool whas[4];\n"
         << "  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;\n"
         << "  for (int r = blockIdx.x; r < " << rows << "; r += gridDim.x) {\n"
         << "    const int base = r * " << len << ";\n"
         << "    " << T << " acc = " << ini << "();\n"
+        << "    bool has = false;\n"
         << fold_loop("0", std::to_string(len)) << block_reduce << "    if (threadIdx.x == 0) {\n"
-        << "      " << T << " t = wpart[0];\n"
-        << "      t = " << cmb << "(t, wpart[1]);\n"
-        << "      t = " << cmb << "(t, wpart[2]);\n"
-        << "      t = " << cmb << "(t, wpart[3]);\n"
-        << "      b" << out << "[r] = t;\n"
+        << wave_parts
+        << "      b" << out << "[r] = th ? " << cmb << "(" << ini << "(), t) : " << ini << "();\n"
         << "    }\n"
         << "    __syncthreads();\n"
         << "  }\n}\n";
@@ -1081,6 +1109,7 @@ struct Lowering {
     std::ostringstream k;
     k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
       << "  __shared__ " << T << " wpart[4];\n"
+      << "  __shared__ bool whas[4];\n"
       << "  __shared__ int s_last;\n"
       << "  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;\n"
       << "  const int r = blockIdx.x / " << G << ";\n"
@@ -1090,11 +1119,9 @@ struct Lowering {
       << "  const int hi = min(lo + " << chunk << ", " << len << ");\n"
       << "  {\n"
       << "    " << T << " acc = " << ini << "();\n"
+      << "    bool has = false;\n"
       << fold_loop("lo", "hi") << block_reduce << "    if (threadIdx.x == 0) {\n"
-      << "      " << T << " t = wpart[0];\n"
-      << "      t = " << cmb << "(t, wpart[1]);\n"
-      << "      t = " << cmb << "(t, wpart[2]);\n"
-      << "      t = " << cmb << "(t, wpart[3]);\n"
+      << wave_parts  // every chunk is non-empty, so th holds
       << "      __hip_atomic_store(&b" << part << "[blockIdx.x], t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
       << "      const int prev = __hip_atomic_fetch_add(&b" << cnt
       << "[r], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);\n"
@@ -1105,15 +1132,13 @@ struct Lowering {
       << "  if (s_last) {\n"
       << "    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, \"agent\");\n"
       << "    " << T << " acc = " << ini << "();\n"
+      << "    bool has = false;\n"
       << "    for (int q = threadIdx.x; q < " << G << "; q += 256)\n"
-      << "      acc = " << cmb << "(acc, __hip_atomic_load(&b" << part << "[r * " << G
-      << " + q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));\n"
+      << "      " << fold_in(cmb, T, "__hip_atomic_load(&b" + std::to_string(part) + "[r * " + std::to_string(G) +
+             " + q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)") << "\n"
       << block_reduce << "    if (threadIdx.x == 0) {\n"
-      << "      " << T << " t = wpart[0];\n"
-      << "      t = " << cmb << "(t, wpart[1]);\n"
-      << "      t = " << cmb << "(t, wpart[2]);\n"
-      << "      t = " << cmb << "(t, wpart[3]);\n"
-      << "      b" << out << "[r] = t;\n"
+      << wave_parts
+      << "      b" << out << "[r] = " << cmb << "(" << ini << "(), t);\n"
       << "      __hip_atomic_store(&b" << cnt << "[r], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
       << "    }\n"
       << "  }\n}\n";
@@ -1285,7 +1310,6 @@ struct Lowering {
     }
     k << "  }\n"
       << "  if (tin == 0 && threadIdx.x == 0) v[0][0] = " << cmb << "(" << ini << "(), v[0][0]);\n"
-      << "  " << T << " ex[" << U << "];\n"
       << "#pragma unroll\n"
       << "  for (int u = 0; u < " << U << "; u++) {\n"
       << "    v[u][1] = " << cmb << "(v[u][0], v[u][1]);\n"
@@ -1295,7 +1319,10 @@ struct Lowering {
     for (int off = 1; off < 64; off *= 2)
       k << "    { const " << T << " o = __shfl_up(incl, " << off << "); if (lane >= " << off << ") incl = " << cmb
         << "(o, incl); }\n";
-    k << "    ex[u] = __shfl_up(incl, 1);\n"
+    // the wave's exclusive prefix is folded in at once (no register per slice kept for it)
+    k << "    { const " << T << " ex = __shfl_up(incl, 1);\n"
+      << "      if (lane > 0) { v[u][0] = " << cmb << "(ex, v[u][0]); v[u][1] = " << cmb << "(ex, v[u][1]);\n"
+      << "                      v[u][2] = " << cmb << "(ex, v[u][2]); v[u][3] = " << cmb << "(ex, v[u][3]); } }\n"
       << "    if (lane == 63) wsum[u][wid] = incl;\n"
       << "  }\n"
       << "  __syncthreads();\n"
@@ -1305,7 +1332,6 @@ struct Lowering {
       << "    bool hp = u > 0;\n"
       << "    " << T << " pf = run;\n"
       << "    for (int w = 0; w < wid; w++) { pf = hp ? " << cmb << "(pf, wsum[u][w]) : wsum[u][w]; hp = true; }\n"
-      << "    if (lane > 0) { pf = hp ? " << cmb << "(pf, ex[u]) : ex[u]; hp = true; }\n"
       << "    if (hp) {\n"
       << "      v[u][0] = " << cmb << "(pf, v[u][0]); v[u][1] = " << cmb << "(pf, v[u][1]);\n"
       << "      v[u][2] = " << cmb << "(pf, v[u][2]); v[u][3] = " << cmb << "(pf, v[u][3]);\n"
@@ -1322,40 +1348,95 @@ struct Lowering {
         << "      bool have = false;\n"
         << "      int j = tile - 1;\n"
         << "      unsigned spins = 0;\n"
-        << "      while (true) {\n"
-        << "        const int q = j - lane;\n"
-        << "        int flag = 2;\n"
-        << "        " << T << " val = " << ini << "();\n"
-        << "        if (q >= rowstart) {\n"
-        << "          while (true) {\n";
+        << "      while (true) {\n";
       if (!wide) {
-        k << "            const cc_u64 w = __hip_atomic_load(&st[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
-          << "            flag = (int)(w >> 32);\n"
-          << "            if (flag != 0) { val = cc_from_bits<" << T << ">(w & 0xffffffffull); break; }\n";
+        // K predecessors per lane (lane l covers tiles j - K*l - k, k = 0..K-1,
+        // position K*l + k counted from the nearest), all loaded in one round
+        // trip. Only words nearer than the nearest inclusive prefix found so
+        // far are waited for. K = 1 measures best on gfx950 (2^28 i32: 475 us
+        // at K = 1, 503 at 2, 601 at 4): the wait is dominated by
+        // predecessors still loading, and more uncached status loads per
+        // round only add latency under load.
+        const int64_t K = std::max<int64_t>(1, std::min<int64_t>(8, tune("lb_window", 1)));
+        std::string sK = std::to_string(K);
+        k << "        const int q0 = j - " << sK << " * lane;\n"
+          << "        int fl[" << sK << "];\n"
+          << "        " << T << " val[" << sK << "];\n"
+          << "#pragma unroll\n"
+          << "        for (int c = 0; c < " << sK << "; c++) {\n"
+          << "          fl[c] = 2; val[c] = " << ini << "();\n"
+          << "          if (q0 - c >= rowstart) {\n"
+          << "            const cc_u64 w = __hip_atomic_load(&st[q0 - c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
+          << "            fl[c] = (int)(w >> 32); val[c] = cc_from_bits<" << T << ">(w & 0xffffffffull);\n"
+          << "          }\n"
+          << "        }\n"
+          << "        int P;\n"
+          << "        while (true) {\n"
+          << "          int mine = " << sK << ";\n"
+          << "#pragma unroll\n"
+          << "          for (int c = " << K - 1 << "; c >= 0; c--) if (fl[c] == 2) mine = c;\n"
+          << "          const cc_u64 im = __ballot(mine < " << sK << ");\n"
+          << "          P = " << 64 * K << ";\n"
+          << "          if (im) { const int Lf = __ffsll((long long)im) - 1; P = " << sK
+          << " * Lf + __shfl(mine, Lf); }\n"
+          << "          bool wait = false;\n"
+          << "#pragma unroll\n"
+          << "          for (int c = 0; c < " << sK << "; c++) wait |= fl[c] == 0 && " << sK << " * lane + c < P;\n"
+          << "          if (!__ballot(wait)) break;\n"
+          << "          if (++spins > (1u << 24)) { cc_flag(err, 4); P = 0;\n"
+          << "#pragma unroll\n"
+          << "            for (int c = 0; c < " << sK << "; c++) { fl[c] = 2; val[c] = " << ini << "(); }\n"
+          << "            break; }\n"
+          << "          __builtin_amdgcn_s_sleep(1);\n"
+          << "#pragma unroll\n"
+          << "          for (int c = 0; c < " << sK << "; c++)\n"
+          << "            if (fl[c] == 0 && " << sK << " * lane + c < P) {\n"
+          << "              const cc_u64 w = __hip_atomic_load(&st[q0 - c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
+          << "              fl[c] = (int)(w >> 32); val[c] = cc_from_bits<" << T << ">(w & 0xffffffffull);\n"
+          << "            }\n"
+          << "        }\n"
+          // lane-local fold, farthest word first, of the positions <= P
+          << "        " << T << " w = " << ini << "();\n"
+          << "        bool hw = false;\n"
+          << "#pragma unroll\n"
+          << "        for (int c = " << K - 1 << "; c >= 0; c--)\n"
+          << "          if (" << sK << " * lane + c <= P) { w = hw ? " << cmb << "(w, val[c]) : val[c]; hw = true; }\n";
+        k << lookback_tree(cmb, T)
+          << "        w = __shfl(w, 0);\n"
+          << "        acc = have ? " << cmb << "(w, acc) : w;\n"
+          << "        have = true;\n"
+          << "        if (P < " << 64 * K << ") break;\n"
+          << "        j -= " << 64 * K << ";\n"
+          << "      }\n";
       } else {
-        k << "            const cc_u64 w0 = __hip_atomic_load(&st[2 * q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
+        k << "        const int q = j - lane;\n"
+          << "        int flag = 2;\n"
+          << "        " << T << " val = " << ini << "();\n"
+          << "        if (q >= rowstart) {\n"
+          << "          while (true) {\n"
+          << "            const cc_u64 w0 = __hip_atomic_load(&st[2 * q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
           << "            const cc_u64 w1 = __hip_atomic_load(&st[2 * q + 1], __ATOMIC_RELAXED, "
              "__HIP_MEMORY_SCOPE_AGENT);\n"
           << "            flag = (int)(w0 >> 32);\n"
           << "            if (flag != 0 && flag == (int)(w1 >> 32)) { val = cc_from_bits<" << T
-          << ">((w0 & 0xffffffffull) | (w1 << 32)); break; }\n";
+          << ">((w0 & 0xffffffffull) | (w1 << 32)); break; }\n"
+          << "            if (++spins > (1u << 24)) { cc_flag(err, 4); flag = 2; break; }\n"
+          << "            __builtin_amdgcn_s_sleep(1);\n"
+          << "          }\n"
+          << "        }\n"
+          << "        const cc_u64 pm = __ballot(flag == 2);\n"
+          << "        const int L = pm ? (__ffsll((long long)pm) - 1) : 63;\n"
+          << "        " << T << " w = val;\n"
+          << "        bool hw = lane <= L;\n";
+        k << lookback_tree(cmb, T)
+          << "        w = __shfl(w, 0);\n"
+          << "        acc = have ? " << cmb << "(w, acc) : w;\n"
+          << "        have = true;\n"
+          << "        if (pm) break;\n"
+          << "        j -= 64;\n"
+          << "      }\n";
       }
-      k << "            if (++spins > (1u << 24)) { cc_flag(err, 4); flag = 2; break; }\n"
-        << "            __builtin_amdgcn_s_sleep(1);\n"
-        << "          }\n"
-        << "        }\n"
-        << "        const cc_u64 pm = __ballot(flag == 2);\n"
-        << "        const int L = pm ? (__ffsll((long long)pm) - 1) : 63;\n"
-        << "        " << T << " w = lane <= L ? val : " << ini << "();\n";
-      for (int off = 1; off < 64; off *= 2)
-        k << "        { const " << T << " o = __shfl_down(w, " << off << "); if ((lane & " << (2 * off - 1)
-          << ") == 0) w = " << cmb << "(o, w); }\n";
-      k << "        w = __shfl(w, 0);\n"
-        << "        acc = have ? " << cmb << "(w, acc) : w;\n"
-        << "        have = true;\n"
-        << "        if (pm) break;\n"
-        << "        j -= 64;\n"
-        << "      }\n"
+      k
         << "      if (lane == 0) {\n"
         << "        s_prefix = acc;\n"
         << "        const " << T << " incl = " << cmb << "(acc, run);\n"
@@ -1392,7 +1473,6 @@ struct Lowering {
     return {kscan};
   }
 
-  // ---- Scatter_add root (K9 zero fill + K10 atomics) ---------------------
   // ---- Scatter_add without global atomics -----------------------------------
   // Device-wide atomics run at roughly one per clock per XCD whatever the
   // table size, so collisions are resolved in LDS instead. The bins are cut
@@ -1406,10 +1486,10 @@ struct Lowering {
   //   accumulate W workgroups per slice fold the slice's pairs into an LDS
   //             table with LDS atomics and store it (W = 1) or a partial
   //   reduce    out[b] = sum over w of the partials, w ascending
-  // With one slice (B <= 4096) the partition is skipped and the workgroups
+  // With one slice (B <= S) the partition is skipped and the workgroups
   // fold contiguous input chunks directly. Out-of-range indices are skipped
   // and flag error 2, as the atomic path does. Within a slice the order of
-  // the additions depends on LDS atomic order, so float sums are not
+  // the additions depends on LDS arrival order, so float sums are not
   // bit-reproducible (the atomic path's are not either).
   std::vector<int> lower_scatter_lds(int t, int64_t B, int64_t N, int64_t S, int64_t P) {
     const TNode &n = g.ts[t];

@@ -91,6 +91,25 @@ def test_reduce_variants(device, rows, n, dtype, tpl):
     check(g, [("x", data(dtype, (rows, n), 12))], [tpl])
 
 
+@pytest.mark.parametrize("rows,n,dtype,tpl", REDUCE_CASES, ids=lambda v: str(v))
+def test_reduce_init_applied_once(device, rows, n, dtype, tpl):
+    """init is not the identity here: the interpreter folds it in once per
+    row (R2), so a template that seeded every lane with it would be off by
+    (lanes - 1) * init."""
+    x = D.param("x", dtype, (rows, n))
+    g = Graph.create("red", [("s", D.reduce_rows(D.add, D.const(dtype, 5), x)),
+                             ("m", D.reduce_rows(D.max, D.const(dtype, 3), x))])
+    check(g, [("x", data(dtype, (rows, n), 14))], [tpl])
+
+
+@pytest.mark.parametrize("rows,n,dtype,tpl", SCAN_CASES, ids=lambda v: str(v))
+def test_scan_init_applied_once(device, rows, n, dtype, tpl):
+    x = D.param("x", dtype, (rows, n))
+    g = Graph.create("scan", [("p", D.scan_rows(D.add, D.const(dtype, 7), x)),
+                              ("q", D.scan_rows(D.max, D.const(dtype, 2), x))])
+    check(g, [("x", data(dtype, (rows, n), 15))], [tpl])
+
+
 def test_reduce_empty_rows(device):
     x = D.param("x", F32, (5, 0))
     g = Graph.create("e", [("s", D.reduce_rows(D.add, D.const(F32, 2.5), x))])
