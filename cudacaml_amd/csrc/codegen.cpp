@@ -2110,6 +2110,84 @@ struct Lowering {
     return {add_kernel(kname, args, (int)ntiles, 256, role)};
   }
 
+  // ---- Skinny matmul: split over k ------------------------------------------
+  // For products with few outputs and a long k (LSM's X^T X : [3;n] x [n;3],
+  // n = 65536) the 16x16 tiling launches one workgroup that walks all of k.
+  // Here workgroup g folds the k-chunk [g*KC, (g+1)*KC): thread t takes
+  // k = k0 + t, k0 + t + 256, ... for every output, the partial sums are
+  // reduced across the workgroup, and a second kernel adds the G partials
+  // of each output in g order. Products and sums are rounded separately
+  // (no FMA), as the interpreter does (R9); the summation order differs
+  // from its k-ascending one, so float results match to rounding.
+  std::vector<int> lower_matmul_splitk(int t, int64_t M, int64_t N, int64_t K, const ElemFn &fa, const ElemFn &fb) {
+    const TNode &n = g.ts[t];
+    std::string id = std::to_string(n.id);
+    std::string kname = "k_" + id;
+    std::string T = dt_ctype(n.dt);
+    std::string acc = n.dt == DT::I32 ? "cc_u32" : (n.dt == DT::I64 ? "cc_u64" : T);  // integers wrap
+    int out = buf_of[t];
+    const int64_t MN = M * N;
+    int64_t G = std::max<int64_t>(1, std::min<int64_t>(tune("mm_splitk_groups", 256), cdiv(K, 512)));
+    int64_t KC = cdiv(cdiv(K, G), 256) * 256;
+    G = cdiv(K, KC);
+    int part = add_buf("t" + id + "_kpart", n.dt, G * MN, BufRole::Scratch);
+    Params p;
+    add_in(p, fa);
+    add_in(p, fb);
+    p.out.push_back(part);
+    std::vector<int> args;
+    std::string params = param_list(p, args);
+    std::ostringstream k;
+    k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_splitk(" << params << ") {\n"
+      << "  __shared__ " << acc << " wpart[4][" << MN << "];\n"
+      << "  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;\n"
+      << "  " << acc << " s[" << MN << "];\n"
+      << "#pragma unroll\n"
+      << "  for (int q = 0; q < " << MN << "; q++) s[q] = (" << acc << ")0;\n"
+      << "  const int k0 = blockIdx.x * " << KC << ";\n"
+      << "  const int k1 = k0 + " << KC << " < " << K << " ? k0 + " << KC << " : " << K << ";\n"
+      << "  for (int kk = k0 + (int)threadIdx.x; kk < k1; kk += 256) {\n"
+      << "    " << T << " a[" << M << "], b[" << N << "];\n";
+    for (int64_t m = 0; m < M; m++)
+      k << "    a[" << m << "] = " << fa.call_scalar(std::to_string(m * K) + " + kk") << ";\n";
+    for (int64_t c = 0; c < N; c++)
+      k << "    b[" << c << "] = " << fb.call_scalar("kk * " + std::to_string(N) + " + " + std::to_string(c)) << ";\n";
+    k << "#pragma unroll\n"
+      << "    for (int m = 0; m < " << M << "; m++)\n"
+      << "#pragma unroll\n"
+      << "      for (int c = 0; c < " << N << "; c++) {\n";
+    if (n.dt == DT::I32 || n.dt == DT::I64)
+      k << "        s[m * " << N << " + c] += (" << acc << ")a[m] * (" << acc << ")b[c];\n";
+    else
+      k << "        const " << T << " pr = a[m] * b[c];\n"
+        << "        s[m * " << N << " + c] = s[m * " << N << " + c] + pr;\n";
+    k << "      }\n"
+      << "  }\n"
+      << "#pragma unroll\n"
+      << "  for (int q = 0; q < " << MN << "; q++) {\n"
+      << "    " << acc << " v = s[q];\n"
+      << "    for (int off = 32; off > 0; off >>= 1) v = v + __shfl_xor(v, off);\n"
+      << "    if (lane == 0) wpart[wid][q] = v;\n"
+      << "  }\n"
+      << "  __syncthreads();\n"
+      << "  for (int q = threadIdx.x; q < " << MN << "; q += 256)\n"
+      << "    b" << part << "[(size_t)blockIdx.x * " << MN << " + q] = (" << T << ")(((wpart[0][q] + wpart[1][q]) + wpart[2][q]) + wpart[3][q]);\n"
+      << "}\n";
+    k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_ksum(const " << T << "* __restrict__ b"
+      << part << ", " << T << "* __restrict__ b" << out << ") {\n"
+      << "  for (int q = blockIdx.x * 256 + threadIdx.x; q < " << MN << "; q += gridDim.x * 256) {\n"
+      << "    " << acc << " v = (" << acc << ")b" << part << "[q];\n"
+      << "    for (int gg = 1; gg < " << G << "; gg++) v = v + (" << acc << ")b" << part << "[(size_t)gg * " << MN
+      << " + q];\n"
+      << "    b" << out << "[q] = (" << T << ")v;\n"
+      << "  }\n"
+      << "}\n";
+    src << k.str();
+    int k1 = add_kernel(kname + "_splitk", args, (int)G, 256, "matmul_splitk");
+    int k2 = add_kernel(kname + "_ksum", {part, out}, (int)std::max<int64_t>(1, cdiv(MN, 256)), 256, "matmul_ksum");
+    return {k1, k2};
+  }
+
   // ---- Matmul root (K11) --------------------------------------------------
   // Generic tiled product: one output per thread, k ascending, each product
   // and sum rounded separately, zero-padded edge tiles. For float dtypes
@@ -2130,6 +2208,9 @@ struct Lowering {
     ElemFn fa = gen.element_fn("fa_" + id, n.a, false, false);
     ElemFn fb = gen.element_fn("fb_" + id, n.b, false, false);
     src << fa.code << fb.code;
+    if (K > 0 && M * N <= tune("mm_splitk_outputs", 32) && cdiv(M, 16) * cdiv(N, 16) < 64 &&
+        K >= tune("mm_splitk_min_k", 4096))
+      return lower_matmul_splitk(t, M, N, K, fa, fb);
     Params p;
     add_in(p, fa);
     add_in(p, fb);

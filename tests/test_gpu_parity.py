@@ -223,3 +223,65 @@ def test_matmul_f32_full_size_vs_exact(device):
     exact = a.astype(np.float64) @ b.astype(np.float64)
     err = np.abs(got - exact) / (1.0 + np.abs(exact))
     assert err.max() <= 1e-4, err.max()
+
+
+@pytest.mark.parametrize("dtype,m,k,n", [(F64, 3, 65536, 3), (F64, 3, 65536, 1), (F32, 4, 100003, 8),
+                                         (I32, 5, 7777, 6), (F32, 1, 4096, 32)])
+def test_matmul_split_k(device, dtype, m, k, n):
+    """Few outputs, long k: the k range is split over workgroups and the
+    partials added in fixed order."""
+    g = C.matmul(n, dtype, k=k, m=m)
+    assert "matmul_splitk" in _plan_roles(g)
+    if dtype is I32:
+        a, b = C.small_ints(21, (m, k)), C.small_ints(22, (k, n))
+    else:
+        a, b = C.uniform_pm1(21, (m, k)).astype(dtype.np), C.uniform_pm1(22, (k, n)).astype(dtype.np)
+    assert_policy(g, [("a", a), ("b", b)])
+
+
+def test_matmul_split_k_fused_transpose(device):
+    """The LSM shape: X^T X with X^T a transpose of a fused map."""
+    x = D.param("x", F64, (20000, 3))
+    xm = D.map(lambda e: D.mul(e, e), x)
+    g = Graph.create("xtx", [("xtx", D.matmul(D.transpose(xm), xm))])
+    assert "matmul_splitk" in _plan_roles(g)
+    assert_policy(g, [("x", C.uniform_pm1(23, (20000, 3)).astype(np.float64))])
+
+
+def test_lsm_graphs_vs_oracle(device):
+    """Each of the three LSM graphs against the oracle on the same inputs,
+    to the f64 bar."""
+    from cudacaml_amd.examples import lsm
+
+    n, ns = 4096, 12
+    disc = math.exp(-0.05 / ns)
+    gp = lsm.paths_graph(n, ns)
+    exp, got = assert_policy(gp, [("seed", np.array(11, np.int32))])
+    s = dict(exp)["S"]
+    cf = np.maximum(100.0 - s[:, ns - 1], 0.0)
+    tv = np.array(ns - 3, np.int32)
+    gr = lsm.regress_graph(n, ns, 100.0, disc)
+    exp, _ = assert_policy(gr, [("S", s), ("cf", cf), ("t", tv)])
+    beta = lsm._beta(dict(exp)["xtx"], dict(exp)["xty"])
+    gu = lsm.update_graph(n, ns, 100.0, disc)
+    assert_policy(gu, [("S", s), ("cf", cf), ("t", tv), ("beta", beta)])
+
+
+def test_lsm_american_put_on_device(device):
+    """S17 (test_system.ml:187-194): 65536 paths x 50 steps, within 0.15 of
+    the binomial value; the resident driver and the host-array driver agree
+    bit for bit, and the device price is close to the oracle's."""
+    from cudacaml_amd.examples import lsm
+
+    binom = lsm.binomial_american_put(500)
+    t = lsm.MakeResident(65536, 50)
+    try:
+        px = t.price(11)
+    finally:
+        t.release()
+    assert abs(px - binom) <= 0.15, (px, binom)
+    px_host = lsm.Make(H, 65536, 50).price(11)
+    assert px_host == px
+    px_oracle = lsm.Make(oracle.Interp, 8192, 50).price(11)
+    px_dev = lsm.Make(H, 8192, 50).price(11)
+    assert abs(px_dev - px_oracle) <= 1e-3, (px_dev, px_oracle)
