@@ -42,26 +42,16 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def plan_bytes(H, graph, kernel_filter=None):
-    """Algorithmic bytes of every kernel of the plan: each distinct buffer
-    argument counted once, scratch excluded."""
-    text = H.plan(graph)
-    bufs = {}
-    kernels = []
-    for line in text.splitlines():
-        f = line.split()
-        if f[0] == "buffer":
-            size = {"f32": 4, "f64": 8, "i32": 4, "i64": 8}[f[3]] * int(f[4])
-            bufs[int(f[1])] = (f[2], size, f[5])
-        elif f[0] == "kernel":
-            args = [int(x) for x in f[f.index("args") + 1:]]
-            kernels.append((f[1], f[2], args))
+def plan_bytes(H, graph):
+    """Algorithmic bytes of every kernel of the plan, as the code generator
+    attributes them: each element a root reads counted once (a gather one
+    element per output, a broadcast source one), its output written once,
+    on the root's main kernel; helper kernels carry 0."""
     out = {}
-    for name, role, args in kernels:
-        if role in ("scan_init",):
-            continue
-        b = sum(bufs[a][1] for a in set(args) if bufs[a][2] in ("param", "computed"))
-        out[name] = (role, b)
+    for line in H.plan(graph).splitlines():
+        f = line.split()
+        if f[0] == "kernel":
+            out[f[1]] = (f[2], int(f[f.index("bytes") + 1]))
     return out
 
 
@@ -200,6 +190,7 @@ def pmc_child(args):
     from cudacaml_amd.examples import configs as C
 
     w = build_workload(args.config, H, C)
+    step(H, w)
     dom = dominant(H, w, args.config)[0]
     cal = build_workload("copy", H, C)
     copy_name = list(plan_bytes(H, cal.programs[0][0]))[0]
@@ -275,16 +266,38 @@ def measure_traffic(config, steps=2):
     return int(fetch + write), detail
 
 
-def dominant(H, w, config):
-    """The kernel with the most algorithmic bytes (the matmul, for flops):
-    (name, role, bytes, compiled) plus every kernel's (role, bytes)."""
+def kernel_table(H, w):
     kinfo = {}
     for g, c, _, _ in w.programs:
         for k, (role, b) in plan_bytes(H, g).items():
             kinfo[k] = (role, b, c)
-    dom = max(kinfo.items(), key=lambda kv: kv[1][1])[0]
-    if config.startswith("matmul"):
-        dom = [k for k, v in kinfo.items() if v[0].startswith("matmul")][0]
+    return kinfo
+
+
+def dominant(H, w, config, timed=True):
+    """The kernel that takes the most time per step (one timed step per
+    kernel, HIP events around its launches), or, without timing, the one
+    with the most algorithmic bytes (the matmul for matmul configs):
+    (name, role, bytes, compiled, table)."""
+    kinfo = kernel_table(H, w)
+    if timed:
+        from cudacaml_amd.runtime import Device
+
+        best, best_ms = None, -1.0
+        for k, (role, b, c) in kinfo.items():
+            H.time_kernel(c, k)
+            step(H, w)
+            Device.synchronize()
+            each = H.timing_each(c)
+            H.time_kernel(c, None)
+            ms = sum(each)
+            if ms > best_ms:
+                best, best_ms = k, ms
+        dom = best
+    else:
+        dom = max(kinfo.items(), key=lambda kv: kv[1][1])[0]
+        if config.startswith("matmul"):
+            dom = [k for k, v in kinfo.items() if v[0].startswith("matmul")][0]
     return (dom,) + kinfo[dom] + (kinfo,)
 
 
@@ -342,10 +355,10 @@ def main():
     w = build_workload(args.config, H, C)
     log("compiled and generated inputs in %.1fs" % (time.perf_counter() - t0))
 
-    dom, dom_role, dom_bytes, dom_c, kinfo = dominant(H, w, args.config)
-
     for _ in range(args.warmup):
         step(H, w)
+    Device.synchronize()
+    dom, dom_role, dom_bytes, dom_c, kinfo = dominant(H, w, args.config)
     Device.synchronize()
     H.time_kernel(dom_c, dom)
     Device.synchronize()
@@ -372,11 +385,11 @@ def main():
     else:
         value = C.PATHS5 * args.steps / elapsed
     dom_avg_ms = sum(each) / max(1, len(each))
-    if w.unit == "TFLOP/s":
-        g = w.programs[0][0]
-        mm = [t for t in g.order if t.kind == "matmul"][0]
+    if dom_role.startswith("matmul"):
+        uid = int(dom.split("_")[1])
+        mm = [t for g, _, _, _ in w.programs for t in g.order if t.uid == uid][0]
         fl = 2 * mm.shape[0] * mm.shape[1] * mm.a.shape[1]
-        peak = FP64_MFMA_TFLOPS if w.dtype == "f64" else FP32_MFMA_TFLOPS
+        peak = FP64_MFMA_TFLOPS if mm.dtype.name == "f64" else FP32_MFMA_TFLOPS
         achieved = fl / (dom_avg_ms * 1e-3) / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
                 "frac": round(achieved / peak, 4), "traffic": traffic, "flops_per_launch": fl}

@@ -652,6 +652,14 @@ std::string fold_in(const std::string &cmb, const std::string &T, const std::str
   return "{ const " + T + " x_ = " + x + "; acc = has ? " + cmb + "(acc, x_) : x_; has = true; }";
 }
 
+// As fold_in, but only where `cond` holds, without a branch: the value is
+// folded and then selected, so the loads that feed it cannot be sunk into a
+// conditional block (which would serialise them behind one another).
+std::string fold_in_if(const std::string &cmb, const std::string &T, const std::string &x, const std::string &cond) {
+  return "{ const " + T + " x_ = " + x + "; const bool ok_ = " + cond + "; const " + T + " y_ = has ? " + cmb +
+         "(acc, x_) : x_; acc = ok_ ? y_ : acc; has = has || ok_; }";
+}
+
 // One butterfly step over (acc, has): the lower lane's value stays on the left.
 std::string xor_combine(const std::string &cmb, const std::string &T, const std::string &off) {
   return "{ const " + T + " o_ = __shfl_xor(acc, " + off + "); const bool oh_ = __shfl_xor((int)has, " + off +
@@ -783,6 +791,130 @@ struct Lowering {
 
   std::function<std::string(int)> tyof() {
     return [this](int b) { return ty(b); };
+  }
+
+  // ---- Algorithmic bytes per root ------------------------------------------
+  // Bytes an element function reads when evaluated at n indices: a buffer
+  // read at the element's own index contributes the elements read; one read
+  // anywhere else (a gather) one element per evaluation, at most the
+  // buffer; a one-element buffer (a scalar or a broadcast source) one.
+  // Only buffers the function's result (or a side effect such as a bounds
+  // flag) depends on count: loads of sub-expressions that end up unused are
+  // dropped by the compiler, so they move no bytes.
+  int64_t fn_bytes(const ElemFn &f, int64_t n) const {
+    std::set<int> ident, ptrs;
+    live_buffers(f.code, ident, ptrs);
+    int64_t b = 0;
+    for (int x : f.ident)
+      if (ident.count(x)) b += std::min(prog.bufs[x].numel, n) * dt_size(prog.bufs[x].dt);
+    for (int x : f.ptrs) {
+      if (!ptrs.count(x) || ident.count(x)) continue;
+      int64_t e = prog.bufs[x].numel <= 1 ? prog.bufs[x].numel : std::min(prog.bufs[x].numel, n);
+      b += e * dt_size(prog.bufs[x].dt);
+    }
+    return b;
+  }
+
+  // Liveness over an element function's body: each line either defines a
+  // temporary vN or is a statement kept for its effect; the return value
+  // and those statements are the roots. Collects the aN (value parameters)
+  // and bN (buffer pointers) the live lines use.
+  static void live_buffers(const std::string &code, std::set<int> &ident, std::set<int> &ptrs) {
+    auto tokens = [](const std::string &line) {
+      std::vector<std::string> out;
+      size_t i = 0;
+      while (i < line.size()) {
+        char c = line[i];
+        if (isdigit((unsigned char)c)) {  // numeric literal, hex floats included
+          while (i < line.size() && (isalnum((unsigned char)line[i]) || line[i] == '.' || line[i] == '_')) i++;
+        } else if (isalpha((unsigned char)c) || c == '_') {
+          size_t j = i;
+          while (j < line.size() && (isalnum((unsigned char)line[j]) || line[j] == '_')) j++;
+          out.push_back(line.substr(i, j - i));
+          i = j;
+        } else {
+          i++;
+        }
+      }
+      return out;
+    };
+    auto kind = [](const std::string &t, char k) {
+      if (t.size() < 2 || t[0] != k) return false;
+      for (size_t i = 1; i < t.size(); i++)
+        if (!isdigit((unsigned char)t[i])) return false;
+      return true;
+    };
+    size_t body = code.find(") {\n");
+    if (body == std::string::npos) return;
+    std::map<std::string, std::vector<std::string>> defs;
+    std::vector<std::string> work;
+    size_t pos = body + 4;
+    while (pos < code.size()) {
+      size_t e = code.find('\n', pos);
+      if (e == std::string::npos) e = code.size();
+      std::string line = code.substr(pos, e - pos);
+      pos = e + 1;
+      std::vector<std::string> t = tokens(line);
+      if (t.empty()) continue;
+      // "const T vN = ..." or "T vN = ...": a definition
+      size_t eq = line.find(" = ");
+      std::string def;
+      if (eq != std::string::npos && line.find("if ") == std::string::npos) {
+        std::vector<std::string> lhs = tokens(line.substr(0, eq));
+        if (!lhs.empty() && kind(lhs.back(), 'v')) def = lhs.back();
+      }
+      if (!def.empty()) {
+        std::vector<std::string> rhs = tokens(line.substr(eq + 3));
+        defs[def].insert(defs[def].end(), rhs.begin(), rhs.end());
+      } else {
+        for (auto &x : t) work.push_back(x);  // return statement or effect
+      }
+    }
+    std::set<std::string> seen;
+    while (!work.empty()) {
+      std::string x = work.back();
+      work.pop_back();
+      if (!seen.insert(x).second) continue;
+      if (kind(x, 'a')) ident.insert(atoi(x.c_str() + 1));
+      if (kind(x, 'b')) ptrs.insert(atoi(x.c_str() + 1));
+      auto it = defs.find(x);
+      if (it != defs.end())
+        for (auto &y : it->second) work.push_back(y);
+    }
+  }
+
+  void attribute_bytes(int r, const std::vector<int> &ks) {
+    if (ks.empty()) return;
+    const TNode &n = g.ts[r];
+    const int64_t out = n.numel * dt_size(n.dt);
+    int64_t bytes = 0;
+    switch (n.kind) {
+      case TK::Reduce:
+      case TK::Scan: bytes = fn_bytes(gen.element_fn("ab_", n.a, false, true), g.ts[n.a].numel) + out; break;
+      case TK::Scatter: {
+        int64_t N = g.ts[n.a].numel;
+        bytes = fn_bytes(gen.element_fn("ab_", n.a, false, true), N) +
+                fn_bytes(gen.element_fn("ab_", n.b, false, true), N) + out;
+        break;
+      }
+      case TK::Matmul: {
+        int64_t M = n.shape[0], N = n.shape[1], K = g.ts[n.a].shape[1];
+        bytes = fn_bytes(gen.element_fn("ab_", n.a, false, true), M * K) +
+                fn_bytes(gen.element_fn("ab_", n.b, false, true), K * N) + out;
+        break;
+      }
+      default: bytes = fn_bytes(gen.element_fn("ab_", r, true, true), n.numel) + out;
+    }
+    static const char *helpers[] = {"scan_init",          "scatter_zero",   "scatter_count",  "scatter_colscan",
+                                    "scatter_bscan",      "scatter_accumulate", "scatter_reduce", "matmul_ksum",
+                                    "reduce_split_fold"};
+    int main = ks.back();
+    for (int k : ks) {
+      bool helper = false;
+      for (const char *h : helpers) helper |= prog.kernels[k].role == h;
+      if (!helper) main = k;
+    }
+    prog.kernels[main].algo_bytes = bytes;
   }
 
   // ---- element-wise root (K1 -> vectorised grid-stride map) --------------
@@ -1026,9 +1158,17 @@ struct Lowering {
         << "    " << T << " acc = " << ini << "();\n"
         << "    bool has = false;\n"
         << "    if (r < " << rows << ") {\n"
-        << "      for (int j = sl; j < " << len << "; j += " << S << ") {\n"
-        << "        const int i = r * " << len << " + j;\n"
-        << "        " << fold_in(cmb, T, f.call_scalar("i")) << "\n"
+        << "      for (int j0 = sl; j0 < " << len << "; j0 += " << 4 * S << ") {\n"
+        << "        " << T << " xs[4];\n"
+        << "#pragma unroll\n"
+        << "        for (int u = 0; u < 4; u++) {\n"
+        << "          const int i = r * " << len << " + (j0 + u * " << S << " < " << len << " ? j0 + u * " << S
+        << " : j0);\n"
+        << "          xs[u] = " << f.call_scalar("i") << ";\n"
+        << "        }\n"
+        << "#pragma unroll\n"
+        << "        for (int u = 0; u < 4; u++) "
+        << fold_in_if(cmb, T, "xs[u]", "j0 + u * " + std::to_string(S) + " < " + std::to_string(len)) << "\n"
         << "      }\n"
         << "    }\n";
       for (int64_t off = S / 2; off > 0; off /= 2) k << "    " << xor_combine(cmb, T, std::to_string(off)) << "\n";
@@ -1049,18 +1189,39 @@ struct Lowering {
     std::string wave_parts = "      " + T + " t = " + ini + "();\n      bool th = false;\n"
                              "      for (int w = 0; w < 4; w++) if (whas[w]) { t = th ? " + cmb +
                              "(t, wpart[w]) : wpart[w]; th = true; }\n";
+    // Four strides per iteration, all loads issued before any is folded
+    // (a one-load loop leaves each workgroup waiting out one memory latency
+    // per stride); strides past the end load at the iteration's first
+    // (valid) index and are not folded.
     auto fold_loop = [&](const std::string &lo, const std::string &hi) {
       std::ostringstream l;
       if (vec) {
-        l << "    for (int j = " << lo << " + threadIdx.x * 4; j < " << hi << "; j += 1024) {\n"
-          << "      const int i = base + j;\n"
-          << vec_loads(f, "i", "      ", tyof());
-        for (int u = 0; u < 4; u++) l << "      " << fold_in(cmb, T, lane_call(f, "i", u)) << "\n";
-        l << "    }\n";
+        l << "    for (int j0 = " << lo << " + threadIdx.x * 4; j0 < " << hi << "; j0 += 4096) {\n";
+        for (int b : f.ident) l << "      cc_v4<" << ty(b) << "> l" << b << "_[4];\n";
+        l << "#pragma unroll\n"
+          << "      for (int u = 0; u < 4; u++) {\n"
+          << "        const int i = base + (j0 + u * 1024 < " << hi << " ? j0 + u * 1024 : j0);\n";
+        for (int b : f.ident)
+          l << "        l" << b << "_[u] = *(const cc_v4<" << ty(b) << ">*)(b" << b << " + i);\n";
+        l << "      }\n"
+          << "#pragma unroll\n"
+          << "      for (int u = 0; u < 4; u++) {\n"
+          << "        const bool in = j0 + u * 1024 < " << hi << ";\n"
+          << "        const int i = base + (in ? j0 + u * 1024 : j0);\n";
+        for (int b : f.ident) l << "        const cc_v4<" << ty(b) << "> l" << b << " = l" << b << "_[u];\n";
+        for (int u = 0; u < 4; u++) l << "        " << fold_in_if(cmb, T, lane_call(f, "i", u), "in") << "\n";
+        l << "      }\n"
+          << "    }\n";
       } else {
-        l << "    for (int j = " << lo << " + threadIdx.x; j < " << hi << "; j += 256) {\n"
-          << "      const int i = base + j;\n"
-          << "      " << fold_in(cmb, T, f.call_scalar("i")) << "\n"
+        l << "    for (int j0 = " << lo << " + threadIdx.x; j0 < " << hi << "; j0 += 1024) {\n"
+          << "      " << T << " xs[4];\n"
+          << "#pragma unroll\n"
+          << "      for (int u = 0; u < 4; u++) {\n"
+          << "        const int i = base + (j0 + u * 256 < " << hi << " ? j0 + u * 256 : j0);\n"
+          << "        xs[u] = " << f.call_scalar("i") << ";\n"
+          << "      }\n"
+          << "#pragma unroll\n"
+          << "      for (int u = 0; u < 4; u++) " << fold_in_if(cmb, T, "xs[u]", "j0 + u * 256 < " + hi) << "\n"
           << "    }\n";
       }
       return l.str();
@@ -1091,59 +1252,69 @@ struct Lowering {
       int grid = (int)std::min<int64_t>(rows, 1 << 20);
       return {add_kernel(kname, args, grid, 256, "reduce_block")};
     }
-    // Few long rows: split each row over G workgroups; the last one to
-    // finish a row folds the row's partials (one launch, no second pass).
-    int64_t unit = vec ? 1024 : 256;
+    // Few long rows: split each row over G workgroups that store one partial
+    // each; a second kernel folds each row's G partials in order. The kernel
+    // boundary makes the partials visible: no per-workgroup release (on a
+    // multi-XCD device an agent-scope release writes back the L2) and no
+    // counter to reset.
+    int64_t unit = vec ? 4096 : 1024;
     int64_t G = std::max<int64_t>(1, std::min<int64_t>(cdiv(2048, rows), cdiv(len, 4096)));
     int64_t chunk = cdiv(cdiv(len, G), unit) * unit;
     G = cdiv(len, chunk);
     int part = add_buf("t" + id + "_partials", n.dt, rows * G, BufRole::Scratch);
-    int cnt = add_buf("t" + id + "_count", DT::I32, rows, BufRole::Scratch);
-    Params p;
-    add_in(p, f);
-    p.out.push_back(out);
-    p.out.push_back(part);
-    p.out.push_back(cnt);
-    std::vector<int> args;
-    std::string params = param_list(p, args);
-    std::ostringstream k;
-    k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
-      << "  __shared__ " << T << " wpart[4];\n"
-      << "  __shared__ bool whas[4];\n"
-      << "  __shared__ int s_last;\n"
-      << "  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;\n"
-      << "  const int r = blockIdx.x / " << G << ";\n"
-      << "  const int g = blockIdx.x - r * " << G << ";\n"
-      << "  const int base = r * " << len << ";\n"
-      << "  const int lo = g * " << chunk << ";\n"
-      << "  const int hi = min(lo + " << chunk << ", " << len << ");\n"
-      << "  {\n"
-      << "    " << T << " acc = " << ini << "();\n"
-      << "    bool has = false;\n"
-      << fold_loop("lo", "hi") << block_reduce << "    if (threadIdx.x == 0) {\n"
-      << wave_parts  // every chunk is non-empty, so th holds
-      << "      __hip_atomic_store(&b" << part << "[blockIdx.x], t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
-      << "      const int prev = __hip_atomic_fetch_add(&b" << cnt
-      << "[r], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);\n"
-      << "      s_last = prev == " << G - 1 << ";\n"
-      << "    }\n"
-      << "    __syncthreads();\n"
-      << "  }\n"
-      << "  if (s_last) {\n"
-      << "    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, \"agent\");\n"
-      << "    " << T << " acc = " << ini << "();\n"
-      << "    bool has = false;\n"
-      << "    for (int q = threadIdx.x; q < " << G << "; q += 256)\n"
-      << "      " << fold_in(cmb, T, "__hip_atomic_load(&b" + std::to_string(part) + "[r * " + std::to_string(G) +
-             " + q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)") << "\n"
-      << block_reduce << "    if (threadIdx.x == 0) {\n"
-      << wave_parts
-      << "      b" << out << "[r] = " << cmb << "(" << ini << "(), t);\n"
-      << "      __hip_atomic_store(&b" << cnt << "[r], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
-      << "    }\n"
-      << "  }\n}\n";
-    src << k.str();
-    return {add_kernel(kname, args, (int)(rows * G), 256, "reduce_split")};
+    std::vector<int> ks;
+    {
+      Params p;
+      add_in(p, f);
+      p.out.push_back(part);
+      std::vector<int> args;
+      std::string params = param_list(p, args);
+      std::ostringstream k;
+      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_part(" << params << ") {\n"
+        << "  __shared__ " << T << " wpart[4];\n"
+        << "  __shared__ bool whas[4];\n"
+        << "  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;\n"
+        << "  const int r = blockIdx.x / " << G << ";\n"
+        << "  const int g = blockIdx.x - r * " << G << ";\n"
+        << "  const int base = r * " << len << ";\n"
+        << "  const int lo = g * " << chunk << ";\n"
+        << "  const int hi = min(lo + " << chunk << ", " << len << ");\n"
+        << "  " << T << " acc = " << ini << "();\n"
+        << "  bool has = false;\n"
+        << fold_loop("lo", "hi") << block_reduce << "  if (threadIdx.x == 0) {\n"
+        << wave_parts  // every chunk is non-empty, so th holds
+        << "    b" << part << "[blockIdx.x] = t;\n"
+        << "  }\n"
+        << "}\n";
+      src << k.str();
+      ks.push_back(add_kernel(kname + "_part", args, (int)(rows * G), 256, "reduce_split"));
+    }
+    {
+      Params p;
+      p.in.push_back(part);
+      p.out.push_back(out);
+      std::vector<int> args;
+      std::string params = param_list(p, args);
+      std::ostringstream k;
+      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
+        << "  __shared__ " << T << " wpart[4];\n"
+        << "  __shared__ bool whas[4];\n"
+        << "  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;\n"
+        << "  for (int r = blockIdx.x; r < " << rows << "; r += gridDim.x) {\n"
+        << "    " << T << " acc = " << ini << "();\n"
+        << "    bool has = false;\n"
+        << "    for (int q = threadIdx.x; q < " << G << "; q += 256) " << fold_in(cmb, T, "b" + std::to_string(part) + "[r * " + std::to_string(G) + " + q]") << "\n"
+        << block_reduce << "    if (threadIdx.x == 0) {\n"
+        << wave_parts
+        << "      b" << out << "[r] = " << cmb << "(" << ini << "(), t);\n"
+        << "    }\n"
+        << "    __syncthreads();\n"
+        << "  }\n"
+        << "}\n";
+      src << k.str();
+      ks.push_back(add_kernel(kname, args, (int)std::min<int64_t>(rows, 1024), 256, "reduce_split_fold"));
+    }
+    return ks;
   }
 
   // ---- Scan root (K5-K8 -> wave / block / decoupled look-back scans) -----
@@ -1507,20 +1678,23 @@ struct Lowering {
     std::vector<int> ks;
     // Loop over [lo, hi) four strides at a time, loads issued first. The
     // clamped index keeps every load in range.
+    // Eight strides per iteration: all loads first (clamped to the chunk's
+    // first index), then the bodies under an in-range flag rather than a
+    // break, so the compiler keeps the loads together.
     auto chunk_loop = [&](bool with_val, const std::string &body) {
       std::ostringstream l;
-      l << "  for (int i0 = lo + (int)threadIdx.x; i0 < hi; i0 += 1024) {\n"
-        << "    int jj[4];\n";
-      if (with_val) l << "    " << T << " xx[4];\n";
+      l << "  for (int i0 = lo + (int)threadIdx.x; i0 < hi; i0 += 2048) {\n"
+        << "    int jj[8];\n";
+      if (with_val) l << "    " << T << " xx[8];\n";
       l << "#pragma unroll\n"
-        << "    for (int u = 0; u < 4; u++) {\n"
+        << "    for (int u = 0; u < 8; u++) {\n"
         << "      const int i = i0 + u * 256 < hi ? i0 + u * 256 : lo;\n"
         << "      jj[u] = " << fi.call_scalar("i") << ";\n";
       if (with_val) l << "      xx[u] = " << fs.call_scalar("i") << ";\n";
       l << "    }\n"
         << "#pragma unroll\n"
-        << "    for (int u = 0; u < 4; u++) {\n"
-        << "      if (i0 + u * 256 >= hi) break;\n"
+        << "    for (int u = 0; u < 8; u++) {\n"
+        << "      const bool in = i0 + u * 256 < hi;\n"
         << "      const int j = jj[u];\n"
         << body << "    }\n"
         << "  }\n";
@@ -1555,7 +1729,8 @@ struct Lowering {
         << "  __syncthreads();\n"
         << "  const int lo = blockIdx.x * " << C << ";\n"
         << "  const int hi = lo + " << C << " < " << N << " ? lo + " << C << " : " << N << ";\n"
-        << chunk_loop(true, "      if ((unsigned)j < " + std::to_string(B) + "u) cc_lds_add(&h[j], xx[u]); else cc_flag(err, 2);\n")
+        << chunk_loop(true, "      if (in) { if ((unsigned)j < " + std::to_string(B) +
+                                "u) cc_lds_add(&h[j], xx[u]); else cc_flag(err, 2); }\n")
         << "  __syncthreads();\n"
         << "  for (int b = threadIdx.x; b < " << B << "; b += 256) b" << dst << "[(size_t)blockIdx.x * " << B
         << " + b] = h[b];\n"
@@ -1592,7 +1767,7 @@ struct Lowering {
         << "  __syncthreads();\n"
         << "  const int lo = blockIdx.x * " << C << ";\n"
         << "  const int hi = lo + " << C << " < " << N << " ? lo + " << C << " : " << N << ";\n"
-        << chunk_loop(false, "      if (" + bounds + ") cc_lds_add(&lc[j >> " + std::to_string(shift) + "], 1);\n")
+        << chunk_loop(false, "      if (in && " + bounds + ") cc_lds_add(&lc[j >> " + std::to_string(shift) + "], 1);\n")
         << "  __syncthreads();\n"
         << "  for (int q = threadIdx.x; q < " << P << "; q += 256) b" << cnt << "[(size_t)blockIdx.x * " << P
         << " + q] = lc[q];\n"
@@ -1744,11 +1919,11 @@ struct Lowering {
         << "  unsigned short* const keys = (unsigned short*)b" << key << ";\n"
         << "  const int lo = blockIdx.x * " << C << ";\n"
         << "  const int hi = lo + " << C << " < " << N << " ? lo + " << C << " : " << N << ";\n"
-        << chunk_loop(true, "      if (" + bounds + ") {\n"
+        << chunk_loop(true, "      if (in && " + bounds + ") {\n"
                             "        const int pos = atomicAdd(&cur[j >> " + std::to_string(shift) + "], 1);\n"
                             "        keys[pos] = (unsigned short)(j & " + std::to_string(S - 1) + ");\n"
                             "        b" + std::to_string(val) + "[pos] = xx[u];\n"
-                            "      } else cc_flag(err, 2);\n")
+                            "      } else if (in) cc_flag(err, 2);\n")
         << "}\n";
       src << k.str();
       ks.push_back(add_kernel(kname + "_partition", args, (int)G, 256, "scatter_partition"));
@@ -1776,9 +1951,14 @@ struct Lowering {
         << "      kk[u] = keys[i];\n"
         << "      xx[u] = b" << val << "[i];\n"
         << "    }\n"
+        // past the end: +0 into bin 0, which leaves every bin unchanged
+        // (tables start at +0, so no bin holds -0) and keeps the use of the
+        // loads unconditional
         << "#pragma unroll\n"
-        << "    for (int u = 0; u < 4; u++)\n"
-        << "      if (i0 + u * 256 < hi) cc_lds_add(&h[kk[u]], xx[u]);\n"
+        << "    for (int u = 0; u < 4; u++) {\n"
+        << "      const bool in = i0 + u * 256 < hi;\n"
+        << "      cc_lds_add(&h[in ? kk[u] : 0], in ? xx[u] : " << zero_of(n.dt) << ");\n"
+        << "    }\n"
         << "  }\n"
         << "  __syncthreads();\n";
       if (part >= 0)
@@ -2283,6 +2463,7 @@ struct Lowering {
         case TK::Matmul: ks = lower_matmul(r); break;
         default: throw Failure("Lower: a Param never gets a kernel");
       }
+      attribute_bytes(r, ks);
       std::vector<int> sc;
       for (size_t b = before; b < prog.bufs.size(); b++)
         if (prog.bufs[b].role == BufRole::Scratch) sc.push_back((int)b);
@@ -2327,7 +2508,7 @@ std::string plan_to_string(const ProgramIR &p) {
   }
   for (auto &k : p.kernels) {
     os << "kernel " << k.name << " " << k.role << " grid " << k.grid << " " << k.grid_y << " block " << k.block
-       << " args";
+       << " bytes " << k.algo_bytes << " args";
     for (int a : k.args) os << " " << a;
     os << "\n";
   }

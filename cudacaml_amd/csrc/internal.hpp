@@ -138,6 +138,10 @@ struct KernelSpec {
   std::vector<int> args;  // buffer indices, in parameter order
   int grid = 1, grid_y = 1, block = 256, block_y = 1, shared_bytes = 0;
   std::string role;       // template that produced it, for the plan dump
+  // Algorithmic bytes of the root this kernel computes (each element the
+  // root reads counted once, its output written once), on the root's main
+  // kernel; 0 on helper kernels (look-back init, scatter bookkeeping, ...).
+  int64_t algo_bytes = 0;
 };
 
 enum class OpK { Alloc, Upload, Launch, Download, Free };

@@ -41,7 +41,7 @@ def test_chain_is_one_kernel():
 
 def test_saxpy_is_map_then_reduce():
     ks = kernels_of(sx.program(1 << 20, 2.0))
-    assert [t for _, t in ks] == ["map", "reduce_split"]
+    assert [t for _, t in ks] == ["map", "reduce_split", "reduce_split_fold"]
 
 
 def test_fanout_materialises_shared_node_once():
@@ -114,7 +114,8 @@ def test_uniform_graph_uploads_only_the_seed():
                                         (600, 4096, "reduce_block"), (64, 64, "reduce_wave")])
 def test_reduce_template_choice(rows, n, tpl):
     x = D.param("x", F32, (rows, n))
-    assert [t for _, t in kernels_of(Graph.create("r", [("s", D.reduce_rows(D.add, D.const(F32, 0), x))]))] == [tpl]
+    got = [t for _, t in kernels_of(Graph.create("r", [("s", D.reduce_rows(D.add, D.const(F32, 0), x))]))]
+    assert got == ([tpl, "reduce_split_fold"] if tpl == "reduce_split" else [tpl])
 
 
 @pytest.mark.parametrize("rows,n,tpls", [(8192, 8192, ["scan_rowseq"]), (1, 1 << 28, ["scan_init", "scan_lookback"]),
@@ -164,3 +165,26 @@ def test_generated_modules_compile_for_gfx950():
 def test_jit_reports_compile_errors():
     with pytest.raises(RuntimeError, match="hiprtc"):
         runtime.Jit.check("bad", "this is not HIP")
+
+
+def _bytes(g):
+    return {k[2]: int(k[k.index("bytes") + 1]) for k in
+            (l.split() for l in H.plan(g).splitlines() if l.startswith("kernel"))}
+
+
+def test_algorithmic_bytes_per_kernel():
+    """Each root's algorithmic bytes sit on its main kernel: identity reads
+    count the elements read, a gather one element per output, a broadcast
+    source one; helper kernels carry none."""
+    n = 1 << 20
+    b = _bytes(sx.program(n, 2.0))
+    assert b["map"] == 3 * 4 * n and b["reduce_split"] == 4 * n + 4
+    b = _bytes(C.global_scan(n))
+    assert b["scan_lookback"] == 8 * n and b["scan_init"] == 0
+    b = _bytes(C.scatter_gather(n, 1 << 14))
+    assert b["scatter_partition"] == 8 * n + 4 * (1 << 14)
+    assert b["scatter_count"] == 0 and b["scatter_accumulate"] == 0
+    assert b["map"] == 4 * n + 4 * (1 << 14) + 4 * n  # idx, the table (once), out
+    # the price reduces the gathered last column only, not the whole path matrix
+    b = _bytes(C.mc_paths(4096, 64))
+    assert b["reduce_split"] < 4 * 4096 + 64
