@@ -2062,6 +2062,13 @@ struct Lowering {
     return ks;
   }
 
+  // Block tile edge of the matrix-core kernels (square tiles; four waves of
+  // BM/2 x BM/2).
+  static int64_t mfma_bm(DT dt) {
+    if (dt == DT::F64) return tune("mm_f64_bm", 64) == 128 ? 128 : 64;
+    return 128;
+  }
+
   // ---- Matmul on the matrix cores ------------------------------------------
   // f32: v_mfma_f32_32x32x2f32, block tile 128x128x16, four waves of 64x64.
   // f64: v_mfma_f64_16x16x4f64, block tile 64x64x16, four waves of 32x32.
@@ -2082,7 +2089,7 @@ struct Lowering {
     bool f64 = n.dt == DT::F64;
     std::string T = dt_ctype(n.dt);
     int out = buf_of[t];
-    const int64_t BM = f64 ? 64 : 128, BK = 16, MT = f64 ? 16 : 32;
+    const int64_t BM = mfma_bm(n.dt), BK = 16, MT = f64 ? 16 : 32;
     const int64_t G = 64 / MT;    // lane groups along k
     const int64_t S = BK / G;     // k steps per tile held by one lane
     const int64_t WT = BM / 2;    // wave tile
@@ -2382,7 +2389,7 @@ struct Lowering {
     int64_t K = g.ts[n.a].shape[1];
     if (M == 0 || N == 0) return {};
     if (dt_is_float(n.dt) && K > 0 && tune("mm_mfma", 1)) {
-      int64_t BM = n.dt == DT::F32 ? 128 : 64;
+      int64_t BM = mfma_bm(n.dt);
       if (M % BM == 0 && N % BM == 0 && K % 16 == 0) return lower_matmul_mfma(t, M, N, K);
     }
     ElemFn fa = gen.element_fn("fa_" + id, n.a, false, false);

@@ -272,14 +272,23 @@ int cchip_device_info(int ordinal, char *name, size_t name_len, char *arch, size
     if (ordinal < 0 || ordinal >= n) throw InvalidArgument(strf("Device.info_of: no device %d", ordinal));
     hipDeviceProp_t p;
     check_hip(hipGetDeviceProperties(&p, ordinal), "hipGetDeviceProperties");
-    if (name && name_len) snprintf(name, name_len, "%s", p.name);
-    if (arch && arch_len) {
-      // "gfx950:sramecc+:xnack-" -> "gfx950"
-      std::string a = p.gcnArchName;
-      size_t c = a.find(':');
-      if (c != std::string::npos) a = a.substr(0, c);
-      snprintf(arch, arch_len, "%s", a.c_str());
+    // "gfx950:sramecc+:xnack-" -> "gfx950"
+    std::string a = p.gcnArchName;
+    size_t c = a.find(':');
+    if (c != std::string::npos) a = a.substr(0, c);
+    if (name && name_len) {
+      // Some drivers report no marketing name; Device.name is never empty
+      // (device.mli), so fall back to hipDeviceGetName, then to the
+      // architecture.
+      std::string nm = p.name;
+      if (nm.empty()) {
+        char buf[256] = {0};
+        if (hipDeviceGetName(buf, sizeof buf - 1, ordinal) == hipSuccess) nm = buf;
+      }
+      if (nm.empty()) nm = "AMD " + a;
+      snprintf(name, name_len, "%s", nm.c_str());
     }
+    if (arch && arch_len) snprintf(arch, arch_len, "%s", a.c_str());
     if (mps) *mps = p.multiProcessorCount;
     if (mem) *mem = (int64_t)p.totalGlobalMem;
   });

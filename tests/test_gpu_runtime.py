@@ -1,0 +1,336 @@
+"""The runtime and executor on the device, as the reference's GPU unit
+suites test them: test_runtime.ml (a hand-written kernel end to end),
+test_info.ml, test_pool.ml (S5), test_streams.ml (S15/S16), test_pinned.ml
+(S18) and the GPU half of test_executor.ml, plus S14 (f32 Greeks against
+the closed form)."""
+
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from cudacaml_amd import backend_hip as H
+from cudacaml_amd import differential as Diff
+from cudacaml_amd import grad as G
+from cudacaml_amd.examples import black_scholes as bs
+from cudacaml_amd.examples import programs as P
+from cudacaml_amd.examples import saxpy as sx
+from cudacaml_amd.ir import F32, Graph
+from cudacaml_amd.runtime import Buffer, Device, Event, Jit, Launch, Pinned, Stream
+
+pytestmark = pytest.mark.gpu
+
+SAXPY_SRC = """
+extern "C" __global__ void saxpy(float* x, float* y, float* out) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < 1000; i += gridDim.x * blockDim.x)
+    out[i] = 2.0f * x[i] + y[i];
+}
+"""
+
+N = 4096
+SAXPY = sx.program(N, 2.0)
+
+
+def inputs(k):
+    return [("x", np.arange(k, N + k, dtype=np.float32)), ("y", np.ones(N, np.float32))]
+
+
+def expect(k):
+    return float(np.sum(2.0 * np.arange(k, N + k, dtype=np.float64) + 1.0))
+
+
+def scalar(outs, name):
+    return float(np.asarray(dict(outs)[name]).reshape(-1)[0])
+
+
+# ---- test_runtime.ml --------------------------------------------------------
+
+
+def test_init_idempotent_and_name(device):
+    Device.init()
+    Device.init()
+    assert len(Device.name()) > 0
+
+
+def test_alloc_free_byte_size(device):
+    b = Buffer.alloc(4096)
+    assert b.byte_size() == 4096
+    b.free()
+
+
+def test_upload_download_roundtrip_and_size_check(device):
+    v = np.array([1, 2, 3, 4], np.int32)
+    b = Buffer.alloc(16)
+    b.upload(v)
+    w = np.zeros(4, np.int32)
+    b.download(w)
+    assert w.tolist() == [1, 2, 3, 4]
+    with pytest.raises(ValueError):
+        b.upload(np.zeros(4, np.float64))
+    b.free()
+    small = Buffer.alloc(8)
+    with pytest.raises(ValueError):
+        small.upload(np.zeros(4, np.float32))
+    small.free()
+
+
+def test_jit_exposes_kernel_by_name(device):
+    """The HIP counterpart of ``.entry saxpy`` in the PTX: a code object and
+    a kernel that resolves by name; an unknown name raises."""
+    m = Jit.compile("saxpy", SAXPY_SRC)
+    assert Jit.code_size(m) > 0
+    assert Jit.get_kernel(m, "saxpy")
+    with pytest.raises(RuntimeError):
+        Jit.get_kernel(m, "nope")
+    Jit.unload(m)
+
+
+def test_jit_compile_error_raises(device):
+    with pytest.raises(RuntimeError, match="hiprtc"):
+        Jit.compile("bad", "this is not hip")
+
+
+def test_hand_written_saxpy_end_to_end(device):
+    n = 1000
+    x = np.arange(n, dtype=np.float32)
+    y = (n - np.arange(n)).astype(np.float32)
+    bx, by, bo = Buffer.alloc(4 * n), Buffer.alloc(4 * n), Buffer.alloc(4 * n)
+    bx.upload(x)
+    by.upload(y)
+    m = Jit.compile("saxpy", SAXPY_SRC)
+    Launch.run(Jit.get_kernel(m, "saxpy"), grid=4, block=256, bufs=[bx, by, bo])
+    Device.synchronize()
+    out = np.zeros(n, np.float32)
+    bo.download(out)
+    np.testing.assert_array_equal(out, 2.0 * x + y)
+    for b in (bx, by, bo):
+        b.free()
+    Jit.unload(m)
+
+
+# ---- test_info.ml -----------------------------------------------------------
+
+
+def test_info_fields_and_rendering(device):
+    i = Device.info()
+    assert len(i.name) > 0 and i.arch.startswith("gfx950")
+    assert i.multiprocessors >= 1 and i.total_memory_bytes >= 1 << 30
+    lines = Device.info_to_string(i).strip().split("\n")
+    assert len(lines) == 4
+    assert lines[0].startswith("device: ")
+    assert lines[1] == "compute: %s" % i.arch
+    assert lines[2] == "multiprocessors: %d" % i.multiprocessors
+    assert lines[3] == "memory_mib: %d" % (i.total_memory_bytes // 1048576)
+    assert Device.name() == i.name
+    assert Device.count() >= 1 and Device.current() == 0
+    with Device.with_device(0):
+        assert Device.current() == 0
+
+
+# ---- test_pool.ml (S5) ------------------------------------------------------
+
+
+def test_pool_allocated_at_compile_and_stable_over_50_runs(device):
+    before = Buffer.live_count()
+    c = H.compile(SAXPY)
+    held = H.executor(c).buffer_count()
+    assert held >= 4
+    assert Buffer.live_count() == before + held
+    for k in range(1, 51):
+        s = scalar(H.run(c, inputs(k)), "s")
+        e = expect(k)
+        assert abs(s - e) <= e * 1e-4
+        assert Buffer.live_count() == before + held
+    c.release()
+    assert Buffer.live_count() == before
+
+
+def test_release_idempotent_and_run_after_release_raises(device):
+    before = Buffer.live_count()
+    c = H.compile(SAXPY)
+    c.release()
+    c.release()
+    assert Buffer.live_count() == before
+    with pytest.raises(RuntimeError):
+        H.run(c, inputs(1))
+
+
+def test_two_programs_interleave(device):
+    chain = P.find("chain")
+    c1, c2 = H.compile(SAXPY), H.compile(chain.graph())
+    want = oracle.run(chain.graph(), chain.inputs())
+    for k in range(1, 6):
+        e = expect(k)
+        assert abs(scalar(H.run(c1, inputs(k)), "s") - e) <= e * 1e-4
+        got = H.run(c2, chain.inputs())
+        assert Diff.compare_all(want, got, 1e-4) == (True, None)
+    c1.release()
+    c2.release()
+
+
+def test_outputs_of_successive_runs_are_distinct(device):
+    c = H.compile(SAXPY)
+    o1 = dict(H.run(c, inputs(1)))
+    o2 = dict(H.run(c, inputs(1)))
+    o1["r"][0] = -999.0
+    assert float(o2["r"][0]) == 3.0
+    c.release()
+
+
+def test_missing_input_raises_and_leaks_nothing(device):
+    c = H.compile(SAXPY)
+    live = Buffer.live_count()
+    with pytest.raises(ValueError):
+        H.run(c, [("x", np.arange(N, dtype=np.float32))])
+    with pytest.raises(ValueError):
+        H.run(c, [("x", np.arange(N, dtype=np.float32)), ("y", np.ones(N - 1, np.float32))])
+    assert Buffer.live_count() == live
+    c.release()
+
+
+# ---- test_executor.ml, GPU half ---------------------------------------------
+
+
+def test_executor_runs_twice_with_different_inputs(device):
+    e = P.sum_(100)
+    c = H.compile(e.graph())
+    assert abs(scalar(H.run(c, [("x", np.full(100, 1.0, np.float32))]), "s") - 100.0) <= 1e-3
+    assert abs(scalar(H.run(c, [("x", np.full(100, 2.0, np.float32))]), "s") - 200.0) <= 1e-3
+    c.release()
+
+
+# ---- test_streams.ml (S15/S16) ----------------------------------------------
+
+
+def test_streams_and_events(device):
+    s = Stream.create()
+    e0 = Event.record(Stream.default)
+    e1 = Event.record(s)
+    e1.synchronize()
+    s.synchronize()
+    e0.synchronize()
+    assert s.is_idle()
+    assert Event.elapsed_ms(e0, e1) == Event.elapsed_ms(e0, e1)  # both complete: a number, no error
+    e2 = Event.record(Stream.default)
+    e2.synchronize()
+    assert Event.elapsed_ms(e0, e2) >= 0.0
+
+
+def test_async_jobs_on_three_streams_equal_sync(device):
+    c = H.compile_with(3, SAXPY)
+    jobs = [(k, H.run_async(c, inputs(k))) for k in range(8)]
+    for k, j in jobs:
+        got = dict(H.wait(j))
+        want = dict(H.run(c, inputs(k)))
+        np.testing.assert_array_equal(got["r"], want["r"])
+        assert float(got["s"]) == float(want["s"])
+    j = H.run_async(c, inputs(99))
+    a, b = dict(H.wait(j)), dict(H.wait(j))
+    assert float(a["s"]) == float(b["s"])
+    c.release()
+
+
+def test_resident_roundtrip(device):
+    v = (np.arange(1000) * 0.25).astype(np.float32)
+    r = H.upload(v)
+    assert tuple(r.shape) == (1000,)
+    np.testing.assert_array_equal(H.download(r), v)
+    H.free_resident(r)
+
+
+def test_run_resident_equals_host_run(device):
+    c = H.compile(SAXPY)
+    ins = inputs(3)
+    rx, ry = H.upload(ins[0][1]), H.upload(ins[1][1])
+    outs = dict(H.run_resident(c, [("x", rx), ("y", ry)]))
+    want = dict(H.run(c, ins))
+    rr, rs = outs["r"], outs["s"]
+    assert tuple(rr.shape) == (N,) and tuple(rs.shape) == () and rr.dtype is F32
+    np.testing.assert_array_equal(H.download(rr), want["r"])
+    assert float(H.download(rs)) == float(want["s"])
+    for r in (rx, ry, rr, rs):
+        H.free_resident(r)
+    c.release()
+
+
+def test_resident_chaining_without_host_round_trip(device):
+    before = Buffer.live_count()
+    chain = P.find("chain")
+    gc, gs = chain.graph(), P.sum_(4096).graph()
+    cc, cs = H.compile(gc), H.compile(gs)
+    rx = H.upload(dict(chain.inputs())["x"])
+    r = dict(H.run_resident(cc, [("x", rx)]))["r"]
+    s = dict(H.run_resident(cs, [("x", r)]))["s"]
+    got = float(H.download(s))
+    want = scalar(oracle.run(gs, [("x", dict(oracle.run(gc, chain.inputs()))["r"])]), "s")
+    assert abs(got - want) <= 1e-4 * (1.0 + abs(want))
+    for x in (rx, r, s):
+        H.free_resident(x)
+    cc.release()
+    cs.release()
+    assert Buffer.live_count() == before
+
+
+# ---- test_pinned.ml (S18) ---------------------------------------------------
+
+
+def test_pinned_alloc_is_pinned(device):
+    v = Pinned.alloc(F32, (1000,))
+    assert v.size == 1000
+    v[:] = np.arange(1000)
+    assert float(v[999]) == 999.0
+    assert Pinned.is_pinned(v)
+    assert not Pinned.is_pinned(np.zeros(4, np.float32))
+
+
+def test_pinned_in_and_out_through_a_device_buffer(device):
+    n = 1 << 24
+    src, dst = Pinned.alloc(F32, (n,)), Pinned.alloc(F32, (n,))
+    src[:] = (np.arange(n) & 1023).astype(np.float32)
+    b = Buffer.alloc(src.nbytes)
+    b.upload(src)
+    b.download(dst)
+    b.free()
+    np.testing.assert_array_equal(src, dst)
+
+
+def test_pinned_inputs_through_run_and_run_async(device):
+    x, y = Pinned.alloc(F32, (N,)), Pinned.alloc(F32, (N,))
+    x[:] = np.arange(N)
+    y[:] = 1.0
+    c = H.compile_with(2, SAXPY)
+    s = scalar(H.run(c, [("x", x), ("y", y)]), "s")
+    e = expect(0)
+    assert abs(s - e) <= e * 1e-4
+    jobs = [H.run_async(c, [("x", x), ("y", y)]) for _ in range(4)]
+    for j in jobs:
+        assert scalar(H.wait(j), "s") == s
+    c.release()
+
+
+def test_pinned_memory_is_freed_when_dropped(device):
+    for _ in range(50):
+        Pinned.alloc(F32, (256 * 1024,))
+    import gc
+
+    gc.collect()
+    Pinned.alloc(F32, (256 * 1024,))
+
+
+# ---- S14 --------------------------------------------------------------------
+
+
+def test_s14_bs_greeks_f32_vs_closed_form(device):
+    cf = bs.analytic()
+    c = H.compile(bs.call_greeks(1 << 20, F32))
+    o = H.run(c, bs.inputs(F32, seed=3))
+    c.release()
+
+    def g(w):
+        return bs.scalar_out(o, G.grad_name("price", w))
+
+    assert abs(bs.scalar_out(o, "price") - cf["price"]) <= 0.1
+    assert abs(g("s0") - cf["delta"]) <= 0.01
+    assert abs(g("vol") - cf["vega"]) <= 0.6
+    assert math.isfinite(g("rate"))
