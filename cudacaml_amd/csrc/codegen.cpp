@@ -907,7 +907,7 @@ struct Lowering {
     }
     static const char *helpers[] = {"scan_init",          "scatter_zero",   "scatter_count",  "scatter_colscan",
                                     "scatter_bscan",      "scatter_accumulate", "scatter_reduce", "matmul_ksum",
-                                    "reduce_split_fold"};
+                                    "reduce_split_fold",  "scatter_coarse"};
     int main = ks.back();
     for (int k : ks) {
       bool helper = false;
@@ -1740,194 +1740,256 @@ struct Lowering {
       if (part >= 0) ks.push_back(scatter_reduce(kname, T, acc, part, out, W, B, B));
       return ks;
     }
-    int64_t G = std::min<int64_t>(tune("scatter_chunks", 1024), cdiv(N, 4096));
-    G = std::max<int64_t>(1, G);
-    int64_t C = cdiv(cdiv(N, G), 256) * 256;
-    G = cdiv(N, C);
     int64_t W = std::max<int64_t>(1, std::min<int64_t>(16, tune("scatter_slice_wgs", 2048) / P));
     while (W > 1 && W * P * S * ES > (int64_t(256) << 20)) W--;
-    int cnt = add_buf("t" + id + "_cnt", DT::I32, G * P, BufRole::Scratch);
-    int start = add_buf("t" + id + "_start", DT::I32, P + 1, BufRole::Scratch);
-    int key = add_buf("t" + id + "_key", DT::I32, cdiv(N, 2), BufRole::Scratch);  // 16-bit keys
-    int val = add_buf("t" + id + "_val", n.dt, N, BufRole::Scratch);
     int part = finish(W, P, P * S);
-    std::string sS = std::to_string(S), sB = std::to_string(B), sP = std::to_string(P);
-    std::string bounds = "(unsigned)j < " + sB + "u";
-    auto bounds_of = [&](const std::string &v) { return "(unsigned)" + v + " < " + sB + "u"; };
-    {  // count
+    std::string sB = std::to_string(B);
+    const int64_t TILE = 4096, E = TILE / 256;
+
+    // One partition pass: elements [0, nvalid) of an input stream are
+    // grouped by bucket (j >> SH, PB buckets) into key/val arrays in bucket
+    // order. `jx`/`xx` give the code for element i's index and value;
+    // `check` bounds-checks the index against the bins (first pass only).
+    struct PassIn {
       Params p;
-      add_in(p, fi);
-      p.out.push_back(cnt);
+      std::function<std::string(const std::string &)> jx, xx;
+      std::string nvalid;
+      bool check;
+    };
+    struct PassOut {
+      int cnt, start, key, val;
+    };
+    auto pass = [&](const std::string &sfx, const PassIn &in, int SH, int64_t PB, bool staged, bool final_keys,
+                    const std::string &part_role) {
+      int64_t G = std::max<int64_t>(1, std::min<int64_t>(tune("scatter_chunks", 1024), cdiv(N, 4096)));
+      int64_t C = cdiv(cdiv(N, G), 256) * 256;
+      G = cdiv(N, C);
+      PassOut o;
+      o.cnt = add_buf("t" + id + "_cnt" + sfx, DT::I32, G * PB, BufRole::Scratch);
+      o.start = add_buf("t" + id + "_start" + sfx, DT::I32, PB + 1, BufRole::Scratch);
+      o.key = final_keys ? add_buf("t" + id + "_key" + sfx, DT::I32, cdiv(N, 2), BufRole::Scratch)  // 16-bit keys
+                         : add_buf("t" + id + "_key" + sfx, DT::I32, N, BufRole::Scratch);
+      o.val = add_buf("t" + id + "_val" + sfx, n.dt, N, BufRole::Scratch);
+      const std::string sh = std::to_string(SH), spb = std::to_string(PB);
+      auto bounds = [&](const std::string &v) { return in.check ? "(unsigned)" + v + " < " + sB + "u" : std::string("true"); };
+      auto chunk_head = [&]() {
+        std::ostringstream l;
+        l << "  const int nv_ = " << in.nvalid << ";\n"
+          << "  const int lo = blockIdx.x * " << C << ";\n"
+          << "  const int hi = lo + " << C << " < nv_ ? lo + " << C << " : nv_;\n";
+        return l.str();
+      };
+      // eight strides per iteration: all loads first (clamped to the chunk's
+      // first index), then the bodies under an in-range flag
+      auto loop8 = [&](bool with_val, const std::string &body) {
+        std::ostringstream l;
+        l << "  for (int i0 = lo + (int)threadIdx.x; i0 < hi; i0 += 2048) {\n"
+          << "    int jj[8];\n";
+        if (with_val) l << "    " << T << " xv[8];\n";
+        l << "#pragma unroll\n"
+          << "    for (int u = 0; u < 8; u++) {\n"
+          << "      const int i = i0 + u * 256 < hi ? i0 + u * 256 : lo;\n"
+          << "      jj[u] = " << in.jx("i") << ";\n";
+        if (with_val) l << "      xv[u] = " << in.xx("i") << ";\n";
+        l << "    }\n"
+          << "#pragma unroll\n"
+          << "    for (int u = 0; u < 8; u++) {\n"
+          << "      const bool in = i0 + u * 256 < hi;\n"
+          << "      const int j = jj[u];\n"
+          << body << "    }\n"
+          << "  }\n";
+        return l.str();
+      };
+      auto key_store = [&](const std::string &pos, const std::string &j) {
+        return final_keys ? "keys[" + pos + "] = (unsigned short)(" + j + " & " + std::to_string(S - 1) + ");"
+                          : "keys[" + pos + "] = " + j + ";";
+      };
+      std::string key_decl = final_keys ? "  unsigned short* const keys = (unsigned short*)b" + std::to_string(o.key) + ";\n"
+                                        : "  int* const keys = b" + std::to_string(o.key) + ";\n";
+      {  // count
+        Params p = in.p;
+        p.out.push_back(o.cnt);
+        std::vector<int> args;
+        std::string params = param_list(p, args);
+        std::ostringstream k;
+        k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_count" << sfx << "(" << params << ") {\n"
+          << "  __shared__ int lc[" << PB << "];\n"
+          << "  for (int q = threadIdx.x; q < " << PB << "; q += 256) lc[q] = 0;\n"
+          << "  __syncthreads();\n"
+          << chunk_head()
+          << loop8(false, "      if (in && " + bounds("j") + ") cc_lds_add(&lc[j >> " + sh + "], 1);\n")
+          << "  __syncthreads();\n"
+          << "  for (int q = threadIdx.x; q < " << PB << "; q += 256) b" << o.cnt << "[(size_t)blockIdx.x * " << PB
+          << " + q] = lc[q];\n"
+          << "}\n";
+        src << k.str();
+        ks.push_back(add_kernel(kname + "_count" + sfx, args, (int)G, 256, "scatter_count"));
+      }
+      {  // colscan: per bucket, running offsets over the chunks
+        std::ostringstream k;
+        k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_colscan" << sfx << "(int* __restrict__ b"
+          << o.cnt << ", int* __restrict__ b" << o.start << ") {\n"
+          << "  const int q = blockIdx.x * 256 + threadIdx.x;\n"
+          << "  if (q >= " << PB << ") return;\n"
+          << "  int run = 0;\n"
+          << "  for (int c = 0; c < " << G << "; c++) {\n"
+          << "    const int v = b" << o.cnt << "[(size_t)c * " << PB << " + q];\n"
+          << "    b" << o.cnt << "[(size_t)c * " << PB << " + q] = run;\n"
+          << "    run += v;\n"
+          << "  }\n"
+          << "  b" << o.start << "[q] = run;\n"
+          << "}\n";
+        src << k.str();
+        ks.push_back(add_kernel(kname + "_colscan" + sfx, {o.cnt, o.start}, (int)cdiv(PB, 256), 256, "scatter_colscan"));
+      }
+      {  // bscan: one workgroup, exclusive prefix of the bucket totals
+        int64_t per = cdiv(PB, 256);
+        std::ostringstream k;
+        k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_bscan" << sfx << "(int* __restrict__ b"
+          << o.start << ") {\n"
+          << "  __shared__ int ps[257];\n"
+          << "  const int lo = threadIdx.x * " << per << ";\n"
+          << "  int s = 0;\n"
+          << "  for (int q = lo; q < lo + " << per << " && q < " << PB << "; q++) s += b" << o.start << "[q];\n"
+          << "  ps[threadIdx.x] = s;\n"
+          << "  __syncthreads();\n"
+          << "  if (threadIdx.x == 0) {\n"
+          << "    int run = 0;\n"
+          << "    for (int w = 0; w < 256; w++) { const int v = ps[w]; ps[w] = run; run += v; }\n"
+          << "    ps[256] = run;\n"
+          << "  }\n"
+          << "  __syncthreads();\n"
+          << "  int run = ps[threadIdx.x];\n"
+          << "  for (int q = lo; q < lo + " << per << " && q < " << PB << "; q++) { const int v = b" << o.start
+          << "[q]; b" << o.start << "[q] = run; run += v; }\n"
+          << "  if (threadIdx.x == 0) b" << o.start << "[" << PB << "] = ps[256];\n"
+          << "}\n";
+        src << k.str();
+        ks.push_back(add_kernel(kname + "_bscan" + sfx, {o.start}, 1, 256, "scatter_bscan"));
+      }
+      Params p = in.p;
+      for (int b : {o.cnt, o.start}) p.in.push_back(b);
+      p.out.push_back(o.key);
+      p.out.push_back(o.val);
+      if (in.check) p.err = true;
       std::vector<int> args;
       std::string params = param_list(p, args);
       std::ostringstream k;
-      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_count(" << params << ") {\n"
-        << "  __shared__ int lc[" << P << "];\n"
-        << "  for (int q = threadIdx.x; q < " << P << "; q += 256) lc[q] = 0;\n"
-        << "  __syncthreads();\n"
-        << "  const int lo = blockIdx.x * " << C << ";\n"
-        << "  const int hi = lo + " << C << " < " << N << " ? lo + " << C << " : " << N << ";\n"
-        << chunk_loop(false, "      if (in && " + bounds + ") cc_lds_add(&lc[j >> " + std::to_string(shift) + "], 1);\n")
-        << "  __syncthreads();\n"
-        << "  for (int q = threadIdx.x; q < " << P << "; q += 256) b" << cnt << "[(size_t)blockIdx.x * " << P
-        << " + q] = lc[q];\n"
-        << "}\n";
+      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_partition" << sfx << "(" << params
+        << ") {\n";
+      if (staged) {
+        // each 4096-element tile is grouped by bucket in LDS, then written
+        // as contiguous runs
+        int64_t PP = cdiv(PB, 256);
+        k << "  __shared__ int cur[" << PB << "];\n"
+          << "  __shared__ int tc[" << PB + 1 << "];\n"
+          << "  __shared__ int sj[" << TILE << "];\n"
+          << "  __shared__ " << T << " sx[" << TILE << "];\n"
+          << "  __shared__ int ws[4];\n"
+          << "  for (int q = threadIdx.x; q < " << PB << "; q += 256) cur[q] = b" << o.start << "[q] + b" << o.cnt
+          << "[(size_t)blockIdx.x * " << PB << " + q];\n"
+          << key_decl << chunk_head()
+          << "  for (int t0 = lo; t0 < hi; t0 += " << TILE << ") {\n"
+          << "    for (int q = threadIdx.x; q < " << PB << "; q += 256) tc[q] = 0;\n"
+          << "    int jj[" << E << "], rk[" << E << "];\n"
+          << "    " << T << " xv[" << E << "];\n"
+          << "#pragma unroll\n"
+          << "    for (int u = 0; u < " << E << "; u++) {\n"
+          << "      const int i = t0 + u * 256 + (int)threadIdx.x < hi ? t0 + u * 256 + (int)threadIdx.x : lo;\n"
+          << "      jj[u] = " << in.jx("i") << ";\n"
+          << "      xv[u] = " << in.xx("i") << ";\n"
+          << "    }\n"
+          << "    __syncthreads();\n"
+          << "#pragma unroll\n"
+          << "    for (int u = 0; u < " << E << "; u++) {\n"
+          << "      rk[u] = 0;\n"
+          << "      if (t0 + u * 256 + (int)threadIdx.x >= hi) { jj[u] = -1; continue; }\n"
+          << "      if (" << bounds("jj[u]") << ") rk[u] = atomicAdd(&tc[jj[u] >> " << sh << "], 1);\n"
+          << "      else { " << (in.check ? "cc_flag(err, 2); " : "") << "jj[u] = -1; }\n"
+          << "    }\n"
+          << "    __syncthreads();\n"
+          << "    {\n"
+          << "      int loc[" << PP << "], s = 0;\n"
+          << "#pragma unroll\n"
+          << "      for (int c = 0; c < " << PP << "; c++) {\n"
+          << "        const int q = threadIdx.x * " << PP << " + c;\n"
+          << "        loc[c] = s;\n"
+          << "        s += q < " << PB << " ? tc[q] : 0;\n"
+          << "      }\n"
+          << "      int tot;\n"
+          << "      const int base = cc_wg_exscan(s, ws, &tot);\n"
+          << "#pragma unroll\n"
+          << "      for (int c = 0; c < " << PP << "; c++) {\n"
+          << "        const int q = threadIdx.x * " << PP << " + c;\n"
+          << "        if (q < " << PB << ") tc[q] = base + loc[c];\n"
+          << "      }\n"
+          << "      if (threadIdx.x == 0) tc[" << PB << "] = tot;\n"
+          << "    }\n"
+          << "    __syncthreads();\n"
+          << "#pragma unroll\n"
+          << "    for (int u = 0; u < " << E << "; u++)\n"
+          << "      if (jj[u] >= 0) {\n"
+          << "        const int slot = tc[jj[u] >> " << sh << "] + rk[u];\n"
+          << "        sj[slot] = jj[u];\n"
+          << "        sx[slot] = xv[u];\n"
+          << "      }\n"
+          << "    __syncthreads();\n"
+          << "    for (int s = threadIdx.x; s < tc[" << PB << "]; s += 256) {\n"
+          << "      const int j = sj[s], q = j >> " << sh << ";\n"
+          << "      const int pos = cur[q] + (s - tc[q]);\n"
+          << "      " << key_store("pos", "j") << "\n"
+          << "      b" << o.val << "[pos] = sx[s];\n"
+          << "    }\n"
+          << "    __syncthreads();\n"
+          << "    for (int q = threadIdx.x; q < " << PB << "; q += 256) cur[q] += tc[q + 1] - tc[q];\n"
+          << "    __syncthreads();\n"
+          << "  }\n";
+      } else {
+        k << "  __shared__ int cur[" << PB << "];\n"
+          << "  for (int q = threadIdx.x; q < " << PB << "; q += 256) cur[q] = b" << o.start << "[q] + b" << o.cnt
+          << "[(size_t)blockIdx.x * " << PB << " + q];\n"
+          << "  __syncthreads();\n"
+          << key_decl << chunk_head()
+          << loop8(true, "      if (in && " + bounds("j") + ") {\n"
+                         "        const int pos = atomicAdd(&cur[j >> " + sh + "], 1);\n"
+                         "        " + key_store("pos", "j") + "\n"
+                         "        b" + std::to_string(o.val) + "[pos] = xv[u];\n"
+                         "      }" + (in.check ? " else if (in) cc_flag(err, 2);" : "") + "\n");
+      }
+      k << "}\n";
       src << k.str();
-      ks.push_back(add_kernel(kname + "_count", args, (int)G, 256, "scatter_count"));
+      ks.push_back(add_kernel(kname + "_partition" + sfx, args, (int)G, 256, part_role));
+      return o;
+    };
+
+    PassIn first;
+    add_in(first.p, fi);
+    add_in(first.p, fs);
+    first.jx = [&](const std::string &i) { return fi.call_scalar(i); };
+    first.xx = [&](const std::string &i) { return fs.call_scalar(i); };
+    first.nvalid = std::to_string(N);
+    first.check = true;
+    const int64_t STAGE_P = tune("scatter_stage_p", 512);
+    PassOut fin;
+    if (P <= STAGE_P) {
+      fin = pass("", first, shift, P, true, true, "scatter_partition");
+    } else if (!tune("scatter_two_level", 1)) {
+      fin = pass("", first, shift, P, false, true, "scatter_partition");  // single level, element-wise stores
+    } else {
+      // Two levels: a coarse pass into super-slices of 64 slices (runs of
+      // about 64 elements per tile), then the slice pass over the coarse
+      // output, whose tiles each touch at most two super-slices.
+      const int64_t P1 = cdiv(P, 64);
+      PassOut c1 = pass("1", first, shift + 6, P1, true, false, "scatter_coarse");
+      PassIn second;
+      for (int b : {c1.key, c1.val, c1.start}) second.p.in.push_back(b);
+      second.jx = [&, c1](const std::string &i) { return "b" + std::to_string(c1.key) + "[" + i + "]"; };
+      second.xx = [&, c1](const std::string &i) { return "b" + std::to_string(c1.val) + "[" + i + "]"; };
+      second.nvalid = "b" + std::to_string(c1.start) + "[" + std::to_string(P1) + "]";
+      second.check = false;
+      fin = pass("", second, shift, P, true, true, "scatter_partition");
     }
-    {  // colscan: per slice, running offsets over the chunks
-      std::ostringstream k;
-      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_colscan(int* __restrict__ b" << cnt
-        << ", int* __restrict__ b" << start << ") {\n"
-        << "  const int q = blockIdx.x * 256 + threadIdx.x;\n"
-        << "  if (q >= " << P << ") return;\n"
-        << "  int run = 0;\n"
-        << "  for (int c = 0; c < " << G << "; c++) {\n"
-        << "    const int v = b" << cnt << "[(size_t)c * " << P << " + q];\n"
-        << "    b" << cnt << "[(size_t)c * " << P << " + q] = run;\n"
-        << "    run += v;\n"
-        << "  }\n"
-        << "  b" << start << "[q] = run;\n"
-        << "}\n";
-      src << k.str();
-      ks.push_back(add_kernel(kname + "_colscan", {cnt, start}, (int)cdiv(P, 256), 256, "scatter_colscan"));
-    }
-    {  // bscan: one workgroup, exclusive prefix of the slice totals
-      int64_t per = cdiv(P, 256);
-      std::ostringstream k;
-      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_bscan(int* __restrict__ b" << start
-        << ") {\n"
-        << "  __shared__ int ps[257];\n"
-        << "  const int lo = threadIdx.x * " << per << ";\n"
-        << "  int s = 0;\n"
-        << "  for (int q = lo; q < lo + " << per << " && q < " << P << "; q++) s += b" << start << "[q];\n"
-        << "  ps[threadIdx.x] = s;\n"
-        << "  __syncthreads();\n"
-        << "  if (threadIdx.x == 0) {\n"
-        << "    int run = 0;\n"
-        << "    for (int w = 0; w < 256; w++) { const int v = ps[w]; ps[w] = run; run += v; }\n"
-        << "    ps[256] = run;\n"
-        << "  }\n"
-        << "  __syncthreads();\n"
-        << "  int run = ps[threadIdx.x];\n"
-        << "  for (int q = lo; q < lo + " << per << " && q < " << P << "; q++) { const int v = b" << start
-        << "[q]; b" << start << "[q] = run; run += v; }\n"
-        << "  if (threadIdx.x == 0) b" << start << "[" << P << "] = ps[256];\n"
-        << "}\n";
-      src << k.str();
-      ks.push_back(add_kernel(kname + "_bscan", {start}, 1, 256, "scatter_bscan"));
-    }
-    const int64_t STAGE_P = tune("scatter_stage_p", 512), TILE = 4096, E = TILE / 256;
-    if (P <= STAGE_P) {  // partition, staged: each 4096-element tile is grouped by slice in LDS
-      Params p;
-      add_in(p, fi);
-      add_in(p, fs);
-      for (int b : {cnt, start}) p.in.push_back(b);
-      p.out.push_back(key);
-      p.out.push_back(val);
-      p.err = true;
-      std::vector<int> args;
-      std::string params = param_list(p, args);
-      int64_t PP = cdiv(P, 256);
-      std::string sh = std::to_string(shift);
-      std::ostringstream k;
-      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_partition(" << params << ") {\n"
-        << "  __shared__ int cur[" << P << "];\n"
-        << "  __shared__ int tc[" << P + 1 << "];\n"
-        << "  __shared__ int sj[" << TILE << "];\n"
-        << "  __shared__ " << T << " sx[" << TILE << "];\n"
-        << "  __shared__ int ws[4];\n"
-        << "  for (int q = threadIdx.x; q < " << P << "; q += 256) cur[q] = b" << start << "[q] + b" << cnt
-        << "[(size_t)blockIdx.x * " << P << " + q];\n"
-        << "  unsigned short* const keys = (unsigned short*)b" << key << ";\n"
-        << "  const int lo = blockIdx.x * " << C << ";\n"
-        << "  const int hi = lo + " << C << " < " << N << " ? lo + " << C << " : " << N << ";\n"
-        << "  for (int t0 = lo; t0 < hi; t0 += " << TILE << ") {\n"
-        << "    for (int q = threadIdx.x; q < " << P << "; q += 256) tc[q] = 0;\n"
-        << "    int jj[" << E << "], rk[" << E << "];\n"
-        << "    " << T << " xx[" << E << "];\n"
-        << "#pragma unroll\n"
-        << "    for (int u = 0; u < " << E << "; u++) {\n"
-        << "      const int i = t0 + u * 256 + (int)threadIdx.x < hi ? t0 + u * 256 + (int)threadIdx.x : lo;\n"
-        << "      jj[u] = " << fi.call_scalar("i") << ";\n"
-        << "      xx[u] = " << fs.call_scalar("i") << ";\n"
-        << "    }\n"
-        << "    __syncthreads();\n"
-        << "#pragma unroll\n"
-        << "    for (int u = 0; u < " << E << "; u++) {\n"
-        << "      rk[u] = 0;\n"
-        << "      if (t0 + u * 256 + (int)threadIdx.x >= hi) { jj[u] = -1; continue; }\n"
-        << "      if (" << bounds_of("jj[u]") << ") rk[u] = atomicAdd(&tc[jj[u] >> " << sh << "], 1);\n"
-        << "      else { cc_flag(err, 2); jj[u] = -1; }\n"
-        << "    }\n"
-        << "    __syncthreads();\n"
-        << "    {\n"
-        << "      int loc[" << PP << "], s = 0;\n"
-        << "#pragma unroll\n"
-        << "      for (int c = 0; c < " << PP << "; c++) {\n"
-        << "        const int q = threadIdx.x * " << PP << " + c;\n"
-        << "        loc[c] = s;\n"
-        << "        s += q < " << P << " ? tc[q] : 0;\n"
-        << "      }\n"
-        << "      int tot;\n"
-        << "      const int base = cc_wg_exscan(s, ws, &tot);\n"
-        << "#pragma unroll\n"
-        << "      for (int c = 0; c < " << PP << "; c++) {\n"
-        << "        const int q = threadIdx.x * " << PP << " + c;\n"
-        << "        if (q < " << P << ") tc[q] = base + loc[c];\n"
-        << "      }\n"
-        << "      if (threadIdx.x == 0) tc[" << P << "] = tot;\n"
-        << "    }\n"
-        << "    __syncthreads();\n"
-        << "#pragma unroll\n"
-        << "    for (int u = 0; u < " << E << "; u++)\n"
-        << "      if (jj[u] >= 0) {\n"
-        << "        const int slot = tc[jj[u] >> " << sh << "] + rk[u];\n"
-        << "        sj[slot] = jj[u];\n"
-        << "        sx[slot] = xx[u];\n"
-        << "      }\n"
-        << "    __syncthreads();\n"
-        << "    for (int s = threadIdx.x; s < tc[" << P << "]; s += 256) {\n"
-        << "      const int j = sj[s], q = j >> " << sh << ";\n"
-        << "      const int pos = cur[q] + (s - tc[q]);\n"
-        << "      keys[pos] = (unsigned short)(j & " << S - 1 << ");\n"
-        << "      b" << val << "[pos] = sx[s];\n"
-        << "    }\n"
-        << "    __syncthreads();\n"
-        << "    for (int q = threadIdx.x; q < " << P << "; q += 256) cur[q] += tc[q + 1] - tc[q];\n"
-        << "    __syncthreads();\n"
-        << "  }\n"
-        << "}\n";
-      src << k.str();
-      ks.push_back(add_kernel(kname + "_partition", args, (int)G, 256, "scatter_partition"));
-    } else {  // partition
-      Params p;
-      add_in(p, fi);
-      add_in(p, fs);
-      for (int b : {cnt, start}) p.in.push_back(b);
-      p.out.push_back(key);
-      p.out.push_back(val);
-      p.err = true;
-      std::vector<int> args;
-      std::string params = param_list(p, args);
-      std::ostringstream k;
-      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_partition(" << params << ") {\n"
-        << "  __shared__ int cur[" << P << "];\n"
-        << "  for (int q = threadIdx.x; q < " << P << "; q += 256) cur[q] = b" << start << "[q] + b" << cnt
-        << "[(size_t)blockIdx.x * " << P << " + q];\n"
-        << "  __syncthreads();\n"
-        << "  unsigned short* const keys = (unsigned short*)b" << key << ";\n"
-        << "  const int lo = blockIdx.x * " << C << ";\n"
-        << "  const int hi = lo + " << C << " < " << N << " ? lo + " << C << " : " << N << ";\n"
-        << chunk_loop(true, "      if (in && " + bounds + ") {\n"
-                            "        const int pos = atomicAdd(&cur[j >> " + std::to_string(shift) + "], 1);\n"
-                            "        keys[pos] = (unsigned short)(j & " + std::to_string(S - 1) + ");\n"
-                            "        b" + std::to_string(val) + "[pos] = xx[u];\n"
-                            "      } else if (in) cc_flag(err, 2);\n")
-        << "}\n";
-      src << k.str();
-      ks.push_back(add_kernel(kname + "_partition", args, (int)G, 256, "scatter_partition"));
-    }
+    const int start = fin.start, key = fin.key, val = fin.val;
     {  // accumulate
       int dst = part >= 0 ? part : out;
       std::ostringstream k;

@@ -176,6 +176,20 @@ def test_scatter_paths(device, n, bins, dtype, tpl):
     check(g, [("idx", scatter_idx(3, n, bins)), ("src", data(dtype, (n,), 4))], tpl)
 
 
+@pytest.mark.parametrize("dtype,tune", [(I32, ""), (F32, ""), (I32, "scatter_two_level=0"), (F64, "")])
+def test_scatter_permutation_two_level(device, dtype, tune, monkeypatch):
+    """Collision-free indices over more than 512 slices: a coarse pass into
+    super-slices, then the slice pass (or, with scatter_two_level=0, one
+    pass with element-wise stores)."""
+    monkeypatch.setenv("CCHIP_TUNE", tune)
+    n, bins = 1 << 22, 1 << 23
+    g = scatter_graph(n, bins, dtype)
+    t = templates(g)
+    assert ("scatter_coarse" in t) == (tune == "")
+    idx = (C.permutation(31, bins)[:n]).astype(np.int32)
+    check(g, [("idx", idx), ("src", data(dtype, (n,), 32))], ["scatter_partition", "scatter_accumulate"])
+
+
 @pytest.mark.parametrize("dtype", [F32, I32])
 def test_scatter_atomic_path(device, dtype, monkeypatch):
     """The global-atomic template, still used where the slices would not
@@ -211,7 +225,7 @@ def test_scatter_fused_operands(device):
     check(g, [("i", scatter_idx(9, n, bins)), ("x", data(F32, (n,), 10))], ["scatter_partition"])
 
 
-@pytest.mark.parametrize("bins", [4, 50000])
+@pytest.mark.parametrize("bins", [4, 50000, 1 << 23])
 def test_scatter_partition_out_of_range_raises(device, bins):
     n = 20000
     idx = scatter_idx(11, n, bins)
