@@ -2130,6 +2130,11 @@ struct Lowering {
     if (dt == DT::F64) return tune("mm_f64_bm", 64) == 128 ? 128 : 64;
     return 128;
   }
+  // k-tile depth: 16, or 32 where K allows it and the knob asks for it.
+  static int64_t mfma_bk(DT dt, int64_t K) {
+    int64_t want = tune(dt == DT::F64 ? "mm_f64_bk" : "mm_bk", 16);
+    return want == 32 && K % 32 == 0 ? 32 : 16;
+  }
 
   // ---- Matmul on the matrix cores ------------------------------------------
   // f32: v_mfma_f32_32x32x2f32, block tile 128x128x16, four waves of 64x64.
@@ -2151,15 +2156,17 @@ struct Lowering {
     bool f64 = n.dt == DT::F64;
     std::string T = dt_ctype(n.dt);
     int out = buf_of[t];
-    const int64_t BM = mfma_bm(n.dt), BK = 16, MT = f64 ? 16 : 32;
+    const int64_t BM = mfma_bm(n.dt), BK = mfma_bk(n.dt, K), MT = f64 ? 16 : 32;
     const int64_t G = 64 / MT;    // lane groups along k
     const int64_t S = BK / G;     // k steps per tile held by one lane
     const int64_t WT = BM / 2;    // wave tile
     const int64_t RT = WT / MT;   // instruction tiles per wave side
     const int64_t VEC = 16 / dt_size(n.dt);        // elements per 16-byte access
     const int64_t PER = BM * BK / 256;             // elements per thread per operand tile
-    const int64_t KP = BK + VEC;                   // k-contiguous row stride (keeps 16-byte alignment)
-    const int64_t MP = BM + VEC;                   // mn-contiguous row stride
+    // row strides padded by whole 16-byte vectors (alignment kept); the pads
+    // spread rows over LDS banks
+    const int64_t KP = BK + VEC * std::max<int64_t>(0, tune("mm_kpad", 1));  // k-contiguous row stride
+    const int64_t MP = BM + VEC * std::max<int64_t>(0, tune("mm_mpad", 1));  // mn-contiguous row stride
     // Operand modes: 0 direct buffer, 1 transpose of a buffer, 2 fused expression.
     struct Opnd {
       int mode;
@@ -2298,7 +2305,8 @@ struct Lowering {
     // Two-level accumulation (f32): the matrix cores sum KC-deep chunks into
     // `acc`, which is folded into `tot` with plain adds and cleared. Error
     // then grows with sqrt(KC) + sqrt(K / KC) instead of sqrt(K).
-    int64_t KCT = f64 ? 0 : tune("mm_chunk_tiles", 4);
+    // chunks of mm_chunk_k (64 by default) k values
+    int64_t KCT = f64 ? 0 : std::max<int64_t>(0, tune("mm_chunk_k", 64) / BK);
     if (KCT > 0 && (K / BK) % KCT != 0) KCT = 0;
     if (KCT > 0)
       k << "  " << accT << " tot[" << RT << "][" << RT << "];\n"
@@ -2452,7 +2460,7 @@ struct Lowering {
     if (M == 0 || N == 0) return {};
     if (dt_is_float(n.dt) && K > 0 && tune("mm_mfma", 1)) {
       int64_t BM = mfma_bm(n.dt);
-      if (M % BM == 0 && N % BM == 0 && K % 16 == 0) return lower_matmul_mfma(t, M, N, K);
+      if (M % BM == 0 && N % BM == 0 && K % mfma_bk(n.dt, K) == 0) return lower_matmul_mfma(t, M, N, K);
     }
     ElemFn fa = gen.element_fn("fa_" + id, n.a, false, false);
     ElemFn fb = gen.element_fn("fb_" + id, n.b, false, false);

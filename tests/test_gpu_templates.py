@@ -12,6 +12,7 @@ from cudacaml_amd import backend_hip as H
 from cudacaml_amd import differential as Diff
 from cudacaml_amd import dsl as D
 from cudacaml_amd.examples import configs as C
+from cudacaml_amd.examples import programs as P
 from cudacaml_amd.ir import F32, F64, I32, I64, Graph
 
 pytestmark = pytest.mark.gpu
@@ -261,3 +262,40 @@ def test_scatter_out_of_range_raises(device):
     with pytest.raises(ValueError, match="scatter_add index out of bounds"):
         H.run(c, [("i", np.array([0, 1, -1, 2], np.int32)), ("s", np.ones(4, np.int32))])
     c.release()
+
+
+KNOB_CASES = [
+    # (knob setting, graph builder, inputs builder, template that must appear)
+    ("lb_window=4", lambda: Graph.create("s", [("p", D.scan_rows(D.add, D.const(I32, 3), D.param("x", I32, (3, 300001))))]),
+     lambda: [("x", data(I32, (3, 300001), 41))], "scan_lookback"),
+    # long look-back scans use exact types: a tree-ordered f32 prefix sum of
+    # this length and the interpreter's sequential one differ by more than
+    # the 1e-4 band near zero, whichever is closer to the exact sum
+    ("lb_window=2,lb_slices4=8", lambda: Graph.create("s", [("p", D.scan_rows(D.add, D.const(I32, 0), D.param("x", I32, (2, 200003))))]),
+     lambda: [("x", data(I32, (2, 200003), 42))], "scan_lookback"),
+    ("lb_slices8=4", lambda: Graph.create("s", [("p", D.scan_rows(D.add, D.const(I64, 0), D.param("x", I64, (2, 100003))))]),
+     lambda: [("x", data(I64, (2, 100003), 56))], "scan_lookback"),
+    ("mm_bk=32,mm_chunk_k=0", lambda: C.matmul(256, F32, k=512, m=128),
+     lambda: [("a", data(F32, (128, 512), 43)), ("b", data(F32, (512, 256), 44))], "matmul_mfma_f32_a0b0"),
+    ("mm_f64_bm=128,mm_f64_bk=32", lambda: C.matmul(256, F64, k=128, m=256),
+     lambda: [("a", data(F64, (256, 128), 45)), ("b", data(F64, (128, 256), 46))], "matmul_mfma_f64_a0b0"),
+    ("mm_kpad=3,mm_mpad=2", lambda: C.matmul_grad(256, F32),
+     lambda: [("a", data(F32, (256, 256), 47)), ("b", data(F32, (256, 256), 48))], "matmul_mfma_f32_a1b0"),
+    ("mm_mfma=0", lambda: C.matmul(128, F32, k=64, m=128),
+     lambda: [("a", data(F32, (128, 64), 49)), ("b", data(F32, (64, 128), 50))], "matmul_tiled"),
+    ("map_nt=2", lambda: P.chain(5000).graph(), lambda: P.chain(5000).inputs(), "map"),
+    ("scatter_slice_bins=16384", lambda: scatter_graph(300001, 70000, F32),
+     lambda: [("idx", scatter_idx(51, 300001, 70000)), ("src", data(F32, (300001,), 52))], "scatter_partition"),
+    ("rs_bytes=8192,rs_groups=64", lambda: C.rows(1024, 3000),
+     lambda: [("x", data(F32, (1024, 3000), 53))], "scan_rowseq"),
+    ("mm_splitk_groups=7", lambda: C.matmul(3, F64, k=65536, m=3),
+     lambda: [("a", data(F64, (3, 65536), 54)), ("b", data(F64, (65536, 3), 55))], "matmul_splitk"),
+]
+
+
+@pytest.mark.parametrize("knob,graph,inputs,tpl", KNOB_CASES, ids=[c[0] for c in KNOB_CASES])
+def test_tuning_knobs_keep_results(device, monkeypatch, knob, graph, inputs, tpl):
+    """A CCHIP_TUNE setting changes launch shapes or tiling, never what is
+    computed: every non-default path against the oracle."""
+    monkeypatch.setenv("CCHIP_TUNE", knob)
+    check(graph(), inputs(), [tpl])
