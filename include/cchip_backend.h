@@ -4,9 +4,11 @@
  * the extensions Backend_cuda adds (lib/backend_cuda/cudacaml_backend_cuda.mli
  * :7-84), as a C-ABI.
  *
- * A graph crosses the boundary as the text wire format written by
- * cudacaml_amd/ir.py (an OCaml caller prints the same text from a Graph.t;
- * see INTEGRATION.md). compile runs the fusion plan, instantiates the CDNA4
+ * A graph crosses the boundary as the text wire format "cchip-graph 1"
+ * (cudacaml_amd/ir.py writes it; an OCaml caller prints the same text from
+ * a Graph.t): one line per expression node ("x"), per tensor node in
+ * topological order ("t"), per output ("o"), then "end". compile runs the
+ * fusion plan, instantiates the CDNA4
  * kernel templates, JITs them with hiprtc and allocates the executor pools;
  * run walks the host plan (upload, launch, download) on the executor's
  * stream.

@@ -2,8 +2,8 @@
  * cchip runtime: the C-ABI that replaces CUDACaml's lib/runtime (which sits
  * on cudajit -> libcuda + libnvrtc) with one over the HIP module API and
  * hiprtc, for gfx950 only. One function per value of the OCaml runtime
- * interface; an OCaml `lib/runtime` rewrite binds these with ctypes (see
- * INTEGRATION.md). Plain pointers and sizes only.
+ * interface; an OCaml `lib/runtime` rewrite binds these with ctypes.
+ * Plain pointers and sizes only.
  *
  * Every function that can fail returns a status:
  *   CCHIP_OK (0), CCHIP_INVALID_ARGUMENT (1) for caller mistakes (the
