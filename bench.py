@@ -10,8 +10,12 @@ programs over inputs already resident in HBM (run_resident_into, outputs
 preallocated, no host traffic). ``value`` is algorithmic bytes per second
 over the K timed steps (each materialised input read once, each output
 written once, per kernel of the plan). Other configs (``--config saxpy``,
-``chain``, ``scatter``, ``gather``, ``matmul``, ``matmul64``, ``matmul_grad``,
-``mc``, ``mc64``) print their own line in the same format.
+``chain``, ``scatter``, ``scatter_perm``, ``matmul``, ``matmul64``, ``matmul_grad``,
+``mc``, ``mc64``, ``mc_greeks``) print their own line in the same format.
+``bs``, ``bs_greeks`` (and their f64 ``bs64``, ``bs_greeks64``) are the
+reference's S20 timing row: the one-step Black-Scholes price and its
+Greeks adjoint at 2^22 paths; their ``whole_run`` is timed as S20 times it
+and set against the published A100 figure.
 
 The JSON line also carries ``roofline`` for the dominant kernel (its
 algorithmic bytes or flops per launch over its mean launch time, timed with
@@ -148,7 +152,23 @@ def build_workload(name, H, C):
         return Workload(name, progs, "paths/s", dt.name,
                         "config5: BS MC %s 2^22 paths x 64 steps %s" % ("greeks" if name == "mc_greeks" else "price",
                                                                         dt.name))
+    if name in BS_CONFIGS:
+        dt = F64 if name.endswith("64") else F32
+        greeks = name.startswith("bs_greeks")
+        g = bs.call_greeks(C.PATHS5, dt) if greeks else bs.call_mc(C.PATHS5, dt)
+        ins = [(k, H.upload(v)) for k, v in bs.inputs(dt, seed=1)]
+        add(g, ins)
+        return Workload(name, progs, "paths/s", dt.name,
+                        "BS MC %s, one step, 2^22 paths %s (the reference's S20 timing row)"
+                        % ("Greeks adjoint (delta, vega, rho)" if greeks else "price", dt.name))
     raise SystemExit("unknown config %s" % name)
+
+
+# The reference's published S20 row (README.md:152-157): Backend_cuda.run of
+# Bs.call_mc / Bs.call_greeks at 2^22 paths, f32, on an A100-SXM4-40GB,
+# mean of 5 warm runs, host inputs to host outputs.
+BS_CONFIGS = ("bs", "bs64", "bs_greeks", "bs_greeks64")
+BS_PUBLISHED_MS = {"bs": 0.2, "bs_greeks": 0.7}
 
 
 def step(H, w, sync=False):
@@ -301,12 +321,22 @@ def dominant(H, w, config, timed=True):
     return (dom,) + kinfo[dom] + (kinfo,)
 
 
-def whole_run_ms(H, w, reps=3):
-    """Median time of a synchronous run from host arrays: upload, launches,
-    download (pageable host memory, as Executor.run)."""
+def whole_run_ms(H, w, reps=3, mean=False):
+    """Time of a synchronous run from host arrays: upload, launches,
+    download (pageable host memory, as Executor.run); the median of
+    ``reps`` runs, or after one warm run their mean (the reference's S20
+    timing, test_system.ml:225-245)."""
     import statistics
 
     hosts = [(c, [(n, H.download(r)) for n, r in ins]) for _, c, ins, _ in w.programs]
+    if mean:
+        for c, ins in hosts:
+            H.run(c, ins)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            for c, ins in hosts:
+                H.run(c, ins)
+        return (time.perf_counter() - t0) * 1e3 / reps
     ts = []
     for _ in range(reps):
         t0 = time.perf_counter()
@@ -408,7 +438,18 @@ def main():
     roof["traffic_detail"] = traffic_detail
 
     whole = None
-    if not args.no_whole_run:
+    vs_baseline, vs_basis = None, None
+    if args.config in BS_CONFIGS:
+        ms = whole_run_ms(H, w, reps=5, mean=True)
+        whole = {"ms": round(ms, 4),
+                 "what": "host scalars in, host scalars out: run after one warm run, mean of 5 (as S20)"}
+        if args.config in BS_PUBLISHED_MS:
+            pub = BS_PUBLISHED_MS[args.config]
+            whole["published_a100_ms"] = pub
+            vs_baseline = round(pub / ms, 3)
+            vs_basis = ("whole-run paths/s against the reference's published A100 S20 time "
+                        "(%.1f ms, README.md:152-157); same graph, size and timing method" % pub)
+    elif not args.no_whole_run:
         whole = {"ms": round(whole_run_ms(H, w), 2),
                  "what": "host arrays in, host arrays out: upload + kernels + download, pageable memory"}
 
@@ -428,7 +469,7 @@ def main():
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
-        "vs_baseline": None,
+        "vs_baseline": vs_baseline,
         "dtype": w.dtype,
         "data": "synthetic (Philox-4x32-10 inputs generated on the device)",
         "config": {"workload": w.describe, "parallelism": "single GPU", "algorithmic_bytes_per_step": total_bytes},
@@ -436,6 +477,8 @@ def main():
         "cpu_baseline": cpu,
         "whole_run": whole,
     }
+    if vs_basis:
+        line["vs_baseline_basis"] = vs_basis
     print(json.dumps(line), flush=True)
 
 

@@ -988,6 +988,12 @@ struct Lowering {
     int64_t S = W + 4;               // row stride keeps 4-element groups 16-byte aligned
     int64_t CH = std::min<int64_t>(16, W);
     bool vec = len % 4 == 0;
+    // Streaming (non-temporal) accesses, a bit mask: 1 a scan's stores,
+    // 2 a reduction's loads, 4 a scan's loads.
+    int64_t rs_nt = n.dt == DT::BOOL ? 0 : tune("rs_nt", 5);
+    for (int b : f.ident)
+      if (prog.bufs[b].dt == DT::BOOL) rs_nt &= 1;
+    const bool nt_loads = (rs_nt & (scan ? 4 : 2)) != 0, nt_stores = scan && (rs_nt & 1);
     Params p;
     add_in(p, f);
     p.out.push_back(out);
@@ -1018,7 +1024,7 @@ struct Lowering {
       // behind a branch, so a thread's loads are all in flight together.
       if (vec) {
         l << "          const int i = row * " << len << " + (c0 + j < " << len << " ? c0 + j : 0);\n"
-          << vec_loads(f, "i", "          ", tyof());
+          << vec_loads(f, "i", "          ", tyof(), nt_loads);
         for (int c = 0; c < 4; c++) l << "          rg[4 * u + " << c << "] = " << lane_call(f, "i", c) << ";\n";
       } else {
         for (int c = 0; c < 4; c++)
@@ -1086,7 +1092,10 @@ struct Lowering {
         << "          const int i = row * " << len << " + c0 + j;\n"
         << "          const " << V4 << " o = sm4[(rr * " << S << " + j) / 4];\n";
       if (vec) {
-        k << "          if (c0 + j < " << len << ") *(" << V4 << "*)(b" << out << " + i) = o;\n";
+        if (nt_stores)
+          k << "          if (c0 + j < " << len << ") cc_st4_nt(b" << out << " + i, o);\n";
+        else
+          k << "          if (c0 + j < " << len << ") *(" << V4 << "*)(b" << out << " + i) = o;\n";
       } else {
         for (int c = 0; c < 4; c++)
           k << "          if (c0 + j + " << c << " < " << len << ") b" << out << "[i + " << c << "] = o." << comp[c]
@@ -1442,6 +1451,10 @@ struct Lowering {
       rep("VAL", val);
       return r;
     };
+    // Streaming (non-temporal) accesses, a bit mask: 1 stores, 2 loads.
+    int64_t scan_nt = n.dt == DT::BOOL ? 0 : tune("scan_nt", 3);
+    for (int b : f.ident)
+      if (prog.bufs[b].dt == DT::BOOL) scan_nt &= ~int64_t(2);
     static const char *comp[] = {"x", "y", "z", "w"};
     std::ostringstream k;
     k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params;
@@ -1471,7 +1484,7 @@ struct Lowering {
     if (vec) {
       k << "    const bool ok = e < tl;\n"
         << "    const int i = base + (ok ? e : 0);\n"
-        << vec_loads(f, "i", "    ", tyof());
+        << vec_loads(f, "i", "    ", tyof(), (scan_nt & 2) != 0);
       for (int c = 0; c < 4; c++)
         k << "    v[u][" << c << "] = ok ? " << lane_call(f, "i", c) << " : " << ini << "();\n";
     } else {
@@ -1630,8 +1643,11 @@ struct Lowering {
       k << "    if (e < tl) {\n"
         << "      cc_v4<" << T << "> o;\n";
       for (int c = 0; c < 4; c++) k << "      o." << comp[c] << " = v[u][" << c << "];\n";
-      k << "      *(cc_v4<" << T << ">*)(b" << out << " + base + e) = o;\n"
-        << "    }\n";
+      if (scan_nt & 1)
+        k << "      cc_st4_nt(b" << out << " + base + e, o);\n";
+      else
+        k << "      *(cc_v4<" << T << ">*)(b" << out << " + base + e) = o;\n";
+      k << "    }\n";
     } else {
       for (int c = 0; c < 4; c++)
         k << "    if (e + " << c << " < tl) b" << out << "[base + e + " << c << "] = v[u][" << c << "];\n";

@@ -16,7 +16,7 @@ from cudacaml_amd import grad as G
 from cudacaml_amd.examples import black_scholes as bs
 from cudacaml_amd.examples import programs as P
 from cudacaml_amd.examples import saxpy as sx
-from cudacaml_amd.ir import F32, Graph
+from cudacaml_amd.ir import F32, F64, Graph
 from cudacaml_amd.runtime import Buffer, Device, Event, Jit, Launch, Pinned, Stream
 
 pytestmark = pytest.mark.gpu
@@ -334,3 +334,34 @@ def test_s14_bs_greeks_f32_vs_closed_form(device):
     assert abs(g("s0") - cf["delta"]) <= 0.01
     assert abs(g("vol") - cf["vega"]) <= 0.6
     assert math.isfinite(g("rate"))
+
+
+# ---- S20 --------------------------------------------------------------------
+
+
+def test_s20_timing_table(device, capsys):
+    """The reference's S20 row (test_system.ml:225-245): the one-step price
+    and its Greeks adjoint at 2^22 paths, f32 and f64, each run once warm
+    and then timed as the mean of 5 host-to-host runs. Informational, as
+    there; the prices are checked against the closed form."""
+    import time
+
+    n = 1 << 22
+    cf = bs.analytic()
+    rows = []
+    for dt in (F32, F64):
+        ins = bs.inputs(dt, seed=1)
+        times = []
+        for g in (bs.call_mc(n, dt), bs.call_greeks(n, dt)):
+            c = H.compile(g)
+            o = H.run(c, ins)
+            t0 = time.perf_counter()
+            for _ in range(5):
+                o = H.run(c, ins)
+            times.append((time.perf_counter() - t0) / 5.0)
+            c.release()
+            assert abs(bs.scalar_out(o, "price") - cf["price"]) <= 0.1
+        rows.append((dt.name, times[0], times[1]))
+    with capsys.disabled():
+        for name, tp, tg in rows:
+            print("\n    %s  price %.3f ms   greeks %.3f ms   ratio %.2fx" % (name, tp * 1e3, tg * 1e3, tg / tp))

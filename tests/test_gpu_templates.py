@@ -290,6 +290,13 @@ KNOB_CASES = [
      lambda: [("x", data(F32, (1024, 3000), 53))], "scan_rowseq"),
     ("mm_splitk_groups=7", lambda: C.matmul(3, F64, k=65536, m=3),
      lambda: [("a", data(F64, (3, 65536), 54)), ("b", data(F64, (65536, 3), 55))], "matmul_splitk"),
+    # streaming (non-temporal) access masks, the default of each being 3 / 5
+    ("scan_nt=0", lambda: Graph.create("s", [("p", D.scan_rows(D.add, D.const(I32, 1), D.param("x", I32, (2, 300004))))]),
+     lambda: [("x", data(I32, (2, 300004), 57))], "scan_lookback"),
+    ("scan_nt=1", lambda: Graph.create("s", [("p", D.scan_rows(D.add, D.const(I64, 0), D.param("x", I64, (1, 200000))))]),
+     lambda: [("x", data(I64, (1, 200000), 58))], "scan_lookback"),
+    ("rs_nt=0", lambda: C.rows(1024, 3000), lambda: [("x", data(F32, (1024, 3000), 59))], "scan_rowseq"),
+    ("rs_nt=2", lambda: C.rows(2048, 1000), lambda: [("x", data(F32, (2048, 1000), 60))], "reduce_rowseq"),
 ]
 
 
