@@ -815,6 +815,13 @@ struct Lowering {
     return b;
   }
 
+  // Kernels that move more than the 256 MB MALL cannot keep their working
+  // set in it: they stream (non-temporal loads and stores), which keeps
+  // their lines from evicting other data and saves the write-back of dirty
+  // lines a later kernel would otherwise pay. Below the MALL's size plain
+  // accesses win (the data is reused from it).
+  static bool streams(int64_t bytes) { return bytes > tune("nt_bytes", int64_t(256) << 20); }
+
   // Liveness over an element function's body: each line either defines a
   // temporary vN or is a statement kept for its effect; the return value
   // and those statements are the roots. Collects the aN (value parameters)
@@ -932,10 +939,10 @@ struct Lowering {
     int64_t N = n.numel;
     if (N == 0) return {};
     std::string T = dt_ctype(n.dt);
-    // Non-temporal streaming accesses when the kernel also gathers (mode 1),
-    // always (2) or never (0).
+    // Non-temporal streaming accesses when the kernel also gathers or moves
+    // more than the MALL holds (mode 1), always (2) or never (0).
     int64_t nt_mode = tune("map_nt", 1);
-    bool nt = nt_mode == 2 || (nt_mode == 1 && !f.ptrs.empty());
+    bool nt = nt_mode == 2 || (nt_mode == 1 && (!f.ptrs.empty() || streams(fn_bytes(f, N) + N * dt_size(n.dt))));
     if (n.dt == DT::BOOL) nt = false;
     for (int b : f.ident) nt = nt && prog.bufs[b].dt != DT::BOOL;
     std::ostringstream k;
@@ -990,7 +997,9 @@ struct Lowering {
     bool vec = len % 4 == 0;
     // Streaming (non-temporal) accesses, a bit mask: 1 a scan's stores,
     // 2 a reduction's loads, 4 a scan's loads.
-    int64_t rs_nt = n.dt == DT::BOOL ? 0 : tune("rs_nt", 5);
+    int64_t rs_nt = tune("rs_nt", -1);
+    if (rs_nt < 0) rs_nt = streams(fn_bytes(f, rows * len) + (scan ? rows * len : rows) * dt_size(n.dt)) ? 5 : 0;
+    if (n.dt == DT::BOOL) rs_nt = 0;
     for (int b : f.ident)
       if (prog.bufs[b].dt == DT::BOOL) rs_nt &= 1;
     const bool nt_loads = (rs_nt & (scan ? 4 : 2)) != 0, nt_stores = scan && (rs_nt & 1);
@@ -1202,6 +1211,10 @@ struct Lowering {
     // (a one-load loop leaves each workgroup waiting out one memory latency
     // per stride); strides past the end load at the iteration's first
     // (valid) index and are not folded.
+    int64_t red_nt = tune("red_nt", -1);
+    if (red_nt < 0) red_nt = streams(fn_bytes(f, rows * len)) ? 1 : 0;
+    for (int b : f.ident)
+      if (prog.bufs[b].dt == DT::BOOL) red_nt = 0;
     auto fold_loop = [&](const std::string &lo, const std::string &hi) {
       std::ostringstream l;
       if (vec) {
@@ -1210,8 +1223,12 @@ struct Lowering {
         l << "#pragma unroll\n"
           << "      for (int u = 0; u < 4; u++) {\n"
           << "        const int i = base + (j0 + u * 1024 < " << hi << " ? j0 + u * 1024 : j0);\n";
-        for (int b : f.ident)
-          l << "        l" << b << "_[u] = *(const cc_v4<" << ty(b) << ">*)(b" << b << " + i);\n";
+        for (int b : f.ident) {
+          if (red_nt)
+            l << "        l" << b << "_[u] = cc_ld4_nt(b" << b << " + i);\n";
+          else
+            l << "        l" << b << "_[u] = *(const cc_v4<" << ty(b) << ">*)(b" << b << " + i);\n";
+        }
         l << "      }\n"
           << "#pragma unroll\n"
           << "      for (int u = 0; u < 4; u++) {\n"
@@ -1452,7 +1469,9 @@ struct Lowering {
       return r;
     };
     // Streaming (non-temporal) accesses, a bit mask: 1 stores, 2 loads.
-    int64_t scan_nt = n.dt == DT::BOOL ? 0 : tune("scan_nt", 3);
+    int64_t scan_nt = tune("scan_nt", -1);
+    if (scan_nt < 0) scan_nt = streams(fn_bytes(f, rows * len) + rows * len * dt_size(n.dt)) ? 3 : 0;
+    if (n.dt == DT::BOOL) scan_nt = 0;
     for (int b : f.ident)
       if (prog.bufs[b].dt == DT::BOOL) scan_nt &= ~int64_t(2);
     static const char *comp[] = {"x", "y", "z", "w"};
