@@ -37,7 +37,20 @@ struct Executor {
   hipStream_t stream = nullptr;
   std::vector<void *> bufs;
   int *err_host = nullptr;  // pinned word the error flag is read into
+  // Small params, the error word and small outputs share one device
+  // allocation, mirrored by one pinned host block: a synchronous run moves
+  // them with one copy each way instead of one pageable copy (and, for a
+  // download, one round trip to the device) per value. Layout: the params
+  // in [0, arena_in), then the error word and the outputs.
+  char *arena = nullptr;
+  char *arena_host = nullptr;
+  size_t arena_in = 0, arena_bytes = 0;
+  std::vector<int64_t> off;  // per buffer: its offset in the arena, or -1
 };
+
+// A value of at most this many bytes travels through the arena.
+constexpr size_t kArenaValue = 4096;
+constexpr size_t kArenaMax = size_t(1) << 20;
 
 const char *err_message(int code) {
   if (code & 1) return "Backend_hip: gather index out of bounds";
@@ -79,8 +92,12 @@ void release_program(cchip_program *p) {
   for (auto &e : p->execs) {
     if (e.stream) (void)hipStreamSynchronize(e.stream);
     else (void)hipDeviceSynchronize();
-    for (void *b : e.bufs) rt_free(b);
+    for (size_t b = 0; b < e.bufs.size(); b++)
+      if (e.off.empty() || e.off[b] < 0) rt_free(e.bufs[b]);
     e.bufs.clear();
+    if (e.arena) rt_free(e.arena);
+    if (e.arena_host) (void)hipHostFree(e.arena_host);
+    e.arena = e.arena_host = nullptr;
     if (e.err_host) (void)hipHostFree(e.err_host);
     e.err_host = nullptr;
     if (e.stream) (void)hipStreamDestroy(e.stream);
@@ -177,25 +194,67 @@ void queue_err_read(cchip_program *p, Executor &e, const std::vector<void *> &pt
             "hipMemcpyAsync err");
 }
 
+// Issues a run from host memory. With `staged` (the synchronous run, which
+// waits before it returns) the arena's values go through its pinned block;
+// the caller copies the small outputs out after the wait (finish_staged).
+// Asynchronous runs copy straight between the caller's memory and the
+// device, since several may be in flight on one lane.
 void issue_host_run(cchip_program *p, int lane, int n, const char *const *names, const void *const *host,
-                    const size_t *bytes, void *const *outputs) {
+                    const size_t *bytes, void *const *outputs, bool staged) {
   if (p->released) throw Failure("Executor.run: this executor has been released");
   std::vector<int> which = bind_inputs(p, n, names, bytes, "Executor.run");
   Executor &e = p->execs[lane];
+  staged = staged && e.arena;
   const std::vector<void *> &ptr = e.bufs;
   for (size_t k = 0; k < p->ir.params.size(); k++) {
     const IOSpec &ps = p->ir.params[k];
     size_t nb = (size_t)p->ir.bufs[ps.buf].bytes();
-    if (nb)
+    if (!nb) continue;
+    if (staged && e.off[ps.buf] >= 0)
+      memcpy(e.arena_host + e.off[ps.buf], host[which[k]], nb);
+    else
       check_hip(hipMemcpyAsync(ptr[ps.buf], host[which[k]], nb, hipMemcpyHostToDevice, e.stream), "upload");
   }
+  if (staged && e.arena_in)
+    check_hip(hipMemcpyAsync(e.arena, e.arena_host, e.arena_in, hipMemcpyHostToDevice, e.stream), "upload");
   launch_kernels(p, e, ptr, lane == 0);
   for (size_t o = 0; o < p->ir.outputs.size(); o++) {
     const IOSpec &os = p->ir.outputs[o];
     size_t nb = (size_t)p->ir.bufs[os.buf].bytes();
-    if (nb) check_hip(hipMemcpyAsync(outputs[o], ptr[os.buf], nb, hipMemcpyDeviceToHost, e.stream), "download");
+    if (!nb || (staged && e.off[os.buf] >= 0)) continue;
+    check_hip(hipMemcpyAsync(outputs[o], ptr[os.buf], nb, hipMemcpyDeviceToHost, e.stream), "download");
   }
-  queue_err_read(p, e, ptr);
+  if (staged) {
+    if (e.arena_bytes > e.arena_in)
+      check_hip(hipMemcpyAsync(e.arena_host + e.arena_in, e.arena + e.arena_in, e.arena_bytes - e.arena_in,
+                               hipMemcpyDeviceToHost, e.stream),
+                "download");
+  } else {
+    queue_err_read(p, e, ptr);
+  }
+}
+
+// After the wait of a staged run: raise the device's error, if any, and
+// copy the small outputs out of the pinned block.
+void finish_staged(cchip_program *p, Executor &e, void *const *outputs) {
+  if (!e.arena) {
+    check_err_after(p, e, e.bufs, true);
+    return;
+  }
+  if (p->ir.err_buf >= 0) {
+    int *slot = (int *)(e.arena_host + e.off[p->ir.err_buf]);
+    int code = *slot;
+    if (code) {
+      *slot = 0;
+      check_hip(hipMemcpy(e.bufs[p->ir.err_buf], slot, sizeof(int), hipMemcpyHostToDevice), "hipMemcpy");
+      throw InvalidArgument(err_message(code));
+    }
+  }
+  for (size_t o = 0; o < p->ir.outputs.size(); o++) {
+    const IOSpec &os = p->ir.outputs[o];
+    size_t nb = (size_t)p->ir.bufs[os.buf].bytes();
+    if (nb && e.off[os.buf] >= 0) memcpy(outputs[o], e.arena_host + e.off[os.buf], nb);
+  }
 }
 
 void run_resident_impl(cchip_program *p, int n, const char *const *names, void *const *dev_inputs,
@@ -298,7 +357,32 @@ int cchip_backend_compile(const char *graph, int device, int streams, cchip_prog
         check_hip(hipHostMalloc((void **)&e.err_host, sizeof(int), hipHostMallocPortable), "hipHostMalloc");
         *e.err_host = 0;
         e.bufs.assign(p->ir.bufs.size(), nullptr);
+        e.off.assign(p->ir.bufs.size(), -1);
+        size_t at = 0;
+        auto place = [&](int b) {
+          if (b < 0 || e.off[b] >= 0) return;
+          size_t nb = (size_t)p->ir.bufs[b].bytes();
+          size_t slot = (std::max<size_t>(nb, 1) + 255) & ~size_t(255);
+          if (nb > kArenaValue || at + slot > kArenaMax) return;
+          e.off[b] = (int64_t)at;
+          at += slot;
+        };
+        for (auto &ps : p->ir.params) place(ps.buf);
+        e.arena_in = at;
+        if (p->ir.err_buf >= 0) place(p->ir.err_buf);
+        for (auto &os : p->ir.outputs) place(os.buf);
+        e.arena_bytes = at;
+        if (at) {
+          e.arena = (char *)rt_alloc(at);
+          check_hip(hipMemset(e.arena, 0, at), "hipMemset");
+          check_hip(hipHostMalloc((void **)&e.arena_host, at, hipHostMallocPortable), "hipHostMalloc");
+          memset(e.arena_host, 0, at);
+        }
         for (size_t b = 0; b < p->ir.bufs.size(); b++) {
+          if (e.off[b] >= 0) {
+            e.bufs[b] = e.arena + e.off[b];
+            continue;
+          }
           e.bufs[b] = rt_alloc((size_t)p->ir.bufs[b].bytes());
           // Scratch (per-row counters, look-back status) and the error word
           // start at zero; the kernels leave them at zero again.
@@ -331,7 +415,11 @@ int cchip_program_destroy(cchip_program *p) {
 int cchip_program_device(const cchip_program *p) { return p->device; }
 int cchip_program_streams(const cchip_program *p) { return (int)p->execs.size(); }
 int cchip_program_buffer_count(const cchip_program *p) {
-  return p->released || p->execs.empty() ? 0 : (int)p->execs[0].bufs.size();
+  if (p->released || p->execs.empty()) return 0;
+  const Executor &e = p->execs[0];
+  int n = e.arena ? 1 : 0;
+  for (int64_t o : e.off) n += o < 0;
+  return n;
 }
 int cchip_program_kernel_count(const cchip_program *p) { return (int)p->ir.kernels.size(); }
 const char *cchip_program_kernel_name(const cchip_program *p, int i) {
@@ -365,10 +453,10 @@ int cchip_program_run(cchip_program *p, int n, const char *const *names, const v
   return guarded([&] {
     std::lock_guard<std::mutex> lk(p->mu);
     DeviceGuard dg(p->device);
-    issue_host_run(p, 0, n, names, host, bytes, outputs);
+    issue_host_run(p, 0, n, names, host, bytes, outputs, true);
     Executor &e = p->execs[0];
     check_hip(hipStreamSynchronize(e.stream), "hipStreamSynchronize");
-    check_err_after(p, e, e.bufs, true);
+    finish_staged(p, e, outputs);
   });
 }
 
@@ -379,7 +467,7 @@ int cchip_program_run_async(cchip_program *p, int n, const char *const *names, c
     DeviceGuard dg(p->device);
     int lane = p->next;
     p->next = (p->next + 1) % (int)p->execs.size();
-    issue_host_run(p, lane, n, names, host, bytes, outputs);
+    issue_host_run(p, lane, n, names, host, bytes, outputs, false);
     auto j = std::make_unique<cchip_job>();
     j->prog = p;
     j->lane = lane;

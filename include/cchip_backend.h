@@ -53,7 +53,9 @@ int cchip_program_destroy(cchip_program *program);
 
 int cchip_program_device(const cchip_program *program);
 int cchip_program_streams(const cchip_program *program);
-/* Device buffers executor 0 holds (Executor.buffer_count). */
+/* Device allocations executor 0 holds (Executor.buffer_count): one per
+   buffer of the plan, except that params and outputs of at most 4 KiB and
+   the error word share a single one. */
 int cchip_program_buffer_count(const cchip_program *program);
 int cchip_program_kernel_count(const cchip_program *program);
 const char *cchip_program_kernel_name(const cchip_program *program, int i);

@@ -318,6 +318,47 @@ def test_pinned_memory_is_freed_when_dropped(device):
     Pinned.alloc(F32, (256 * 1024,))
 
 
+# ---- the pinned staging block of a synchronous run -----------------------------
+
+
+def test_small_values_through_the_staging_block(device):
+    """Params and outputs of at most 4 KiB and the error word travel through
+    one pinned block per synchronous run: an output that is a param, one
+    value under two names, small and large outputs side by side, a gather's
+    error raised and cleared; run, run_async and the oracle agree."""
+    from cudacaml_amd import dsl as D
+    from cudacaml_amd.ir import I32
+
+    x = D.param("x", F32, (5,))
+    y = D.param("y", F32, (100000,))
+    i = D.param("i", I32, (3,))
+    s = D.reduce(D.add, D.const(F32, 0.0), y)
+    g = Graph.create("stage", [("x", x), ("s", s), ("s2", s), ("r", D.map(lambda v: D.mul(v, D.const(F32, 2.0)), x)),
+                               ("ny", D.map(D.neg, y)), ("gx", D.gather(i, x))])
+    c = H.compile_with(2, g)
+    try:
+        for k in range(3):
+            ins = [("x", np.arange(k, k + 5, dtype=np.float32)),
+                   ("y", np.linspace(0.5, 1 + k, 100000, dtype=np.float32)),
+                   ("i", np.array([4, 0, k], np.int32))]
+            want = oracle.run(g, ins)
+            got = H.run(c, ins)
+            assert [n for n, _ in got] == ["x", "s", "s2", "r", "ny", "gx"]
+            same, msg = Diff.compare_all(want, got, 1e-4)
+            assert same, msg
+            assert float(dict(got)["s"]) == float(dict(got)["s2"])
+            asy = H.wait(H.run_async(c, ins))
+            for (n, a), (_, b) in zip(got, asy):
+                np.testing.assert_array_equal(a, b, err_msg=n)
+        bad = [("x", np.zeros(5, np.float32)), ("y", np.zeros(100000, np.float32)), ("i", np.array([0, 5, 1], np.int32))]
+        with pytest.raises(ValueError, match="gather index out of bounds"):
+            H.run(c, bad)
+        ok = dict(H.run(c, ins))
+        assert ok["gx"].tolist() == [float(k + 4), float(k), float(k + 2)]
+    finally:
+        c.release()
+
+
 # ---- S14 --------------------------------------------------------------------
 
 
