@@ -205,34 +205,31 @@ def cpu_baseline(name, C, H=None):
 
 def pmc_child(args):
     """Child of a counter pass: the workload's warm-up and steps, then the
-    copy calibration kernel; prints the two kernel names as JSON."""
+    copy calibration kernel; prints the calibration kernel's name as JSON."""
     from cudacaml_amd import backend_hip as H
     from cudacaml_amd.examples import configs as C
 
     w = build_workload(args.config, H, C)
-    step(H, w)
-    dom = dominant(H, w, args.config)[0]
     cal = build_workload("copy", H, C)
     copy_name = list(plan_bytes(H, cal.programs[0][0]))[0]
-    for _ in range(1 + args.steps):
+    for _ in range(2 + args.steps):
         step(H, w)
     for _ in range(2):
         step(H, cal)
     from cudacaml_amd.runtime import Device
 
     Device.synchronize()
-    print(json.dumps({"dom": dom, "copy": copy_name}), flush=True)
+    print(json.dumps({"copy": copy_name}), flush=True)
 
 
 COPY_BYTES = (1 << 28) * 4  # read once and written once by the calibration kernel
 
 
-def measure_traffic(config, steps=2):
-    """HBM bytes per launch of the dominant kernel from two rocprofv3 counter
-    passes (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by
-    what the same counter reads for a plain copy kernel of known size. Runs
-    as child processes, before this process touches the GPU. Returns
-    (traffic_bytes, detail) or (None, reason)."""
+def measure_counters(config, steps=2):
+    """Two rocprofv3 counter passes over the workload (FETCH_SIZE, then
+    WRITE_SIZE, KiB per dispatch), run as child processes before this
+    process touches the GPU. Returns ({kernel: {counter: median}}, copy
+    kernel name) or (None, reason)."""
     import csv
     import glob
     import shutil
@@ -243,8 +240,8 @@ def measure_traffic(config, steps=2):
     exe = shutil.which("rocprofv3")
     if exe is None:
         return None, "rocprofv3 not found"
-    vals = {}
-    names = None
+    per = {}
+    copy_name = None
     for counter in ("FETCH_SIZE", "WRITE_SIZE"):
         out = tempfile.mkdtemp(prefix="cchip_pmc_", dir="/tmp")
         cmd = [exe, "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "p", "--",
@@ -260,27 +257,36 @@ def measure_traffic(config, steps=2):
         lines = [l for l in r.stdout.decode(errors="replace").splitlines() if l.startswith("{")]
         if r.returncode != 0 or not lines:
             return None, "rocprofv3 %s pass failed (rc %d)" % (counter, r.returncode)
-        names = json.loads(lines[-1])
+        copy_name = json.loads(lines[-1])["copy"]
         files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
         if not files:
             return None, "no counter file from the %s pass" % counter
-        per = {"dom": [], "copy": []}
+        vals = {}
         with open(files[0]) as f:
             for row in csv.DictReader(f):
-                if row["Counter_Name"] != counter:
-                    continue
-                for key in per:
-                    if row["Kernel_Name"] == names[key]:
-                        per[key].append(float(row["Counter_Value"]))
+                if row["Counter_Name"] == counter:
+                    vals.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
         shutil.rmtree(out, ignore_errors=True)
-        if not per["dom"] or not per["copy"]:
-            return None, "kernel rows missing from the %s pass" % counter
-        vals[counter] = (statistics.median(per["dom"]), statistics.median(per["copy"]))
-    fetch_scale = COPY_BYTES / (vals["FETCH_SIZE"][1] * 1024)
-    write_scale = COPY_BYTES / (vals["WRITE_SIZE"][1] * 1024)
-    fetch = vals["FETCH_SIZE"][0] * 1024 * fetch_scale
-    write = vals["WRITE_SIZE"][0] * 1024 * write_scale
-    detail = {"kernel": names["dom"], "fetch_kib": vals["FETCH_SIZE"][0], "write_kib": vals["WRITE_SIZE"][0],
+        for k, v in vals.items():
+            per.setdefault(k, {})[counter] = statistics.median(v)
+    return per, copy_name
+
+
+def traffic_of(counters, kernel):
+    """HBM bytes per launch of ``kernel``: each counter scaled by what the
+    same counter reads for a plain copy kernel of known size. Returns
+    (traffic_bytes, detail) or (None, reason)."""
+    per, copy_name = counters
+    if per is None:
+        return None, copy_name
+    dom, cal = per.get(kernel, {}), per.get(copy_name, {})
+    if len(dom) < 2 or len(cal) < 2:
+        return None, "kernel rows missing from the counter passes"
+    fetch_scale = COPY_BYTES / (cal["FETCH_SIZE"] * 1024)
+    write_scale = COPY_BYTES / (cal["WRITE_SIZE"] * 1024)
+    fetch = dom["FETCH_SIZE"] * 1024 * fetch_scale
+    write = dom["WRITE_SIZE"] * 1024 * write_scale
+    detail = {"kernel": kernel, "fetch_kib": dom["FETCH_SIZE"], "write_kib": dom["WRITE_SIZE"],
               "fetch_scale": round(fetch_scale, 4), "write_scale": round(write_scale, 4),
               "fetch_bytes": int(fetch), "write_bytes": int(write)}
     return int(fetch + write), detail
@@ -366,10 +372,9 @@ def main():
         return
     # Counter passes first: they are child processes, started before this
     # process initialises the GPU.
-    traffic, traffic_detail = (None, "skipped (--no-traffic)")
+    counters = (None, "skipped (--no-traffic)")
     if not args.no_traffic:
-        traffic, traffic_detail = measure_traffic(args.config)
-        log("traffic:", traffic, traffic_detail)
+        counters = measure_counters(args.config)
 
     import statistics
 
@@ -389,6 +394,8 @@ def main():
         step(H, w)
     Device.synchronize()
     dom, dom_role, dom_bytes, dom_c, kinfo = dominant(H, w, args.config)
+    traffic, traffic_detail = traffic_of(counters, dom)
+    log("traffic:", traffic, traffic_detail)
     Device.synchronize()
     H.time_kernel(dom_c, dom)
     Device.synchronize()
