@@ -1404,7 +1404,7 @@ struct Lowering {
     // words carry the flag (1 aggregate, 2 inclusive prefix) in the high
     // half and the value bits in the low half (8-byte values use two
     // words, each tagged).
-    int64_t Umax = tune(wide ? "lb_slices8" : "lb_slices4", wide ? 8 : 16);
+    int64_t Umax = tune(wide ? "lb_slices8" : "lb_slices4", wide ? 8 : 24);
     if (Umax < 1) throw InvalidArgument("CCHIP_TUNE: look-back slices must be >= 1");
     int64_t U = std::min<int64_t>(Umax, std::max<int64_t>(1, cdiv(len, 1024)));
     int64_t tile = 1024 * U;
