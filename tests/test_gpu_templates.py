@@ -297,6 +297,8 @@ KNOB_CASES = [
      lambda: [("x", data(I64, (1, 200000), 58))], "scan_lookback"),
     ("rs_nt=0", lambda: C.rows(1024, 3000), lambda: [("x", data(F32, (1024, 3000), 59))], "scan_rowseq"),
     ("rs_nt=2", lambda: C.rows(2048, 1000), lambda: [("x", data(F32, (2048, 1000), 60))], "reduce_rowseq"),
+    ("rr_bytes=16384,rr_groups=64", lambda: C.rows(1500, 2001),
+     lambda: [("x", data(F32, (1500, 2001), 61))], "reduce_rowseq"),
 ]
 
 
