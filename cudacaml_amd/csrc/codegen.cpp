@@ -995,7 +995,12 @@ struct Lowering {
     int64_t NT = cdiv(len, W);
     int64_t REM = len - (NT - 1) * W;
     int64_t S = W + 4;               // row stride keeps 4-element groups 16-byte aligned
-    int64_t CH = std::min<int64_t>(16, W);
+    // Elements per batch of LDS reads in the fold: a multiple of 4 that
+    // divides W, so a batch never reads past its row.
+    // Long scanned rows read 64 at a time; short ones (whose loads carry the
+    // heavier element functions, as in Monte Carlo paths) 16.
+    int64_t CH = std::max<int64_t>(4, std::min<int64_t>(scan ? tune("rs_chunk", W >= 256 ? 64 : 16) : tune("rr_chunk", 16), W));
+    while (CH > 4 && (W % CH || CH % 4)) CH -= 4;
     bool vec = len % 4 == 0;
     // Streaming (non-temporal) accesses, a bit mask: 1 a scan's stores,
     // 2 a reduction's loads, 4 a scan's loads.
@@ -1012,15 +1017,18 @@ struct Lowering {
     std::string params = param_list(p, args);
     static const char *comp[] = {"x", "y", "z", "w"};
     std::string V4 = "cc_v4<" + T + ">";
+    // Tiles in flight in registers while one is folded: D register buffers
+    // rotate, buffer d receiving tile kt + 1 + D when tile kt has been folded.
+    const int64_t D = std::max<int64_t>(1, std::min<int64_t>(2, scan ? tune("rs_depth", 1) : tune("rr_depth", 1)));
     std::ostringstream k;
     k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
       << "  __shared__ " << V4 << " sm4[" << R * S / 4 << "];\n"
-      << "  " << T << "* const sm = (" << T << "*)sm4;\n"
-      << "  " << T << " rg[" << E * 4 << "];\n"
-      << "  for (int g0 = blockIdx.x * " << R << "; g0 < " << rows << "; g0 += gridDim.x * " << R << ") {\n";
+      << "  " << T << "* const sm = (" << T << "*)sm4;\n";
+    for (int64_t d = 0; d < D; d++) k << "  " << T << " rg" << d << "[" << E * 4 << "];\n";
+    k << "  for (int g0 = blockIdx.x * " << R << "; g0 < " << rows << "; g0 += gridDim.x * " << R << ") {\n";
     // Tile c0 into registers: group u of thread t covers flat tile elements
     // q..q+3 with q = 4 (t + 256 u), at row q / W, column q % W.
-    auto load = [&](const std::string &c0) {
+    auto load = [&](const std::string &c0, const std::string &rg) {
       std::ostringstream l;
       l << "    {\n"
         << "      const int c0 = " << c0 << ";\n"
@@ -1036,18 +1044,18 @@ struct Lowering {
       if (vec) {
         l << "          const int i = row * " << len << " + (c0 + j < " << len << " ? c0 + j : 0);\n"
           << vec_loads(f, "i", "          ", tyof(), nt_loads);
-        for (int c = 0; c < 4; c++) l << "          rg[4 * u + " << c << "] = " << lane_call(f, "i", c) << ";\n";
+        for (int c = 0; c < 4; c++) l << "          " << rg << "[4 * u + " << c << "] = " << lane_call(f, "i", c) << ";\n";
       } else {
         for (int c = 0; c < 4; c++)
           l << "          { const int i = row * " << len << " + (c0 + j + " << c << " < " << len << " ? c0 + j + " << c
-            << " : 0); rg[4 * u + " << c << "] = " << f.call_scalar("i") << "; }\n";
+            << " : 0); " << rg << "[4 * u + " << c << "] = " << f.call_scalar("i") << "; }\n";
       }
       l << "        }\n"
         << "      }\n"
         << "    }\n";
       return l.str();
     };
-    auto to_lds = [&]() {
+    auto to_lds = [&](const std::string &rg) {
       std::ostringstream l;
       l << "#pragma unroll\n"
         << "    for (int u = 0; u < " << E << "; u++) {\n"
@@ -1055,71 +1063,85 @@ struct Lowering {
         << "      const int rr = q / " << W << ", j = q - rr * " << W << ";\n"
         << "      if (q < " << elems << ") {\n"
         << "        " << V4 << " w;\n";
-      for (int c = 0; c < 4; c++) l << "        w." << comp[c] << " = rg[4 * u + " << c << "];\n";
+      for (int c = 0; c < 4; c++) l << "        w." << comp[c] << " = " << rg << "[4 * u + " << c << "];\n";
       l << "        sm4[(rr * " << S << " + j) / 4] = w;\n"
         << "      }\n"
         << "    }\n";
       return l.str();
     };
-    k << load("0") << to_lds();
-    k << "    if (" << NT << " > 1) {\n" << load(std::to_string(W)) << "    }\n"
-      << "    __syncthreads();\n"
-      << "    " << T << " acc = " << ini << "();\n"
-      << "    for (int kt = 0; kt < " << NT << "; kt++) {\n"
-      << "      const int c0 = kt * " << W << ";\n"
-      << "      if (threadIdx.x < " << R << " && g0 + threadIdx.x < " << rows << ") {\n"
-      << "        " << T << "* const s = sm + threadIdx.x * " << S << ";\n"
-      << "        if (kt + 1 < " << NT << " || " << REM << " == " << W << ") {\n"
-      << "          for (int j0 = 0; j0 < " << W << "; j0 += " << CH << ") {\n"
-      << "            " << T << " tv[" << CH << "];\n"
-      << "#pragma unroll\n"
-      << "            for (int u = 0; u < " << CH / 4 << "; u++) {\n"
-      << "              const " << V4 << " w = ((const " << V4 << "*)(s + j0))[u];\n"
-      << "              tv[4 * u] = w.x; tv[4 * u + 1] = w.y; tv[4 * u + 2] = w.z; tv[4 * u + 3] = w.w;\n"
-      << "            }\n"
-      << "#pragma unroll\n"
-      << "            for (int u = 0; u < " << CH << "; u++) { acc = " << cmb << "(acc, tv[u]);"
-      << (scan ? " tv[u] = acc;" : "") << " }\n";
-    if (scan)
-      k << "#pragma unroll\n"
+    // One tile: fold it (lane r folds row r of the tile), store it (scans),
+    // move the next tile from registers into LDS, refill the registers.
+    auto body = [&](const std::string &rg) {
+      std::ostringstream b;
+      b << "      const int c0 = kt * " << W << ";\n"
+        << "      if (threadIdx.x < " << R << " && g0 + threadIdx.x < " << rows << ") {\n"
+        << "        " << T << "* const s = sm + threadIdx.x * " << S << ";\n"
+        << "        if (kt + 1 < " << NT << " || " << REM << " == " << W << ") {\n"
+        << "          for (int j0 = 0; j0 < " << W << "; j0 += " << CH << ") {\n"
+        << "            " << T << " tv[" << CH << "];\n"
+        << "#pragma unroll\n"
         << "            for (int u = 0; u < " << CH / 4 << "; u++) {\n"
-        << "              " << V4 << " w; w.x = tv[4 * u]; w.y = tv[4 * u + 1]; w.z = tv[4 * u + 2]; w.w = tv[4 * u + 3];\n"
-        << "              ((" << V4 << "*)(s + j0))[u] = w;\n"
-        << "            }\n";
-    k << "          }\n"
-      << "        } else {\n"
-      << "          for (int j = 0; j < " << REM << "; j++) { acc = " << cmb << "(acc, s[j]);"
-      << (scan ? " s[j] = acc;" : "") << " }\n"
-      << "        }\n"
-      << "      }\n"
-      << "      __syncthreads();\n";
-    if (scan) {
-      k << "#pragma unroll\n"
-        << "      for (int u = 0; u < " << E << "; u++) {\n"
-        << "        const int q = 4 * (threadIdx.x + 256 * u);\n"
-        << "        const int rr = q / " << W << ", j = q - rr * " << W << ";\n"
-        << "        const int row = g0 + rr;\n"
-        << "        if (q < " << elems << " && row < " << rows << ") {\n"
-        << "          const int i = row * " << len << " + c0 + j;\n"
-        << "          const " << V4 << " o = sm4[(rr * " << S << " + j) / 4];\n";
-      if (vec) {
-        if (nt_stores)
-          k << "          if (c0 + j < " << len << ") cc_st4_nt(b" << out << " + i, o);\n";
-        else
-          k << "          if (c0 + j < " << len << ") *(" << V4 << "*)(b" << out << " + i) = o;\n";
-      } else {
-        for (int c = 0; c < 4; c++)
-          k << "          if (c0 + j + " << c << " < " << len << ") b" << out << "[i + " << c << "] = o." << comp[c]
-            << ";\n";
-      }
-      k << "        }\n"
+        << "              const " << V4 << " w = ((const " << V4 << "*)(s + j0))[u];\n"
+        << "              tv[4 * u] = w.x; tv[4 * u + 1] = w.y; tv[4 * u + 2] = w.z; tv[4 * u + 3] = w.w;\n"
+        << "            }\n"
+        << "#pragma unroll\n"
+        << "            for (int u = 0; u < " << CH << "; u++) { acc = " << cmb << "(acc, tv[u]);"
+        << (scan ? " tv[u] = acc;" : "") << " }\n";
+      if (scan)
+        b << "#pragma unroll\n"
+          << "            for (int u = 0; u < " << CH / 4 << "; u++) {\n"
+          << "              " << V4 << " w; w.x = tv[4 * u]; w.y = tv[4 * u + 1]; w.z = tv[4 * u + 2]; w.w = tv[4 * u + 3];\n"
+          << "              ((" << V4 << "*)(s + j0))[u] = w;\n"
+          << "            }\n";
+      b << "          }\n"
+        << "        } else {\n"
+        << "          for (int j = 0; j < " << REM << "; j++) { acc = " << cmb << "(acc, s[j]);"
+        << (scan ? " s[j] = acc;" : "") << " }\n"
+        << "        }\n"
         << "      }\n"
         << "      __syncthreads();\n";
+      if (scan) {
+        b << "#pragma unroll\n"
+          << "      for (int u = 0; u < " << E << "; u++) {\n"
+          << "        const int q = 4 * (threadIdx.x + 256 * u);\n"
+          << "        const int rr = q / " << W << ", j = q - rr * " << W << ";\n"
+          << "        const int row = g0 + rr;\n"
+          << "        if (q < " << elems << " && row < " << rows << ") {\n"
+          << "          const int i = row * " << len << " + c0 + j;\n"
+          << "          const " << V4 << " o = sm4[(rr * " << S << " + j) / 4];\n";
+        if (vec) {
+          if (nt_stores)
+            b << "          if (c0 + j < " << len << ") cc_st4_nt(b" << out << " + i, o);\n";
+          else
+            b << "          if (c0 + j < " << len << ") *(" << V4 << "*)(b" << out << " + i) = o;\n";
+        } else {
+          for (int c = 0; c < 4; c++)
+            b << "          if (c0 + j + " << c << " < " << len << ") b" << out << "[i + " << c << "] = o." << comp[c]
+              << ";\n";
+        }
+        b << "        }\n"
+          << "      }\n"
+          << "      __syncthreads();\n";
+      }
+      b << "      if (kt + 1 < " << NT << ") {\n" << to_lds(rg) << "      }\n"
+        << "      if (kt + " << 1 + D << " < " << NT << ") {\n"
+        << load("(kt + " + std::to_string(1 + D) + ") * " + std::to_string(W), rg) << "      }\n"
+        << "      __syncthreads();\n";
+      return b.str();
+    };
+    k << load("0", "rg0") << to_lds("rg0");
+    for (int64_t d = 0; d < D; d++)
+      k << "    if (" << NT << " > " << d + 1 << ") {\n"
+        << load(std::to_string((d + 1) * W), "rg" + std::to_string(d)) << "    }\n";
+    k << "    __syncthreads();\n"
+      << "    " << T << " acc = " << ini << "();\n"
+      << "    for (int kt0 = 0; kt0 < " << NT << "; kt0 += " << D << ") {\n";
+    for (int64_t d = 0; d < D; d++) {
+      k << "      if (kt0 + " << d << " < " << NT << ") {\n"
+        << "      const int kt = kt0 + " << d << ";\n"
+        << body("rg" + std::to_string(d)) << "      }\n";
     }
-    k << "      if (kt + 1 < " << NT << ") {\n" << to_lds() << "      }\n"
-      << "      if (kt + 2 < " << NT << ") {\n" << load("(kt + 2) * " + std::to_string(W)) << "      }\n"
-      << "      __syncthreads();\n"
-      << "    }\n";
+    k << "    }\n";
     if (!scan)
       k << "    if (threadIdx.x < " << R << " && g0 + threadIdx.x < " << rows << ") b" << out
         << "[g0 + threadIdx.x] = acc;\n";

@@ -299,6 +299,12 @@ KNOB_CASES = [
     ("rs_nt=2", lambda: C.rows(2048, 1000), lambda: [("x", data(F32, (2048, 1000), 60))], "reduce_rowseq"),
     ("rr_bytes=16384,rr_groups=64", lambda: C.rows(1500, 2001),
      lambda: [("x", data(F32, (1500, 2001), 61))], "reduce_rowseq"),
+    # two tiles in flight: an odd tile count with a ragged last tile
+    ("rs_depth=2,rs_bytes=4096,rr_depth=2,rr_bytes=16384", lambda: C.rows(1024, 3000),
+     lambda: [("x", data(F32, (1024, 3000), 62))], "scan_rowseq"),
+    ("rr_depth=2,rr_bytes=16384", lambda: C.rows(2048, 5003),
+     lambda: [("x", data(F32, (2048, 5003), 63))], "reduce_rowseq"),
+    ("rs_chunk=4,rr_chunk=128", lambda: C.rows(1024, 3000), lambda: [("x", data(F32, (1024, 3000), 64))], "scan_rowseq"),
 ]
 
 
