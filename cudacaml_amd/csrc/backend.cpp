@@ -10,6 +10,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstring>
 #include <mutex>
 
@@ -33,8 +34,20 @@ struct DeviceGuard {
   }
 };
 
+// A recorded launch sequence for one set of buffer pointers.
+struct GraphEntry {
+  std::vector<void *> key;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+
 struct Executor {
   hipStream_t stream = nullptr;
+  // Launch sequences are recorded on this private stream (lane 0 runs on
+  // the null stream, which cannot be captured) and replayed on `stream`;
+  // most recently used last.
+  hipStream_t capture = nullptr;
+  std::vector<GraphEntry> graphs;
   std::vector<void *> bufs;
   int *err_host = nullptr;  // pinned word the error flag is read into
   // Small params, the error word and small outputs share one device
@@ -47,6 +60,9 @@ struct Executor {
   size_t arena_in = 0, arena_bytes = 0;
   std::vector<int64_t> off;  // per buffer: its offset in the arena, or -1
 };
+
+// Recorded launch sequences kept per executor (distinct pointer sets).
+constexpr size_t kGraphCache = 8;
 
 // A value of at most this many bytes travels through the arena.
 constexpr size_t kArenaValue = 4096;
@@ -68,6 +84,7 @@ struct cchip_program {
   std::vector<Executor> execs;
   int next = 0;
   bool released = false;
+  bool graphs = false;  // replay launch sequences as HIP graphs
   std::mutex mu;
   // timing hook
   int timed = -1;
@@ -92,6 +109,13 @@ void release_program(cchip_program *p) {
   for (auto &e : p->execs) {
     if (e.stream) (void)hipStreamSynchronize(e.stream);
     else (void)hipDeviceSynchronize();
+    for (auto &g : e.graphs) {
+      if (g.exec) (void)hipGraphExecDestroy(g.exec);
+      if (g.graph) (void)hipGraphDestroy(g.graph);
+    }
+    e.graphs.clear();
+    if (e.capture) (void)hipStreamDestroy(e.capture);
+    e.capture = nullptr;
     for (size_t b = 0; b < e.bufs.size(); b++)
       if (e.off.empty() || e.off[b] < 0) rt_free(e.bufs[b]);
     e.bufs.clear();
@@ -143,7 +167,7 @@ std::vector<int> bind_inputs(const cchip_program *p, int n, const char *const *n
   return which;
 }
 
-void launch_kernels(cchip_program *p, Executor &e, const std::vector<void *> &ptr, bool timing) {
+void issue_launches(cchip_program *p, hipStream_t stream, const std::vector<void *> &ptr, bool timing) {
   for (auto &op : p->ir.plan) {
     if (op.kind != OpK::Launch) continue;
     const KernelSpec &k = p->ir.kernels[op.kernel];
@@ -163,16 +187,59 @@ void launch_kernels(cchip_program *p, Executor &e, const std::vector<void *> &pt
         check_hip(hipEventCreate(&ev.first), "hipEventCreate");
         check_hip(hipEventCreate(&ev.second), "hipEventCreate");
       }
-      check_hip(hipEventRecord(ev.first, e.stream), "hipEventRecord");
+      check_hip(hipEventRecord(ev.first, stream), "hipEventRecord");
     }
     check_hip(hipModuleLaunchKernel((hipFunction_t)p->kfn[op.kernel], k.grid, k.grid_y, 1, k.block, k.block_y, 1,
-                                    k.shared_bytes, e.stream, args.data(), nullptr),
+                                    k.shared_bytes, stream, args.data(), nullptr),
               "hipModuleLaunchKernel");
     if (timed) {
-      check_hip(hipEventRecord(ev.second, e.stream), "hipEventRecord");
+      check_hip(hipEventRecord(ev.second, stream), "hipEventRecord");
       p->ev_used.push_back(ev);
     }
   }
+}
+
+// The plan's launches on the executor's stream: replayed from a recorded
+// HIP graph when graphs are on (CCHIP_TUNE graphs=1), the program has
+// several kernels and none is being timed (one graph launch in place of a
+// launch call per kernel), else issued one by one. Graphs are recorded per set of buffer pointers, since the
+// kernels' arguments are baked into them.
+void launch_kernels(cchip_program *p, Executor &e, const std::vector<void *> &ptr, bool timing) {
+  if (!p->graphs || (timing && p->timed >= 0)) {
+    issue_launches(p, e.stream, ptr, timing);
+    return;
+  }
+  for (size_t i = 0; i < e.graphs.size(); i++)
+    if (e.graphs[i].key == ptr) {
+      std::rotate(e.graphs.begin() + i, e.graphs.begin() + i + 1, e.graphs.end());
+      check_hip(hipGraphLaunch(e.graphs.back().exec, e.stream), "hipGraphLaunch");
+      return;
+    }
+  if (!e.capture) check_hip(hipStreamCreateWithFlags(&e.capture, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+  GraphEntry g;
+  g.key = ptr;
+  check_hip(hipStreamBeginCapture(e.capture, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+  try {
+    issue_launches(p, e.capture, ptr, false);
+  } catch (...) {
+    hipGraph_t partial = nullptr;
+    (void)hipStreamEndCapture(e.capture, &partial);
+    if (partial) (void)hipGraphDestroy(partial);
+    throw;
+  }
+  check_hip(hipStreamEndCapture(e.capture, &g.graph), "hipStreamEndCapture");
+  hipError_t rc = hipGraphInstantiate(&g.exec, g.graph, nullptr, nullptr, 0);
+  if (rc != hipSuccess) {
+    (void)hipGraphDestroy(g.graph);
+    check_hip(rc, "hipGraphInstantiate");
+  }
+  if (e.graphs.size() >= kGraphCache) {
+    (void)hipGraphExecDestroy(e.graphs.front().exec);
+    (void)hipGraphDestroy(e.graphs.front().graph);
+    e.graphs.erase(e.graphs.begin());
+  }
+  e.graphs.push_back(g);
+  check_hip(hipGraphLaunch(e.graphs.back().exec, e.stream), "hipGraphLaunch");
 }
 
 // Reads the error word after the work already queued; on a flag, clears it
@@ -348,6 +415,11 @@ int cchip_backend_compile(const char *graph, int device, int streams, cchip_prog
     if (device < 0 || device >= ndev) throw InvalidArgument(strf("Backend_hip.compile_on: no device %d", device));
     DeviceGuard dg(device);
     p->mod = jit_compile("cchip_" + g.name, p->ir.source);
+    int nlaunch = 0;
+    for (auto &op : p->ir.plan) nlaunch += op.kind == OpK::Launch;
+    // Off by default: on gfx950 a replayed graph measured no faster than
+    // eager launches for resident steps, and slower for short host runs.
+    p->graphs = tune_knob("graphs", 0) != 0 && nlaunch >= tune_knob("graph_min_kernels", 2);
     for (auto &k : p->ir.kernels) p->kfn.push_back(module_kernel(*p->mod, k.name));
     p->execs.resize(streams);
     try {

@@ -2629,6 +2629,8 @@ struct Lowering {
 
 }  // namespace
 
+int64_t tune_knob(const char *key, int64_t dflt) { return tune(key, dflt); }
+
 ProgramIR lower_program(const Graph &g) {
   Lowering l(g);
   l.run();

@@ -173,6 +173,8 @@ struct ProgramIR {
 
 ProgramIR lower_program(const Graph &g);
 std::string plan_to_string(const ProgramIR &p);
+// A CCHIP_TUNE knob ("key=value,..."), or dflt when unset.
+int64_t tune_knob(const char *key, int64_t dflt);
 
 // ---------------------------------------------------------------------------
 // Runtime internals shared with the executor

@@ -359,6 +359,90 @@ def test_small_values_through_the_staging_block(device):
         c.release()
 
 
+# ---- recorded launch sequences (HIP graphs) ------------------------------------
+
+
+def _eager_and_graphed(monkeypatch, g, streams=1):
+    monkeypatch.setenv("CCHIP_TUNE", "graphs=0")
+    eager = H.compile_with(streams, g)
+    monkeypatch.setenv("CCHIP_TUNE", "graphs=1")
+    graphed = H.compile_with(streams, g)
+    monkeypatch.delenv("CCHIP_TUNE")
+    return eager, graphed
+
+
+def _same(a, b):
+    assert [n for n, _ in a] == [n for n, _ in b]
+    for (n, x), (_, y) in zip(a, b):
+        np.testing.assert_array_equal(np.asarray(x), np.asarray(y), err_msg=n)
+
+
+def test_graph_replays_equal_eager_launches(device, monkeypatch):
+    """A program of many kernels (the Greeks adjoint, 25 launches) replayed
+    from its recorded graph gives, on every replay, exactly what eager
+    launches give: host runs with eager work and synchronisation between
+    the replays, async runs on a ring of lanes, and resident runs whose
+    output buffers change (each pointer set records its own graph, and more
+    sets than the cache holds evict the oldest)."""
+    from cudacaml_amd.runtime import Buffer, Device
+
+    g = bs.call_greeks(1 << 16, F32)
+    eager, graphed = _eager_and_graphed(monkeypatch, g, streams=2)
+    try:
+        for seed in (1, 2, 3, 1):
+            ins = bs.inputs(F32, seed=seed)
+            want = H.run(eager, ins)
+            _same(want, H.run(graphed, ins))
+            Device.synchronize()
+            _same(want, H.wait(H.run_async(graphed, ins)))
+        ins = bs.inputs(F32, seed=5)
+        want = H.run(eager, ins)
+        res_in = [(n, H.upload(v)) for n, v in ins]
+        sets = []
+        for k in range(11):
+            outs = [(o.name, H.Resident(Buffer.alloc(o.nbytes), o.dtype, o.shape)) for o in graphed.outputs]
+            sets.append(outs)
+            H.run_resident_into(graphed, res_in, outs, sync=(k % 3 == 0))
+        Device.synchronize()
+        for outs in sets + sets[:2]:
+            H.run_resident_into(graphed, res_in, outs, sync=True)
+            _same(want, [(n, H.download(r)) for n, r in outs])
+        for outs in sets:
+            for _, r in outs:
+                H.free_resident(r)
+        for _, r in res_in:
+            H.free_resident(r)
+    finally:
+        eager.release()
+        graphed.release()
+
+
+def test_graph_replays_of_a_look_back_scan(device, monkeypatch):
+    """The look-back scan's status words are cleared by its own fill kernel
+    in every replay: repeated graphed runs stay bit-exact (i32)."""
+    from cudacaml_amd import dsl as D
+    from cudacaml_amd.ir import I32
+
+    n = 3 * (1 << 20) + 7
+    g = Graph.create("s", [("p", D.scan_rows(D.add, D.const(I32, 5), D.param("x", I32, (1, n))))])
+    eager, graphed = _eager_and_graphed(monkeypatch, g)
+    try:
+        for seed in (11, 12, 11):
+            ins = [("x", _small_ints(seed, n).reshape(1, n))]
+            want = H.run(eager, ins)
+            for _ in range(3):
+                _same(want, H.run(graphed, ins))
+    finally:
+        eager.release()
+        graphed.release()
+
+
+def _small_ints(seed, n):
+    from cudacaml_amd.examples import configs as C
+
+    return C.small_ints(seed, (n,))
+
+
 # ---- S14 --------------------------------------------------------------------
 
 
