@@ -518,6 +518,16 @@ template <typename T> __device__ __forceinline__ void cc_st4_nt(T* p, const cc_v
   __builtin_nontemporal_store(v, (v4*)p);
 }
 template <typename T> struct __attribute__((aligned(2 * sizeof(T)))) cc_v2 { T x, y; };
+template <typename T> __device__ __forceinline__ cc_v2<T> cc_ld2_nt(const T* p) {
+  typedef T v2 __attribute__((ext_vector_type(2)));
+  const v2 v = __builtin_nontemporal_load((const v2*)p);
+  return {v.x, v.y};
+}
+template <typename T> __device__ __forceinline__ void cc_st2_nt(T* p, const cc_v2<T>& r) {
+  typedef T v2 __attribute__((ext_vector_type(2)));
+  const v2 v = {r.x, r.y};
+  __builtin_nontemporal_store(v, (v2*)p);
+}
 
 // Float.min / Float.max of OCaml: NaN if either operand is NaN, -0 below
 // +0. These are IEEE 754-2019 minimum/maximum, which gfx950 executes as
@@ -769,16 +779,18 @@ struct Lowering {
   }
 
   // Loads of the identity-indexed buffers of `f` as 4-wide vectors at `i`.
+  // One vector load per identity-indexed input: `w` elements (4, or 2 for
+  // the 16-byte groups of 8-byte types) at index i.
   static std::string vec_loads(const ElemFn &f, const std::string &i, const std::string &indent,
-                               const std::function<std::string(int)> &tyof, bool nt = false) {
-    std::string s;
+                               const std::function<std::string(int)> &tyof, bool nt = false, int w = 4) {
+    std::string s, V = "cc_v" + std::to_string(w), ld = "cc_ld" + std::to_string(w) + "_nt(";
     for (int b : f.ident) {
       std::string bb = "b" + std::to_string(b);
       if (nt)
-        s += indent + "const cc_v4<" + tyof(b) + "> l" + std::to_string(b) + " = cc_ld4_nt(" + bb + " + " + i + ");\n";
+        s += indent + "const " + V + "<" + tyof(b) + "> l" + std::to_string(b) + " = " + ld + bb + " + " + i + ");\n";
       else
-        s += indent + "const cc_v4<" + tyof(b) + "> l" + std::to_string(b) + " = *(const cc_v4<" + tyof(b) + ">*)(" +
-             bb + " + " + i + ");\n";
+        s += indent + "const " + V + "<" + tyof(b) + "> l" + std::to_string(b) + " = *(const " + V + "<" + tyof(b) +
+             ">*)(" + bb + " + " + i + ");\n";
     }
     return s;
   }
@@ -821,6 +833,17 @@ struct Lowering {
   // lines a later kernel would otherwise pay. Below the MALL's size plain
   // accesses win (the data is reused from it).
   static bool streams(int64_t bytes) { return bytes > tune("nt_bytes", int64_t(256) << 20); }
+  // The row, look-back and reduction templates give each lane groups of 4
+  // consecutive elements; for 8-byte types one group is two interleaved
+  // 16-byte accesses, which stream badly (measured: a 2 GiB f64 fill at
+  // 2.2 TB/s streaming against 6.3 TB/s plain). Those templates stream
+  // 4-byte operands only.
+  bool narrow(const ElemFn &f, DT out) const {
+    if (dt_size(out) > 4) return false;
+    for (int b : f.ident)
+      if (dt_size(prog.bufs[b].dt) > 4) return false;
+    return true;
+  }
 
   // Liveness over an element function's body: each line either defines a
   // temporary vN or is a statement kept for its effect; the return value
@@ -945,26 +968,41 @@ struct Lowering {
     bool nt = nt_mode == 2 || (nt_mode == 1 && (!f.ptrs.empty() || streams(fn_bytes(f, N) + N * dt_size(n.dt))));
     if (n.dt == DT::BOOL) nt = false;
     for (int b : f.ident) nt = nt && prog.bufs[b].dt != DT::BOOL;
+    // Loads and stores separately: -1 follows map_nt, 0 plain, 1 streaming.
+    // A map that reads no stream (a fill from scalars) stores plainly: that
+    // measured faster for write-only kernels (1 GiB: 168 us against 190).
+    int64_t ntl_k = tune("map_ntl", -1), nts_k = tune("map_nts", -1);
+    bool ntl = ntl_k < 0 ? nt : ntl_k != 0;
+    bool nts = nts_k < 0 ? nt && (nt_mode == 2 || !f.ident.empty()) : nts_k != 0;
+    if (n.dt == DT::BOOL) nts = false;
+    for (int b : f.ident) ntl = ntl && prog.bufs[b].dt != DT::BOOL;
+    // Elements per thread and access: 16 bytes of the widest type, so each
+    // wave instruction covers one contiguous run (4 for 4-byte types, 2 when
+    // any operand is 8 bytes wide).
+    int G = dt_size(n.dt) == 8 ? 2 : 4;
+    for (int b : f.ident)
+      if (dt_size(prog.bufs[b].dt) == 8) G = 2;
+    const std::string VG = "cc_v" + std::to_string(G);
     std::ostringstream k;
     k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
       << "  const int stride = gridDim.x * 256;\n"
-      << "  const int nvec = " << N / 4 << ";\n"
+      << "  const int nvec = " << N / G << ";\n"
       << "  for (int v = blockIdx.x * 256 + threadIdx.x; v < nvec; v += stride) {\n"
-      << "    const int i = v * 4;\n"
-      << vec_loads(f, "i", "    ", tyof(), nt) << "    cc_v4<" << T << "> r;\n";
+      << "    const int i = v * " << G << ";\n"
+      << vec_loads(f, "i", "    ", tyof(), ntl, G) << "    " << VG << "<" << T << "> r;\n";
     static const char *comp[] = {"x", "y", "z", "w"};
-    for (int u = 0; u < 4; u++) k << "    r." << comp[u] << " = " << lane_call(f, "i", u) << ";\n";
-    if (nt)
-      k << "    cc_st4_nt(b" << out << " + i, r);\n";
+    for (int u = 0; u < G; u++) k << "    r." << comp[u] << " = " << lane_call(f, "i", u) << ";\n";
+    if (nts)
+      k << "    cc_st" << G << "_nt(b" << out << " + i, r);\n";
     else
-      k << "    *(cc_v4<" << T << ">*)(b" << out << " + i) = r;\n";
+      k << "    *(" << VG << "<" << T << ">*)(b" << out << " + i) = r;\n";
     k
       << "  }\n"
-      << "  for (int i = nvec * 4 + blockIdx.x * 256 + threadIdx.x; i < " << N << "; i += stride)\n"
+      << "  for (int i = nvec * " << G << " + blockIdx.x * 256 + threadIdx.x; i < " << N << "; i += stride)\n"
       << "    b" << out << "[i] = " << f.call_scalar("i") << ";\n"
       << "}\n";
     src << k.str();
-    int64_t nvec = std::max<int64_t>(1, N / 4);
+    int64_t nvec = std::max<int64_t>(1, N / G);
     int grid = (int)std::min<int64_t>(cdiv(nvec, 256), tune("map_blocks", 65536));
     return {add_kernel(kname, args, grid, 256, "map")};
   }
@@ -1005,7 +1043,8 @@ struct Lowering {
     // Streaming (non-temporal) accesses, a bit mask: 1 a scan's stores,
     // 2 a reduction's loads, 4 a scan's loads.
     int64_t rs_nt = tune("rs_nt", -1);
-    if (rs_nt < 0) rs_nt = streams(fn_bytes(f, rows * len) + (scan ? rows * len : rows) * dt_size(n.dt)) ? 5 : 0;
+    if (rs_nt < 0)  // 8-byte scans stream their stores only
+      rs_nt = streams(fn_bytes(f, rows * len) + (scan ? rows * len : rows) * dt_size(n.dt)) ? (narrow(f, n.dt) ? 5 : 1) : 0;
     if (n.dt == DT::BOOL) rs_nt = 0;
     for (int b : f.ident)
       if (prog.bufs[b].dt == DT::BOOL) rs_nt &= 1;
@@ -1236,7 +1275,7 @@ struct Lowering {
     // per stride); strides past the end load at the iteration's first
     // (valid) index and are not folded.
     int64_t red_nt = tune("red_nt", -1);
-    if (red_nt < 0) red_nt = streams(fn_bytes(f, rows * len)) ? 1 : 0;
+    if (red_nt < 0) red_nt = narrow(f, n.dt) && streams(fn_bytes(f, rows * len)) ? 1 : 0;
     for (int b : f.ident)
       if (prog.bufs[b].dt == DT::BOOL) red_nt = 0;
     auto fold_loop = [&](const std::string &lo, const std::string &hi) {
@@ -1494,7 +1533,7 @@ struct Lowering {
     };
     // Streaming (non-temporal) accesses, a bit mask: 1 stores, 2 loads.
     int64_t scan_nt = tune("scan_nt", -1);
-    if (scan_nt < 0) scan_nt = streams(fn_bytes(f, rows * len) + rows * len * dt_size(n.dt)) ? 3 : 0;
+    if (scan_nt < 0) scan_nt = narrow(f, n.dt) && streams(fn_bytes(f, rows * len) + rows * len * dt_size(n.dt)) ? 3 : 0;
     if (n.dt == DT::BOOL) scan_nt = 0;
     for (int b : f.ident)
       if (prog.bufs[b].dt == DT::BOOL) scan_nt &= ~int64_t(2);

@@ -140,6 +140,24 @@ def test_map_ragged(device, n):
     check(g, [("x", data(F32, (n,), 1)), ("y", data(I32, (n,), 2))], [] if n == 0 else ["map"])
 
 
+@pytest.mark.parametrize("n", [0, 1, 2, 3, 5, 1023, 1025, 65537])
+@pytest.mark.parametrize("tune", ["", "map_nt=2"])
+def test_map_ragged_8_byte(device, monkeypatch, n, tune):
+    """Maps with an 8-byte operand take 2-element (16-byte) groups: f64 and
+    i64 outputs, a mixed f32/f64 input pair, ragged tails, plain and
+    streaming accesses."""
+    if tune:
+        monkeypatch.setenv("CCHIP_TUNE", tune)
+    x = D.param("x", F64, (n,))
+    y = D.param("y", F32, (n,))
+    z = D.param("z", I64, (n,))
+    g = Graph.create("m", [("r", D.map2(lambda a, b: D.add(D.mul(a, a), D.cast(F64, b)), x, y)),
+                           ("f", D.map2(lambda a, b: D.mul(b, D.cast(F32, a)), x, y)),
+                           ("q", D.map(lambda b: D.sub(D.mul(b, D.const(I64, 3)), D.const(I64, 1)), z))])
+    check(g, [("x", data(F64, (n,), 3)), ("y", data(F32, (n,), 4)), ("z", data(I64, (n,), 5))],
+          [] if n == 0 else ["map"])
+
+
 def scatter_graph(n, bins, dtype):
     idx = D.param("idx", I32, (n,))
     src = D.param("src", dtype, (n,))
