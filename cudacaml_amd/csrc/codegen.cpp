@@ -518,6 +518,27 @@ template <typename T> __device__ __forceinline__ void cc_st4_nt(T* p, const cc_v
   __builtin_nontemporal_store(v, (v4*)p);
 }
 template <typename T> struct __attribute__((aligned(2 * sizeof(T)))) cc_v2 { T x, y; };
+// Buffer-resource accesses of 16 bytes: a descriptor in scalar registers,
+// one shared per-lane byte offset and a uniform offset, so a run of loads
+// costs one vector register of addressing; out-of-range loads read zero.
+// AUX 2 streams (non-temporal), 0 does not. Word 3 is gfx9's.
+typedef unsigned int cc_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t cc_rsrc(const void* p, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+template <typename T, int AUX> __device__ __forceinline__ cc_v4<T> cc_bld4(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  static_assert(sizeof(T) == 4, "4-byte elements");
+  const cc_u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, AUX);
+  cc_v4<T> o;
+  __builtin_memcpy(&o, &v, 16);
+  return o;
+}
+template <typename T, int AUX> __device__ __forceinline__ void cc_bst4(__amdgpu_buffer_rsrc_t r, int voff, int soff, const cc_v4<T>& x) {
+  static_assert(sizeof(T) == 4, "4-byte elements");
+  cc_u32x4 v;
+  __builtin_memcpy(&v, &x, 16);
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, soff, AUX);
+}
 template <typename T> __device__ __forceinline__ cc_v2<T> cc_ld2_nt(const T* p) {
   typedef T v2 __attribute__((ext_vector_type(2)));
   const v2 v = __builtin_nontemporal_load((const v2*)p);
@@ -1467,7 +1488,7 @@ struct Lowering {
     // words carry the flag (1 aggregate, 2 inclusive prefix) in the high
     // half and the value bits in the low half (8-byte values use two
     // words, each tagged).
-    int64_t Umax = tune(wide ? "lb_slices8" : "lb_slices4", wide ? 8 : 24);
+    int64_t Umax = tune(wide ? "lb_slices8" : "lb_slices4", wide ? 8 : 22);
     if (Umax < 1) throw InvalidArgument("CCHIP_TUNE: look-back slices must be >= 1");
     int64_t U = std::min<int64_t>(Umax, std::max<int64_t>(1, cdiv(len, 1024)));
     int64_t tile = 1024 * U;
@@ -1531,6 +1552,13 @@ struct Lowering {
       rep("VAL", val);
       return r;
     };
+    // Buffer-resource loads and stores (one shared offset register for the
+    // whole tile): 4-byte operands under 2 GiB, and an element function
+    // without gathers, since lanes past the tile read (and discard) data
+    // beyond it.
+    bool bufx = vec && tune("lb_buf", 1) && f.ptrs.empty() && dt_size(n.dt) == 4 &&
+                prog.bufs[out].bytes() < (int64_t(1) << 31);
+    for (int b : f.ident) bufx = bufx && dt_size(prog.bufs[b].dt) == 4 && prog.bufs[b].bytes() < (int64_t(1) << 31);
     // Streaming (non-temporal) accesses, a bit mask: 1 stores, 2 loads.
     int64_t scan_nt = tune("scan_nt", -1);
     if (scan_nt < 0) scan_nt = narrow(f, n.dt) && streams(fn_bytes(f, rows * len) + rows * len * dt_size(n.dt)) ? 3 : 0;
@@ -1556,8 +1584,13 @@ struct Lowering {
     k << "  const int row = tile / " << tpr << ";\n"
       << "  const int tin = tile - row * " << tpr << ";\n"
       << "  const int base = row * " << len << " + tin * " << tile << ";\n"
-      << "  const int tl = min(" << tile << ", " << len << " - tin * " << tile << ");\n"
-      << "  " << T << " v[" << U << "][4];\n"
+      << "  const int tl = min(" << tile << ", " << len << " - tin * " << tile << ");\n";
+    if (bufx) {
+      for (int b : f.ident)
+        k << "  const __amdgpu_buffer_rsrc_t r" << b << " = cc_rsrc(b" << b << ", " << prog.bufs[b].bytes() << "u);\n";
+      k << "  const __amdgpu_buffer_rsrc_t ro = cc_rsrc(b" << out << ", " << prog.bufs[out].bytes() << "u);\n";
+    }
+    k << "  " << T << " v[" << U << "][4];\n"
       << "#pragma unroll\n"
       << "  for (int u = 0; u < " << U << "; u++) {\n"
       << "    const int e = threadIdx.x * 4 + 1024 * u;\n";
@@ -1565,8 +1598,14 @@ struct Lowering {
     // take init: no load sits behind a branch.
     if (vec) {
       k << "    const bool ok = e < tl;\n"
-        << "    const int i = base + (ok ? e : 0);\n"
-        << vec_loads(f, "i", "    ", tyof(), (scan_nt & 2) != 0);
+        << "    const int i = base + (ok ? e : 0);\n";
+      if (bufx) {
+        for (int b : f.ident)
+          k << "    const cc_v4<" << ty(b) << "> l" << b << " = cc_bld4<" << ty(b) << ", " << ((scan_nt & 2) ? 2 : 0)
+            << ">(r" << b << ", threadIdx.x * 16, (base + 1024 * u) * 4);\n";
+      } else {
+        k << vec_loads(f, "i", "    ", tyof(), (scan_nt & 2) != 0);
+      }
       for (int c = 0; c < 4; c++)
         k << "    v[u][" << c << "] = ok ? " << lane_call(f, "i", c) << " : " << ini << "();\n";
     } else {
@@ -1725,7 +1764,10 @@ struct Lowering {
       k << "    if (e < tl) {\n"
         << "      cc_v4<" << T << "> o;\n";
       for (int c = 0; c < 4; c++) k << "      o." << comp[c] << " = v[u][" << c << "];\n";
-      if (scan_nt & 1)
+      if (bufx)
+        k << "      cc_bst4<" << T << ", " << ((scan_nt & 1) ? 2 : 0)
+          << ">(ro, threadIdx.x * 16, (base + 1024 * u) * 4, o);\n";
+      else if (scan_nt & 1)
         k << "      cc_st4_nt(b" << out << " + base + e, o);\n";
       else
         k << "      *(cc_v4<" << T << ">*)(b" << out << " + base + e) = o;\n";
