@@ -2028,18 +2028,37 @@ struct Lowering {
           << "  __shared__ int ws[4];\n"
           << "  for (int q = threadIdx.x; q < " << PB << "; q += 256) cur[q] = b" << o.start << "[q] + b" << o.cnt
           << "[(size_t)blockIdx.x * " << PB << " + q];\n"
-          << key_decl << chunk_head()
-          << "  for (int t0 = lo; t0 < hi; t0 += " << TILE << ") {\n"
+          << key_decl << chunk_head();
+        // The next tile's indices and values are loaded into a second set of
+        // registers before this tile's LDS work starts (scatter_prefetch).
+        const bool pf = tune("scatter_prefetch", 1) != 0;
+        auto tile_load = [&](const std::string &t, const std::string &jv, const std::string &xvv) {
+          std::ostringstream l;
+          l << "#pragma unroll\n"
+            << "    for (int u = 0; u < " << E << "; u++) {\n"
+            << "      const int i = " << t << " + u * 256 + (int)threadIdx.x < hi ? " << t
+            << " + u * 256 + (int)threadIdx.x : lo;\n"
+            << "      " << jv << "[u] = " << in.jx("i") << ";\n"
+            << "      " << xvv << "[u] = " << in.xx("i") << ";\n"
+            << "    }\n";
+          return l.str();
+        };
+        if (pf)
+          k << "  int jn[" << E << "];\n"
+            << "  " << T << " xn[" << E << "];\n"
+            << "  if (lo < hi) {\n" << tile_load("lo", "jn", "xn") << "  }\n";
+        k << "  for (int t0 = lo; t0 < hi; t0 += " << TILE << ") {\n"
           << "    for (int q = threadIdx.x; q < " << PB << "; q += 256) tc[q] = 0;\n"
           << "    int jj[" << E << "], rk[" << E << "];\n"
-          << "    " << T << " xv[" << E << "];\n"
-          << "#pragma unroll\n"
-          << "    for (int u = 0; u < " << E << "; u++) {\n"
-          << "      const int i = t0 + u * 256 + (int)threadIdx.x < hi ? t0 + u * 256 + (int)threadIdx.x : lo;\n"
-          << "      jj[u] = " << in.jx("i") << ";\n"
-          << "      xv[u] = " << in.xx("i") << ";\n"
-          << "    }\n"
-          << "    __syncthreads();\n"
+          << "    " << T << " xv[" << E << "];\n";
+        if (pf)
+          k << "#pragma unroll\n"
+            << "    for (int u = 0; u < " << E << "; u++) { jj[u] = jn[u]; xv[u] = xn[u]; }\n"
+            << "    if (t0 + " << TILE << " < hi) {\n" << tile_load("(t0 + " + std::to_string(TILE) + ")", "jn", "xn")
+            << "    }\n";
+        else
+          k << tile_load("t0", "jj", "xv");
+        k << "    __syncthreads();\n"
           << "#pragma unroll\n"
           << "    for (int u = 0; u < " << E << "; u++) {\n"
           << "      rk[u] = 0;\n"

@@ -325,6 +325,8 @@ KNOB_CASES = [
     ("rs_chunk=4,rr_chunk=128", lambda: C.rows(1024, 3000), lambda: [("x", data(F32, (1024, 3000), 64))], "scan_rowseq"),
     ("lb_buf=0", lambda: Graph.create("s", [("p", D.scan_rows(D.add, D.const(I32, 2), D.param("x", I32, (3, 100001))))]),
      lambda: [("x", data(I32, (3, 100001), 65))], "scan_lookback"),
+    ("scatter_prefetch=0", lambda: scatter_graph(300001, 70000, F32),
+     lambda: [("idx", scatter_idx(68, 300001, 70000)), ("src", data(F32, (300001,), 69))], "scatter_partition"),
 ]
 
 
