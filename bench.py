@@ -12,6 +12,12 @@ over the K timed steps (each materialised input read once, each output
 written once, per kernel of the plan). Other configs (``--config saxpy``,
 ``chain``, ``scatter``, ``scatter_perm``, ``matmul``, ``matmul64``, ``matmul_grad``,
 ``mc``, ``mc64``, ``mc_greeks``) print their own line in the same format.
+``poly`` and ``poly64`` are the reference benchmark's own workload
+(bench/bench.ml): the degree-64 Horner chain plus its sum over 2^24
+elements; their ``value`` is GFLOP/s with the input resident, and their
+``whole_run`` carries the reference's RESULT fields (saxpy and poly whole
+runs, best of 5, and the host-device copy rates) beside its published
+A100 figures.
 ``bs``, ``bs_greeks`` (and their f64 ``bs64``, ``bs_greeks64``) are the
 reference's S20 timing row: the one-step Black-Scholes price and its
 Greeks adjoint at 2^22 paths; their ``whole_run`` is timed as S20 times it
@@ -152,6 +158,15 @@ def build_workload(name, H, C):
         return Workload(name, progs, "paths/s", dt.name,
                         "config5: BS MC %s 2^22 paths x 64 steps %s" % ("greeks" if name == "mc_greeks" else "price",
                                                                         dt.name))
+    if name in ("poly", "poly64"):
+        from cudacaml_amd.examples import refbench as RB
+
+        dt = F64 if name == "poly64" else F32
+        x = H.upload(RB.x_input(RB.N, dt))
+        add(RB.poly_graph(RB.N, dt), [("x", x)])
+        return Workload(name, progs, "GFLOP/s", dt.name,
+                        "the reference benchmark's poly: degree-64 Horner chain (63 fused maps) + sum over "
+                        "%s[2^24], x[i] = (i mod 17) - 8, c[j] = 1/(j+1) (bench/bench.ml:97-111,223,253)" % dt.name)
     if name in BS_CONFIGS:
         dt = F64 if name.endswith("64") else F32
         greeks = name.startswith("bs_greeks")
@@ -171,6 +186,47 @@ BS_CONFIGS = ("bs", "bs64", "bs_greeks", "bs_greeks64")
 BS_PUBLISHED_MS = {"bs": 0.2, "bs_greeks": 0.7}
 
 
+def refbench_whole_runs(H, dt, reps=5):
+    """The reference benchmark's RESULT fields (bench/bench.ml:227-300),
+    measured as it measures them: best of ``reps`` whole runs (upload,
+    launches, download; pageable host memory) of saxpy and poly after one
+    warm run, and the 2^24-element host-to-device and device-to-host copy
+    rates."""
+    import numpy as np
+
+    from cudacaml_amd.examples import refbench as RB
+    from cudacaml_amd.runtime import Buffer
+
+    def best(f):
+        t = math.inf
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            f()
+            t = min(t, time.perf_counter() - t0)
+        return t
+
+    n = RB.N
+    x, y = RB.x_input(n, dt), RB.y_input(n, dt)
+    buf = Buffer.alloc(x.nbytes)
+    sink = np.empty_like(x)
+    buf.upload(x)
+    t_h2d = best(lambda: buf.upload(x))
+    t_d2h = best(lambda: buf.download(sink))
+    buf.free()
+    cs = H.compile(RB.saxpy_graph(n, dt))
+    H.run(cs, [("x", x), ("y", y)])
+    t_saxpy = best(lambda: H.run(cs, [("x", x), ("y", y)]))
+    cs.release()
+    cp = H.compile(RB.poly_graph(n, dt))
+    H.run(cp, [("x", x)])
+    t_poly = best(lambda: H.run(cp, [("x", x)]))
+    cp.release()
+    return {"saxpy_cuda_s": round(t_saxpy, 5), "poly_cuda_s": round(t_poly, 5),
+            "poly_gflops": round(n * RB.poly_flops() / t_poly / 1e9, 2),
+            "h2d_gbs": round(x.nbytes / t_h2d / 1e9, 2), "d2h_gbs": round(x.nbytes / t_d2h / 1e9, 2),
+            "hostmem": "pageable", "n": n, "reps": reps}
+
+
 def step(H, w, sync=False):
     for g, c, ins, outs in w.programs:
         H.run_resident_into(c, ins, outs, sync=sync)
@@ -183,6 +239,20 @@ def cpu_baseline(name, C, H=None):
     device when one is given."""
     import oracle
 
+    if name in ("poly", "poly64"):
+        from cudacaml_amd.examples import refbench as RB
+        from cudacaml_amd.ir import F32, F64
+
+        dt = F64 if name == "poly64" else F32
+        n = 1 << 22
+        g = RB.poly_graph(n, dt)
+        c = oracle.Interp.compile(g)
+        x = RB.x_input(n, dt)
+        t0 = time.perf_counter()
+        oracle.Interp.run(c, [("x", x)])
+        secs = time.perf_counter() - t0
+        return (n * RB.poly_flops() / secs / 1e9, "GFLOP/s",
+                "poly graph on the first 2^22 of the 2^24 elements (a quarter of the workload)", secs)
     if name == "rows":
         r = C.ROWS2
         n = C.SCAN2
@@ -419,6 +489,10 @@ def main():
                 if t.kind == "matmul":
                     flops += 2 * t.shape[0] * t.shape[1] * t.a.shape[1]
         value = flops * args.steps / elapsed / 1e12
+    elif w.unit == "GFLOP/s":
+        from cudacaml_amd.examples import refbench as RB
+
+        value = RB.N * RB.poly_flops() * args.steps / elapsed / 1e9
     else:
         value = C.PATHS5 * args.steps / elapsed
     dom_avg_ms = sum(each) / max(1, len(each))
@@ -434,6 +508,24 @@ def main():
         achieved = dom_bytes / (dom_avg_ms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic}
+    if args.config in ("poly", "poly64") and dom_role == "map":
+        # The Horner map is VALU-bound. Its instruction count per element
+        # is read from the gfx950 ISA of this build's kernel (main loop):
+        # f32 62 v_mul_f32 + 6 v_add_f32 + 57 x (v_cvt_f64_f32, v_add_f64,
+        # v_cvt_f32_f64) for the constants that are not single-precision
+        # values (kept as doubles, as the interpreter does); f64 62
+        # v_mul_f64 + 63 v_add_f64. The issue peak is one wave64 VALU
+        # instruction per SIMD per 4 clocks: 256 CUs x 64 lanes x 2.4 GHz.
+        from cudacaml_amd.examples import refbench as RB
+
+        ipe = 125 if args.config == "poly64" else 239
+        n_el = RB.N
+        issue_peak = 256 * 64 * 2.4e9
+        rate = n_el * ipe / (dom_avg_ms * 1e-3)
+        roof["valu"] = {"instructions_per_element": ipe, "achieved_lane_instr_per_s": float("%.4g" % rate),
+                        "issue_peak": float("%.4g" % issue_peak), "frac": round(rate / issue_peak, 4),
+                        "flops_per_element": RB.poly_flops(),
+                        "achieved_tflops": round(n_el * RB.poly_flops() / (dom_avg_ms * 1e-3) / 1e12, 2)}
     roof["kernel"] = dom
     roof["template"] = dom_role
     roof["algorithmic_bytes"] = dom_bytes
@@ -456,12 +548,27 @@ def main():
             vs_baseline = round(pub / ms, 3)
             vs_basis = ("whole-run paths/s against the reference's published A100 S20 time "
                         "(%.1f ms, README.md:152-157); same graph, size and timing method" % pub)
+    elif args.config in ("poly", "poly64") and not args.no_whole_run:
+        from cudacaml_amd.examples import refbench as RB
+        from cudacaml_amd.ir import F32, F64
+
+        dts = "f64" if args.config == "poly64" else "f32"
+        whole = refbench_whole_runs(H, F64 if dts == "f64" else F32)
+        whole["what"] = ("the reference benchmark's RESULT fields, measured as bench/bench.ml:227-300 does: "
+                         "best of 5 whole runs, host arrays in and out")
+        pub = RB.PUBLISHED_A100[dts]
+        whole["published_a100"] = pub
+        whole["ms"] = round(whole["poly_cuda_s"] * 1e3, 3)
+        vs_baseline = round(whole["poly_gflops"] / pub["poly_gflops"], 3)
+        vs_basis = ("whole-run poly GFLOP/s against the reference's published A100-SXM4-40GB figure "
+                    "(%.2f GFLOP/s, bench/results/nvidia-a100-sxm4-40gb.md:36-37); same graph, inputs, size "
+                    "and timing method" % pub["poly_gflops"])
     elif not args.no_whole_run:
         whole = {"ms": round(whole_run_ms(H, w), 2),
                  "what": "host arrays in, host arrays out: upload + kernels + download, pageable memory"}
 
     cpu = None
-    if not args.no_cpu and args.config == "rows":
+    if not args.no_cpu and args.config in ("rows", "poly", "poly64"):
         v, unit, sample, secs = cpu_baseline(args.config, C, H)
         cpu = {"value": round(v, 3), "unit": unit, "cores": 1, "kind": "port",
                "sample": sample + " (%.1fs, C restatement of the OCaml interpreter, one thread)" % secs}

@@ -16,6 +16,7 @@
 // constant that f32 cannot hold exactly stays a double until an operation
 // rounds it (an F32 Const is the unrounded double in the interpreter).
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <functional>
@@ -1004,19 +1005,53 @@ struct Lowering {
     for (int b : f.ident)
       if (dt_size(prog.bufs[b].dt) == 8) G = 2;
     const std::string VG = "cc_v" + std::to_string(G);
+    // Groups per lane per iteration. An element function with a long
+    // dependent chain (a Horner recurrence) needs about four independent
+    // chains per lane to keep the VALU busy: a group of 4-byte elements
+    // has four, a group of 8-byte ones two, so heavy functions over 8-byte
+    // groups take two groups, which the scheduler interleaves (degree-64
+    // Horner in f64: 80 -> 75 us per 2^24; in f32 a second group measured
+    // slower, 105 -> 108 us).
+    // The extra group's index is clamped to the last group, and its store
+    // is unconditional too: a lane past the end recomputes the last group
+    // and stores the same values its owner stores. A guarded store would
+    // let the compiler sink the whole second chain under the guard.
+    int64_t UN = tune("map_unroll", -1);
+    if (UN < 0) UN = std::count(f.code.begin(), f.code.end(), '\n') >= 48 ? 4 / G : 1;
+    UN = std::max<int64_t>(1, std::min<int64_t>(4, UN));
+    static const char *comp[] = {"x", "y", "z", "w"};
     std::ostringstream k;
     k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
       << "  const int stride = gridDim.x * 256;\n"
-      << "  const int nvec = " << N / G << ";\n"
-      << "  for (int v = blockIdx.x * 256 + threadIdx.x; v < nvec; v += stride) {\n"
-      << "    const int i = v * " << G << ";\n"
-      << vec_loads(f, "i", "    ", tyof(), ntl, G) << "    " << VG << "<" << T << "> r;\n";
-    static const char *comp[] = {"x", "y", "z", "w"};
-    for (int u = 0; u < G; u++) k << "    r." << comp[u] << " = " << lane_call(f, "i", u) << ";\n";
-    if (nts)
-      k << "    cc_st" << G << "_nt(b" << out << " + i, r);\n";
-    else
-      k << "    *(" << VG << "<" << T << ">*)(b" << out << " + i) = r;\n";
+      << "  const int nvec = " << N / G << ";\n";
+    if (UN == 1) {
+      k << "  for (int v = blockIdx.x * 256 + threadIdx.x; v < nvec; v += stride) {\n"
+        << "    const int i = v * " << G << ";\n"
+        << vec_loads(f, "i", "    ", tyof(), ntl, G) << "    " << VG << "<" << T << "> r;\n";
+      for (int u = 0; u < G; u++) k << "    r." << comp[u] << " = " << lane_call(f, "i", u) << ";\n";
+      if (nts)
+        k << "    cc_st" << G << "_nt(b" << out << " + i, r);\n";
+      else
+        k << "    *(" << VG << "<" << T << ">*)(b" << out << " + i) = r;\n";
+    } else {
+      k << "  for (int v0 = blockIdx.x * 256 + threadIdx.x; v0 < nvec; v0 += stride * " << UN << ") {\n"
+        << "    " << VG << "<" << T << "> r[" << UN << "];\n";
+      for (int64_t q = 0; q < UN; q++) {
+        k << "    {\n"
+          << "      const int i = min(v0 + " << q << " * stride, nvec - 1) * " << G << ";\n"
+          << vec_loads(f, "i", "      ", tyof(), ntl, G);
+        for (int u = 0; u < G; u++) k << "      r[" << q << "]." << comp[u] << " = " << lane_call(f, "i", u) << ";\n";
+        k << "    }\n";
+      }
+      for (int64_t q = 0; q < UN; q++) {
+        std::string iq = "min(v0 + " + std::to_string(q) + " * stride, nvec - 1) * " + std::to_string(G);
+        k << "    ";
+        if (nts)
+          k << "cc_st" << G << "_nt(b" << out << " + " << iq << ", r[" << q << "]);\n";
+        else
+          k << "*(" << VG << "<" << T << ">*)(b" << out << " + " << iq << ") = r[" << q << "];\n";
+      }
+    }
     k
       << "  }\n"
       << "  for (int i = nvec * " << G << " + blockIdx.x * 256 + threadIdx.x; i < " << N << "; i += stride)\n"
@@ -1024,7 +1059,7 @@ struct Lowering {
       << "}\n";
     src << k.str();
     int64_t nvec = std::max<int64_t>(1, N / G);
-    int grid = (int)std::min<int64_t>(cdiv(nvec, 256), tune("map_blocks", 65536));
+    int grid = (int)std::min<int64_t>(cdiv(nvec, 256 * UN), tune("map_blocks", 65536));
     return {add_kernel(kname, args, grid, 256, "map")};
   }
 

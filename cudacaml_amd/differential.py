@@ -159,7 +159,8 @@ def verdict(name, rule, e, g):
         g64 = gf.astype(np.float64)
         with np.errstate(invalid="ignore"):
             ratio = np.abs(g64 - e64) / (tol * (1.0 + np.abs(e64)))
-        ratio = np.where(np.isnan(e64) & np.isnan(g64), 0.0, ratio)
+        # equal values (infinities included) and NaN against NaN agree
+        ratio = np.where((e64 == g64) | (np.isnan(e64) & np.isnan(g64)), 0.0, ratio)
         ratio = np.where(np.isnan(ratio), np.inf, ratio)
         bad = ratio > 1.0
         worst = float(ratio.max())

@@ -285,3 +285,60 @@ def test_lsm_american_put_on_device(device):
     px_oracle = lsm.Make(oracle.Interp, 8192, 50).price(11)
     px_dev = lsm.Make(H, 8192, 50).price(11)
     assert abs(px_dev - px_oracle) <= 1e-3, (px_dev, px_oracle)
+
+
+# ---------------------------------------------------------------------------
+# The reference benchmark's graphs (bench/bench.ml:97-126): saxpy at both
+# dtypes and the degree-64 Horner chain, on the benchmark's own inputs.
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", [F32, F64], ids=["f32", "f64"])
+def test_refbench_poly(device, dtype):
+    from cudacaml_amd.examples import refbench as RB
+
+    n = 1 << 16
+    g = RB.poly_graph(n, dtype)
+    # Fusion keeps two roots (bench.ml:97-100): the 63 maps in one kernel,
+    # then the reduce (a partial pass and its fold over 2^16 elements)
+    roles = [l.split()[2] for l in H.plan(g).splitlines() if l.startswith("kernel")]
+    assert roles == ["map", "reduce_split", "reduce_split_fold"], roles
+    exp, got = assert_policy(g, [("x", RB.x_input(n, dtype))])
+    e, r = dict(exp)["r"], dict(got)["r"]
+    # each Horner step rounds like the interpreter, so r is bit-exact, not just within 2 ulp
+    assert np.array_equal(e.view(np.uint8), r.view(np.uint8))
+
+
+@pytest.mark.parametrize("n", [1, 7, 1000, 100003])
+def test_refbench_poly_ragged(device, n):
+    """The heavy-map path (two groups per lane, the last group clamped and
+    stored by two lanes) at sizes that leave partial groups and strides."""
+    from cudacaml_amd.examples import refbench as RB
+
+    for dtype in (F32, F64):
+        g = RB.poly_graph(n, dtype)
+        exp, got = assert_policy(g, [("x", RB.x_input(n, dtype))])
+        assert np.array_equal(dict(exp)["r"].view(np.uint8), dict(got)["r"].view(np.uint8))
+
+
+@pytest.mark.parametrize("dtype", [F32, F64], ids=["f32", "f64"])
+def test_refbench_saxpy(device, dtype):
+    from cudacaml_amd.examples import refbench as RB
+
+    n = 1 << 20
+    g = RB.saxpy_graph(n, dtype)
+    x, y = RB.x_input(n, dtype), RB.y_input(n, dtype)
+    exp, got = both(g, [("x", x), ("y", y)])
+    e, d = dict(exp), dict(got)
+    assert np.array_equal(e["r"], d["r"])
+    # Every term is a multiple of 1/4 below 2^18, so the float64 sum is exact.
+    exact = float(np.sum(2.0 * x.astype(np.float64) + y.astype(np.float64)))
+    assert exact == n * (n + 1) / 8 - 16
+    if dtype is F64:
+        assert float(d["s"]) == exact and float(e["s"]) == exact
+    else:
+        # The oracle's sequential f32 sum is itself 1.6e-4 (relative) off the
+        # exact sum here, outside the 1e-4 band; the device's tree sum is
+        # held to the band against the exact value instead.
+        assert abs(float(d["s"]) - exact) <= 1e-4 * (1 + abs(exact))
+        assert abs(float(e["s"]) - exact) > 1e-4 * (1 + abs(exact))

@@ -13,6 +13,7 @@ from cudacaml_amd import differential as Diff
 from cudacaml_amd import dsl as D
 from cudacaml_amd.examples import configs as C
 from cudacaml_amd.examples import programs as P
+from cudacaml_amd.examples import refbench as RB
 from cudacaml_amd.ir import F32, F64, I32, I64, Graph
 
 pytestmark = pytest.mark.gpu
@@ -327,6 +328,11 @@ KNOB_CASES = [
      lambda: [("x", data(I32, (3, 100001), 65))], "scan_lookback"),
     ("scatter_prefetch=0", lambda: scatter_graph(300001, 70000, F32),
      lambda: [("idx", scatter_idx(68, 300001, 70000)), ("src", data(F32, (300001,), 69))], "scatter_partition"),
+    # groups per lane in the map template: a light map forced to two and three
+    # (ragged tails, clamped last groups), a heavy one forced back to one
+    ("map_unroll=2", lambda: P.chain(5003).graph(), lambda: P.chain(5003).inputs(), "map"),
+    ("map_unroll=3", lambda: RB.poly_graph(10001, F64), lambda: [("x", RB.x_input(10001, F64))], "map"),
+    ("map_unroll=1", lambda: RB.poly_graph(70001, F64), lambda: [("x", RB.x_input(70001, F64))], "map"),
 ]
 
 

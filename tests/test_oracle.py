@@ -616,3 +616,54 @@ def test_greeks_graph_shape():
     g = bs.call_greeks(4096, F64)
     assert sorted(n for n, _ in g.params) == ["rate", "s0", "seed", "vol"]
     assert len(g.outputs) == 4
+
+
+# ---------------------------------------------------------------------------
+# bench/bench.ml:70-126 (the reference benchmark's graphs): the degree-64
+# Horner chain against an independent numpy restatement of R1/R3 (each
+# product rounded to single, each f32 constant added as the unrounded
+# double, then rounded), and the f64 chain against plain float64 Horner.
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", [F32, F64], ids=["f32", "f64"])
+def test_refbench_poly_horner(dtype):
+    from cudacaml_amd.examples import refbench as RB
+
+    n = 4096
+    x = RB.x_input(n, dtype)
+    o = dict(run(RB.poly_graph(n, dtype), [("x", x)]))
+    c = RB.coefficients()
+    assert len(c) == 64 and c[2] == 1.0 / 3.0
+    with np.errstate(over="ignore", invalid="ignore"):
+        if dtype is F32:
+            acc = np.full(n, np.float32(c[0]), dtype=np.float32)
+            for cj in c[1:]:
+                acc = ((acc * x).astype(np.float64) + cj).astype(np.float32)
+            s = np.cumsum(acc, dtype=np.float32)[-1]
+        else:
+            acc = np.full(n, c[0])
+            for cj in c[1:]:
+                acc = acc * x + cj
+            s = np.cumsum(acc)[-1]
+    assert np.array_equal(o["r"].view(np.uint8), acc.view(np.uint8))
+    assert np.array_equal(np.array(o["s"]).reshape(1).view(np.uint8), np.array([s], dtype=dtype.np).view(np.uint8))
+    if dtype is F32:
+        # |x| >= 5 overflows single precision: +-inf rows, and the sum is NaN
+        assert np.isinf(o["r"][0]) and np.isnan(o["s"])
+    else:
+        # the benchmark's `agree` check (bench.ml:157-164) against vanilla_poly
+        assert abs(float(o["s"]) - RB.vanilla_poly_sum(c, x)) <= max(1e-3, abs(float(o["s"])) * 1e-3)
+
+
+def test_refbench_saxpy_inputs():
+    from cudacaml_amd.examples import refbench as RB
+
+    n = 1 << 24
+    x, y = RB.x_input(n), RB.y_input(n)
+    # bench.ml:223-224: x[i] = (i mod 17) - 8, y[i] = (n - i) / 4, both exact in f32
+    assert x[:18].tolist() == list(range(-8, 9)) + [-8]
+    assert y[0] == n / 4 and y[-1] == 0.25 and float(y[12345]) == (n - 12345) / 4.0
+    o = dict(run(RB.saxpy_graph(1000, F64), [("x", RB.x_input(1000, F64)), ("y", RB.y_input(1000, F64))]))
+    xi = np.arange(1000) % 17 - 8.0
+    assert o["r"].tolist() == (2.0 * xi + (1000 - np.arange(1000)) / 4.0).tolist()
