@@ -295,11 +295,21 @@ def pmc_child(args):
 COPY_BYTES = (1 << 28) * 4  # read once and written once by the calibration kernel
 
 
+# Configs whose dominant kernel is bound by instruction issue rather than
+# HBM: a third counter pass counts its VALU instructions.
+VALU_CONFIGS = ("poly", "poly64", "mc", "mc64", "mc_greeks", "bs", "bs64", "bs_greeks", "bs_greeks64")
+# One wave64 VALU instruction per SIMD every 4 clocks: 256 CUs x 64 lanes
+# x 2.4 GHz lane-instructions per second (packed FP32 is off in every
+# build here, so it is not counted).
+VALU_ISSUE_PEAK = 256 * 64 * 2.4e9
+
+
 def measure_counters(config, steps=2):
-    """Two rocprofv3 counter passes over the workload (FETCH_SIZE, then
-    WRITE_SIZE, KiB per dispatch), run as child processes before this
-    process touches the GPU. Returns ({kernel: {counter: median}}, copy
-    kernel name) or (None, reason)."""
+    """rocprofv3 counter passes over the workload (FETCH_SIZE, then
+    WRITE_SIZE, KiB per dispatch; SQ_INSTS_VALU, wave instructions per
+    dispatch, for the VALU-bound configs), each run as a child process
+    before this process touches the GPU. Returns ({kernel: {counter:
+    median}}, copy kernel name) or (None, reason)."""
     import csv
     import glob
     import shutil
@@ -312,7 +322,7 @@ def measure_counters(config, steps=2):
         return None, "rocprofv3 not found"
     per = {}
     copy_name = None
-    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+    for counter in ("FETCH_SIZE", "WRITE_SIZE") + (("SQ_INSTS_VALU",) if config in VALU_CONFIGS else ()):
         out = tempfile.mkdtemp(prefix="cchip_pmc_", dir="/tmp")
         cmd = [exe, "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "p", "--",
                sys.executable, os.path.abspath(__file__), "--config", config, "--steps", str(steps),
@@ -360,6 +370,21 @@ def traffic_of(counters, kernel):
               "fetch_scale": round(fetch_scale, 4), "write_scale": round(write_scale, 4),
               "fetch_bytes": int(fetch), "write_bytes": int(write)}
     return int(fetch + write), detail
+
+
+def kernel_elements(H, w, kernel):
+    """Elements of the buffer a kernel writes: its last argument that is
+    not the error word or scratch."""
+    for g, _, _, _ in w.programs:
+        sizes = {}
+        for line in H.plan(g).splitlines():
+            f = line.split()
+            if f[0] == "buffer" and f[-1] not in ("err", "scratch"):
+                sizes[f[1]] = int(f[4])
+            elif f[0] == "kernel" and f[1] == kernel:
+                outs = [a for a in f[f.index("args") + 1:] if a in sizes]
+                return sizes[outs[-1]] if outs else 0
+    return 0
 
 
 def kernel_table(H, w):
@@ -508,24 +533,22 @@ def main():
         achieved = dom_bytes / (dom_avg_ms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic}
-    if args.config in ("poly", "poly64") and dom_role == "map":
-        # The Horner map is VALU-bound. Its instruction count per element
-        # is read from the gfx950 ISA of this build's kernel (main loop):
-        # f32 62 v_mul_f32 + 6 v_add_f32 + 57 x (v_cvt_f64_f32, v_add_f64,
-        # v_cvt_f32_f64) for the constants that are not single-precision
-        # values (kept as doubles, as the interpreter does); f64 62
-        # v_mul_f64 + 63 v_add_f64. The issue peak is one wave64 VALU
-        # instruction per SIMD per 4 clocks: 256 CUs x 64 lanes x 2.4 GHz.
-        from cudacaml_amd.examples import refbench as RB
+    per = counters[0] or {}
+    if args.config in VALU_CONFIGS and "SQ_INSTS_VALU" in per.get(dom, {}):
+        # Issue-bound kernels: VALU lane-instructions per second (wave
+        # instructions counted by SQ_INSTS_VALU, times 64 lanes) against
+        # the issue peak, and per element of the kernel's output.
+        winst = per[dom]["SQ_INSTS_VALU"]
+        n_el = kernel_elements(H, w, dom)
+        rate = winst * 64 / (dom_avg_ms * 1e-3)
+        roof["valu"] = {"wave_instructions": int(winst),
+                        "lane_instructions_per_element": round(winst * 64 / max(1, n_el), 1),
+                        "achieved_lane_instr_per_s": float("%.4g" % rate),
+                        "issue_peak": float("%.4g" % VALU_ISSUE_PEAK), "frac": round(rate / VALU_ISSUE_PEAK, 4)}
+        if args.config in ("poly", "poly64"):
+            from cudacaml_amd.examples import refbench as RB
 
-        ipe = 125 if args.config == "poly64" else 239
-        n_el = RB.N
-        issue_peak = 256 * 64 * 2.4e9
-        rate = n_el * ipe / (dom_avg_ms * 1e-3)
-        roof["valu"] = {"instructions_per_element": ipe, "achieved_lane_instr_per_s": float("%.4g" % rate),
-                        "issue_peak": float("%.4g" % issue_peak), "frac": round(rate / issue_peak, 4),
-                        "flops_per_element": RB.poly_flops(),
-                        "achieved_tflops": round(n_el * RB.poly_flops() / (dom_avg_ms * 1e-3) / 1e12, 2)}
+            roof["valu"]["achieved_tflops"] = round(RB.N * RB.poly_flops() / (dom_avg_ms * 1e-3) / 1e12, 2)
     roof["kernel"] = dom
     roof["template"] = dom_role
     roof["algorithmic_bytes"] = dom_bytes
