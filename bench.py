@@ -373,8 +373,9 @@ def traffic_of(counters, kernel):
 
 
 def kernel_elements(H, w, kernel):
-    """Elements of the buffer a kernel writes: its last argument that is
-    not the error word or scratch."""
+    """Elements a kernel processes: its largest argument that is not the
+    error word or scratch (the output of a map or scan, the input of a
+    reduction)."""
     for g, _, _, _ in w.programs:
         sizes = {}
         for line in H.plan(g).splitlines():
@@ -382,8 +383,8 @@ def kernel_elements(H, w, kernel):
             if f[0] == "buffer" and f[-1] not in ("err", "scratch"):
                 sizes[f[1]] = int(f[4])
             elif f[0] == "kernel" and f[1] == kernel:
-                outs = [a for a in f[f.index("args") + 1:] if a in sizes]
-                return sizes[outs[-1]] if outs else 0
+                outs = [sizes[a] for a in f[f.index("args") + 1:] if a in sizes]
+                return max(outs) if outs else 0
     return 0
 
 

@@ -351,6 +351,23 @@ class Gen {
         int xa = -1, xb = -1;
         if (n.dt == DT::I64 && n.op == B_MUL && zext32(n.a, &xa) && zext32(n.b, &xb))
           return wide_product(go(xa), go(xb));
+        // A 32-bit XOR of a XOR (Philox's hi ^ ctr ^ key, rng.ml:31-36) is
+        // one three-input v_bitop3_b32 (truth table 0x96) on gfx950, where
+        // the compiler leaves two v_xor_b32. The inner XOR is only
+        // evaluated here if something else uses it. Constant operands are
+        // left to the compiler, which folds them.
+        if (n.dt == DT::I32 && n.op == B_XOR) {
+          for (int side = 0; side < 2; side++) {
+            const XNode &in = g_.xs[side ? n.b : n.a];
+            int other = side ? n.a : n.b;
+            if (in.kind == XK::Bin && in.dt == DT::I32 && in.op == B_XOR && g_.xs[in.a].kind != XK::Const &&
+                g_.xs[in.b].kind != XK::Const && g_.xs[other].kind != XK::Const) {
+              Val x = go(in.a), y = go(in.b), z = go(other);
+              return def(VC::I32, "((int)__builtin_amdgcn_bitop3_b32((cc_u32)(" + x.s + "), (cc_u32)(" + y.s +
+                                      "), (cc_u32)(" + z.s + "), 0x96))");
+            }
+          }
+        }
         Val a = go(n.a), b = go(n.b);
         if (n.dt == DT::I32 && n.op == B_MUL && wide_pairs_.count({n.a, n.b})) {
           Val p = wide_product(a, b);
