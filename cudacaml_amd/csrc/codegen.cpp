@@ -392,6 +392,18 @@ class Gen {
       }
       case XK::Not: return def(VC::B, "(!" + go(n.a).s + ")");
       case XK::Select: {
+        // Rng.to_unit_interval's unsigned reading of a word (rng.ml:61-67):
+        // select (w < 0) ((double)w + 2^32) ((double)w) is exactly
+        // (double)(unsigned)w, one v_cvt_f64_u32.
+        {
+          const XNode &cn = g_.xs[n.a], &tn = g_.xs[n.b], &en = g_.xs[n.c];
+          if (n.dt == DT::F64 && cn.kind == XK::Cmp && cn.op == C_LT && g_.xs[cn.a].dt == DT::I32 &&
+              g_.xs[cn.b].kind == XK::Const && g_.xs[cn.b].i == 0 && en.kind == XK::Cast && en.dt == DT::F64 &&
+              en.a == cn.a && tn.kind == XK::Bin && tn.op == B_ADD && tn.dt == DT::F64 &&
+              g_.xs[tn.a].kind == XK::Cast && g_.xs[tn.a].a == cn.a && g_.xs[tn.b].kind == XK::Const &&
+              g_.xs[tn.b].f == 4294967296.0)
+            return def(VC::F64, "((double)(cc_u32)(" + go(cn.a).s + "))");
+        }
         Val c = go(n.a), a = go(n.b), b = go(n.c);
         if (a.c == b.c) return def(a.c, "(" + c.s + " ? " + a.s + " : " + b.s + ")");
         // F32 and F32D meet: keep the exact double.
