@@ -468,7 +468,7 @@ class Gen {
 
   Val unop(const XNode &n, const Val &a) {
     static const char *f32n[] = {"", "sqrtf", "expf", "logf", "fabsf", "sinf", "cosf", "erff", "cc_erfinvf"};
-    static const char *f64n[] = {"", "sqrt", "exp", "log", "fabs", "sin", "cos", "erf", "erfinv"};
+    static const char *f64n[] = {"", "sqrt", "exp", "log", "fabs", "sin", "cos", "erf", "cc_erfinv"};
     switch (n.dt) {
       case DT::F32:
         if (n.op == U_NEG) {
@@ -631,6 +631,98 @@ __device__ __forceinline__ float cc_erfinvf(float x) {
   const float y = __builtin_copysignf(__builtin_fmaf(x, c0, x * (u * q)), x);
   const float ax = __builtin_fabsf(x);
   return ax < 1.0f ? y : (ax == 1.0f ? __builtin_copysignf(__builtin_inff(), x) : __builtin_nanf(""));
+}
+// erfinv in double precision, with the same structure as cc_erfinvf:
+// w = -ln(1 - x^2); erfinv(x) = x p(w - 1) for w < 5, x p1(sqrt(w) - 3)
+// for 5 <= w < 16, x p2(sqrt(w) - 5) beyond. The coefficients are this
+// backend's own fits to erfinv(x)/x (degrees 17, 17 and 14; relative
+// error below 4e-14), and w comes from this function's own logarithm:
+// 1 - x^2 = m 2^e with m in [sqrt(1/2), sqrt(2)), ln m = 2 atanh(s) with
+// s = (m - 1)/(m + 1) summed to s^19.
+__device__ __forceinline__ double cc_erfinv(double x) {
+  const double t = __builtin_fma(-x, x, 1.0);
+  double m = __builtin_amdgcn_frexp_mant(t);
+  int e = __builtin_amdgcn_frexp_exp(t);
+  if (m < 0x1.6a09e667f3bcdp-1) { m = m + m; e = e - 1; }
+  const double f = m - 1.0, d = m + 1.0;
+  double r = __builtin_amdgcn_rcp(d);
+  r = __builtin_fma(__builtin_fma(-d, r, 1.0), r, r);
+  r = __builtin_fma(__builtin_fma(-d, r, 1.0), r, r);
+  const double s = f * r, s2 = s * s;
+  double a = 0x1.af286bca1af28p-5;  // 1/19
+  a = __builtin_fma(a, s2, 0x1.e1e1e1e1e1e1ep-5);  // 1/17
+  a = __builtin_fma(a, s2, 0x1.1111111111111p-4);  // 1/15
+  a = __builtin_fma(a, s2, 0x1.3b13b13b13b14p-4);  // 1/13
+  a = __builtin_fma(a, s2, 0x1.745d1745d1746p-4);  // 1/11
+  a = __builtin_fma(a, s2, 0x1.c71c71c71c71cp-4);  // 1/9
+  a = __builtin_fma(a, s2, 0x1.2492492492492p-3);  // 1/7
+  a = __builtin_fma(a, s2, 0x1.999999999999ap-3);  // 1/5
+  a = __builtin_fma(a, s2, 0x1.5555555555555p-2);  // 1/3
+  const double lnm = __builtin_fma(s + s, s2 * a, s + s);
+  const double de = (double)e;
+  const double w = -__builtin_fma(de, 0x1.62e42fefa39efp-1, __builtin_fma(de, 0x1.abc9e3b39803fp-56, lnm));
+  double u, q, c0;
+  if (w < 5.0) {
+    u = w - 1.0;
+    q = 0x1.5fd4a83d5303fp-50;
+    q = __builtin_fma(q, u, -0x1.441d7737d7005p-45);
+    q = __builtin_fma(q, u, 0x1.daaa8103bac40p-42);
+    q = __builtin_fma(q, u, -0x1.1c2a201a4a356p-39);
+    q = __builtin_fma(q, u, -0x1.aabd1379244f4p-39);
+    q = __builtin_fma(q, u, 0x1.2bac1ac83a37dp-34);
+    q = __builtin_fma(q, u, 0x1.f08db44ecf9abp-37);
+    q = __builtin_fma(q, u, -0x1.9f5c30f1ec20fp-29);
+    q = __builtin_fma(q, u, 0x1.9f2d0f3cb9727p-28);
+    q = __builtin_fma(q, u, 0x1.06aacfd6db79ep-23);
+    q = __builtin_fma(q, u, -0x1.2f73e1e1ad259p-21);
+    q = __builtin_fma(q, u, -0x1.1eedf9e372c45p-18);
+    q = __builtin_fma(q, u, 0x1.4075e51ae7966p-15);
+    q = __builtin_fma(q, u, 0x1.a3f0f037575bep-14);
+    q = __builtin_fma(q, u, -0x1.3779be7bbdc91p-9);
+    q = __builtin_fma(q, u, 0x1.16931130fc047p-8);
+    q = __builtin_fma(q, u, 0x1.fb8fccc6063e1p-3);
+    c0 = 0x1.209b9bb73e397p+0;
+  } else if (w < 16.0) {
+    u = __builtin_sqrt(w) - 3.0;
+    q = -0x1.f6f78b1e45962p-28;
+    q = __builtin_fma(q, u, -0x1.65291a0e0614ep-22);
+    q = __builtin_fma(q, u, 0x1.b798876d2a805p-20);
+    q = __builtin_fma(q, u, -0x1.f088ab5adff9dp-20);
+    q = __builtin_fma(q, u, -0x1.72be2022a173dp-18);
+    q = __builtin_fma(q, u, 0x1.7055c2fd0ca29p-16);
+    q = __builtin_fma(q, u, -0x1.83d25844d1db4p-16);
+    q = __builtin_fma(q, u, -0x1.857740e3bbcd1p-15);
+    q = __builtin_fma(q, u, 0x1.af29a78ddf842p-13);
+    q = __builtin_fma(q, u, -0x1.28e4fa6089a85p-12);
+    q = __builtin_fma(q, u, -0x1.384aa31a9136fp-13);
+    q = __builtin_fma(q, u, 0x1.84f424156f67ap-10);
+    q = __builtin_fma(q, u, -0x1.d2754411716b9p-9);
+    q = __builtin_fma(q, u, 0x1.7495875fc62eap-8);
+    q = __builtin_fma(q, u, -0x1.f4f1c7334e800p-8);
+    q = __builtin_fma(q, u, 0x1.3582c81608189p-7);
+    q = __builtin_fma(q, u, 0x1.006dca7a9d03ap+0);
+    c0 = 0x1.6a9efbd66ea86p+1;
+  } else {
+    u = __builtin_sqrt(w) - 5.0;
+    q = 0x1.7f9d77becd44dp-30;
+    q = __builtin_fma(q, u, -0x1.46c201482688ep-28);
+    q = __builtin_fma(q, u, 0x1.0c1ab2bf246fep-27);
+    q = __builtin_fma(q, u, -0x1.cfdea2298af79p-27);
+    q = __builtin_fma(q, u, 0x1.f1fa914c3ba30p-26);
+    q = __builtin_fma(q, u, -0x1.27a66f89781d0p-24);
+    q = __builtin_fma(q, u, 0x1.ebf30ad12e6eap-23);
+    q = __builtin_fma(q, u, -0x1.0a6d5ab35fc61p-20);
+    q = __builtin_fma(q, u, 0x1.2fbcd2fc1a433p-18);
+    q = __builtin_fma(q, u, -0x1.4a3504248dcc9p-16);
+    q = __builtin_fma(q, u, 0x1.3ebf4f5dc40b3p-14);
+    q = __builtin_fma(q, u, -0x1.c2f3694b61557p-13);
+    q = __builtin_fma(q, u, -0x1.22ea5df45c621p-13);
+    q = __builtin_fma(q, u, 0x1.02a30d1fb9c75p+0);
+    c0 = 0x1.3664ddd1ad7fcp+2;
+  }
+  const double y = __builtin_copysign(__builtin_fma(x, c0, x * (u * q)), x);
+  const double ax = __builtin_fabs(x);
+  return ax < 1.0 ? y : (ax == 1.0 ? __builtin_copysign(__builtin_inf(), x) : __builtin_nan(""));
 }
 // Int32.div / Int64.div: truncation, min_int / -1 wraps. Division by zero
 // raises in the interpreter; on the device it yields 0.

@@ -361,3 +361,39 @@ def test_erfinv_f32_dense_sweep(device):
     assert int(d.max()) <= 2, (x[np.argmax(d)], e[np.argmax(d)], r[np.argmax(d)])
     assert (d > 1).mean() < 2e-5  # 74 of 8.4M on gfx950
     assert np.isinf(r[x == 1.0]).all() and np.signbit(r[(x == 0) & np.signbit(x)]).all()
+
+
+def test_erfinv_f64_dense_sweep(device):
+    """erfinv in f64 (the backend's own fit and logarithm) on a linear grid
+    over (-1, 1), the branch boundaries, random bit patterns of every
+    magnitude and the last doubles below 1 (the deepest tail branch).
+
+    Against the oracle where the interpreter's own erfinv is accurate:
+    Giles' polynomial plus two Newton steps on erf (R7) loses accuracy as
+    |x| nears 1, because erf rounds to 1 there (relative error 2e-14 at
+    1 - |x| = 1e-4, 1.4e-12 at 1e-6, 8.5e-2 at the last double below 1).
+    So the oracle comparison takes 1 - |x| >= 1e-4 (within 6e-14
+    relative), and nearer to 1 the device is held to the exact value
+    (mpmath at 30 digits) within 1e-13."""
+    import mpmath
+
+    n = 1 << 21
+    grid = -1.0 + 2.0 * (np.arange(n) + 0.5) / n
+    bounds = np.array([math.sqrt(-math.expm1(-w)) for w in (5.0, 16.0)])
+    bounds = np.concatenate([np.nextafter(bounds, 0), bounds, np.nextafter(bounds, 2)])
+    rb = np.random.default_rng(5).integers(0, 0x3FF0000000000000, size=1 << 18, dtype=np.int64).view(np.float64)
+    near1 = np.concatenate([1.0 - np.arange(1, 65) * 2.0 ** -53, 1.0 - np.geomspace(1e-15, 1e-4, 64)])
+    pos = np.concatenate([grid, bounds, rb, near1, [0.0, 1.0]])
+    x = np.concatenate([pos, -pos])
+    g = Graph.create("erfinv64", [("r", D.map(D.erfinv, D.param("x", F64, (x.size,))))])
+    exp, got = both(g, [("x", x)])
+    e, r = dict(exp)["r"], dict(got)["r"]
+    sel = np.isfinite(e) & (np.abs(e) > 1e-300) & (1.0 - np.abs(x) >= 1e-4)
+    rel = np.abs(r[sel] - e[sel]) / np.abs(e[sel])
+    assert rel.max() <= 6e-14, (x[sel][np.argmax(rel)], rel.max())
+    assert np.array_equal(np.isinf(r), np.isinf(e)) and np.array_equal(np.signbit(r), np.signbit(e))
+    mpmath.mp.dps = 30
+    near = np.flatnonzero((1.0 - np.abs(x) < 1e-4) & (np.abs(x) < 1.0))
+    for k in near:
+        exact = float(mpmath.erfinv(mpmath.mpf(float(x[k]))))
+        assert abs(r[k] - exact) <= 1e-13 * abs(exact), (x[k], r[k], exact)

@@ -149,15 +149,15 @@ def test_printer_integer_exactness():
     z = D.param("z", F32, (4,))
     src = H.source(Graph.create("g", [("r", D.map(lambda e: D.max(D.mul(e, D.const(F32, 0.1)), e), z))]))
     assert "(float)(" in src and "(double)" in src and "cc_maxf" in src
-    # f32 erfinv is the backend's own cc_erfinvf; f64 calls the device
-    # library's erfinv (the element functions follow the shared prelude)
+    # erfinv is the backend's own: cc_erfinvf in f32, cc_erfinv in f64 (the
+    # element functions follow the shared prelude)
     src = H.source(Graph.create("g", [("r", D.map(lambda e: D.erfinv(D.sin(e)), z))]))
     body = src[src.rindex("__device__ __forceinline__ float f_"):]
     assert "cc_erfinvf(" in body and "sinf(" in body
     w = D.param("w", F64, (4,))
     src = H.source(Graph.create("g", [("r", D.map(lambda e: D.erfinv(D.cos(e)), w))]))
     body = src[src.rindex("__device__ __forceinline__ double f_"):]
-    assert " erfinv(" in body and "erfinvf(" not in body
+    assert "cc_erfinv(" in body and "erfinvf(" not in body
 
 
 def test_generated_modules_compile_for_gfx950():
