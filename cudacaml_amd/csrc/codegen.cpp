@@ -875,6 +875,38 @@ std::string lookback_tree(const std::string &cmb, const std::string &T) {
   return r;
 }
 
+// The look-back's fallback: the aggregate `agg` of tile `q`, folded by the
+// calling wave: lane l folds its contiguous share of the tile left to
+// right, then the lanes' partials are combined with lower lanes on the
+// left (a row's first tile starts from init, as the tile itself does).
+// Few registers are live, so the fallback does not cost the main path its
+// occupancy; it is only taken when a predecessor never publishes.
+// Declares tq (q's index within its row).
+std::string tile_fold(const ElemFn &f, const std::string &cmb, const std::string &ini, const std::string &T, int64_t U,
+                      int64_t tpr, int64_t len, int64_t tile) {
+  (void)U;
+  const int64_t C = cdiv(tile, 64);
+  std::ostringstream a;
+  a << "            const int rq = q / " << tpr << ", tq = q - rq * " << tpr << ";\n"
+    << "            const int bq = rq * " << len << " + tq * " << tile << ";\n"
+    << "            const int lq = min(" << tile << ", " << len << " - tq * " << tile << ");\n"
+    << "            " << T << " w = " << ini << "();\n"
+    << "            bool hw = false;\n"
+    << "            for (int e = lane * " << C << "; e < min(lq, (lane + 1) * " << C << "); e++) {\n"
+    << "              const " << T << " x = " << f.call_scalar("(bq + e)") << ";\n"
+    << "              w = hw ? " << cmb << "(w, x) : x;\n"
+    << "              hw = true;\n"
+    << "            }\n";
+  for (int off = 1; off < 64; off *= 2)
+    a << "            { const " << T << " o = __shfl_down(w, " << off << "); const bool oh = __shfl_down((int)hw, " << off
+      << ") != 0;\n"
+      << "              if ((lane & " << 2 * off - 1 << ") == 0 && oh) { w = hw ? " << cmb
+      << "(w, o) : o; hw = true; } }\n";
+  a << "            " << T << " agg = __shfl(w, 0);\n"
+    << "            if (tq == 0) agg = " << cmb << "(" << ini << "(), agg);\n";
+  return a.str();
+}
+
 // ---------------------------------------------------------------------------
 // The lowering proper
 // ---------------------------------------------------------------------------
@@ -1683,12 +1715,20 @@ struct Lowering {
     // thread, a wave scan of thread totals per slice, one barrier to share
     // the 4 wave totals of every slice, and the slice prefixes are folded
     // in with earlier elements always on the left. When a row spans
-    // several tiles they are chained by a single-pass decoupled look-back:
-    // tiles are handed out in launch order by an atomic counter, so a tile
-    // only waits on tiles whose workgroups are already running; status
-    // words carry the flag (1 aggregate, 2 inclusive prefix) in the high
-    // half and the value bits in the low half (8-byte values use two
+    // several tiles they are chained by a single-pass decoupled look-back;
+    // status words carry the flag (1 aggregate, 2 inclusive prefix) in the
+    // high half and the value bits in the low half (8-byte values use two
     // words, each tagged).
+    //
+    // Which tile a workgroup takes: for 4-byte values, its own blockIdx.
+    // Nothing then makes a predecessor's workgroup run before its
+    // successors, so the look-back never waits unboundedly: after lb_spin
+    // polls of a predecessor that has published nothing, the waiting wave
+    // reads that tile's elements and folds them itself, in the tile's own
+    // order, and goes on. Progress is guaranteed whatever the dispatch
+    // order; with the usual in-order dispatch the fallback is never taken.
+    // 8-byte values take tiles in launch order from an atomic counter, so
+    // a tile only waits on tiles whose workgroups are already running.
     int64_t Umax = tune(wide ? "lb_slices8" : "lb_slices4", wide ? 8 : 22);
     if (Umax < 1) throw InvalidArgument("CCHIP_TUNE: look-back slices must be >= 1");
     int64_t U = std::min<int64_t>(Umax, std::max<int64_t>(1, cdiv(len, 1024)));
@@ -1698,23 +1738,26 @@ struct Lowering {
     bool chained = tpr > 1;
     bool vec = len % 4 == 0;
     int words = wide ? 2 : 1;
+    const bool selfsched = chained && !wide && tune("lb_counter", 0) == 0;
     int status = -1, ctr = -1, kinit = -1;
     if (chained) {
       status = add_buf("t" + id + "_status", DT::I64, tiles * words, BufRole::Scratch);
-      ctr = add_buf("t" + id + "_tiles", DT::I32, 2, BufRole::Scratch);
+      if (!selfsched) ctr = add_buf("t" + id + "_tiles", DT::I32, 2, BufRole::Scratch);
       need_err = true;
       std::string iname = kname + "_init";
       std::ostringstream k;
-      k << "extern \"C\" __global__ __launch_bounds__(256) void " << iname << "(long long* __restrict__ b" << status
-        << ", int* __restrict__ b" << ctr << ") {\n"
+      k << "extern \"C\" __global__ __launch_bounds__(256) void " << iname << "(long long* __restrict__ b" << status;
+      if (!selfsched) k << ", int* __restrict__ b" << ctr;
+      k << ") {\n"
         << "  const int stride = gridDim.x * 256;\n"
         << "  for (int q = blockIdx.x * 256 + threadIdx.x; q < " << tiles * words << "; q += stride) b" << status
-        << "[q] = 0;\n"
-        << "  if (blockIdx.x == 0 && threadIdx.x < 2) b" << ctr << "[threadIdx.x] = 0;\n"
-        << "}\n";
+        << "[q] = 0;\n";
+      if (!selfsched) k << "  if (blockIdx.x == 0 && threadIdx.x < 2) b" << ctr << "[threadIdx.x] = 0;\n";
+      k << "}\n";
       src << k.str();
-      kinit =
-          add_kernel(iname, {status, ctr}, (int)std::min<int64_t>(cdiv(tiles * words, 256), 1024), 256, "scan_init");
+      std::vector<int> iargs = {status};
+      if (!selfsched) iargs.push_back(ctr);
+      kinit = add_kernel(iname, iargs, (int)std::min<int64_t>(cdiv(tiles * words, 256), 1024), 256, "scan_init");
     }
     Params p;
     add_in(p, f);
@@ -1724,7 +1767,7 @@ struct Lowering {
     std::string params = param_list(p, args);
     if (chained) {
       args.push_back(status);
-      args.push_back(ctr);
+      if (!selfsched) args.push_back(ctr);
     }
     std::string pub;
     if (!wide) {
@@ -1768,13 +1811,16 @@ struct Lowering {
       if (prog.bufs[b].dt == DT::BOOL) scan_nt &= ~int64_t(2);
     static const char *comp[] = {"x", "y", "z", "w"};
     std::ostringstream k;
-    k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params;
-    if (chained) k << ", cc_u64* __restrict__ st, int* __restrict__ ctr";
+    // Four waves per SIMD (at most 128 VGPRs): the fallback's registers
+    // must not cost the main path its occupancy.
+    k << "extern \"C\" __global__ __launch_bounds__(256) "
+      << (selfsched ? "__attribute__((amdgpu_waves_per_eu(4))) " : "") << "void " << kname << "(" << params;
+    if (chained) k << ", cc_u64* __restrict__ st" << (selfsched ? "" : ", int* __restrict__ ctr");
     k << ") {\n"
       << "  __shared__ " << T << " wsum[" << U << "][4];\n"
       << "  __shared__ " << T << " s_prefix;\n"
       << "  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;\n";
-    if (chained) {
+    if (chained && !selfsched) {
       k << "  __shared__ int s_tile;\n"
         << "  if (threadIdx.x == 0) s_tile = atomicAdd(ctr, 1);\n"
         << "  __syncthreads();\n"
@@ -1888,12 +1934,31 @@ struct Lowering {
           << "          bool wait = false;\n"
           << "#pragma unroll\n"
           << "          for (int c = 0; c < " << sK << "; c++) wait |= fl[c] == 0 && " << sK << " * lane + c < P;\n"
-          << "          if (!__ballot(wait)) break;\n"
-          << "          if (++spins > (1u << 24)) { cc_flag(err, 4); P = 0;\n"
-          << "#pragma unroll\n"
-          << "            for (int c = 0; c < " << sK << "; c++) { fl[c] = 2; val[c] = " << ini << "(); }\n"
-          << "            break; }\n"
-          << "          __builtin_amdgcn_s_sleep(1);\n"
+          << "          if (!__ballot(wait)) break;\n";
+        if (selfsched) {
+          // The nearest word still unpublished: its tile is folded here.
+          const int64_t spin = std::max<int64_t>(1, tune("lb_spin", 1 << 14));
+          k << "          if (++spins > " << spin << "u) {\n"
+            << "            int mz = " << sK << ";\n"
+            << "#pragma unroll\n"
+            << "            for (int c = " << K - 1 << "; c >= 0; c--) if (fl[c] == 0 && " << sK << " * lane + c < P) mz = c;\n"
+            << "            const int Lz = __ffsll((long long)__ballot(mz < " << sK << ")) - 1;\n"
+            << "            const int cz = __shfl(mz, Lz);\n"
+            << "            const int q = j - (" << sK << " * Lz + cz);\n"
+            << tile_fold(f, cmb, ini, T, U, tpr, len, tile)
+            << "#pragma unroll\n"
+            << "            for (int c = 0; c < " << sK << "; c++)\n"
+            << "              if (lane == Lz && c == cz) { fl[c] = tq == 0 ? 2 : 1; val[c] = agg; }\n"
+            << "            spins = " << spin << "u - 8u;\n"
+            << "            continue;\n"
+            << "          }\n";
+        } else {
+          k << "          if (++spins > (1u << 24)) { cc_flag(err, 4); P = 0;\n"
+            << "#pragma unroll\n"
+            << "            for (int c = 0; c < " << sK << "; c++) { fl[c] = 2; val[c] = " << ini << "(); }\n"
+            << "            break; }\n";
+        }
+        k << "          __builtin_amdgcn_s_sleep(1);\n"
           << "#pragma unroll\n"
           << "          for (int c = 0; c < " << sK << "; c++)\n"
           << "            if (fl[c] == 0 && " << sK << " * lane + c < P) {\n"

@@ -328,6 +328,20 @@ KNOB_CASES = [
      lambda: [("x", data(I32, (3, 100001), 65))], "scan_lookback"),
     ("scatter_prefetch=0", lambda: scatter_graph(300001, 70000, F32),
      lambda: [("idx", scatter_idx(68, 300001, 70000)), ("src", data(F32, (300001,), 69))], "scatter_partition"),
+    # the look-back's own fold of a predecessor tile that has not published
+    # (taken after lb_spin polls; one poll forces it on nearly every wait):
+    # row-start tiles with a non-identity init, floats, many small tiles
+    ("lb_spin=1", lambda: Graph.create("s", [("p", D.scan_rows(D.add, D.const(I32, 2), D.param("x", I32, (3, 100001))))]),
+     lambda: [("x", data(I32, (3, 100001), 70))], "scan_lookback"),
+    ("lb_spin=1,lb_slices4=2", lambda: Graph.create("s", [("p", D.scan(D.add, D.const(I32, 0), D.param("x", I32, (50001,))))]),
+     lambda: [("x", data(I32, (50001,), 71))], "scan_lookback"),
+    ("lb_spin=1", lambda: Graph.create("s", [("p", D.scan_rows(D.add, D.const(F32, 0.5), D.param("x", F32, (2, 200000))))]),
+     lambda: [("x", data(F32, (2, 200000), 72))], "scan_lookback"),
+    ("lb_spin=1,lb_window=4", lambda: Graph.create("s", [("p", D.scan_rows(D.max, D.const(I32, -5), D.param("x", I32, (2, 300004))))]),
+     lambda: [("x", data(I32, (2, 300004), 73))], "scan_lookback"),
+    # tiles from the atomic counter instead of blockIdx
+    ("lb_counter=1", lambda: Graph.create("s", [("p", D.scan_rows(D.add, D.const(I32, 1), D.param("x", I32, (2, 300004))))]),
+     lambda: [("x", data(I32, (2, 300004), 74))], "scan_lookback"),
     # groups per lane in the map template: a light map forced to two and three
     # (ragged tails, clamped last groups), a heavy one forced back to one
     ("map_unroll=2", lambda: P.chain(5003).graph(), lambda: P.chain(5003).inputs(), "map"),
