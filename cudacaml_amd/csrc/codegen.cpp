@@ -553,6 +553,8 @@ template <typename T> struct __attribute__((aligned(2 * sizeof(T)))) cc_v2 { T x
 // costs one vector register of addressing; out-of-range loads read zero.
 // AUX 2 streams (non-temporal), 0 does not. Word 3 is gfx9's.
 typedef unsigned int cc_u32x4 __attribute__((ext_vector_type(4)));
+typedef float cc_f4v __attribute__((ext_vector_type(4)));
+typedef double cc_d2v __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t cc_rsrc(const void* p, unsigned bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
 }
@@ -2635,6 +2637,12 @@ struct Lowering {
     const int64_t ALDS = A.kcontig ? BM * KP : BK * MP;
     const int64_t BLDS = B.kcontig ? BM * KP : BK * MP;
     std::string V = f64 ? "cc_v2<double>" : "cc_v4<float>";  // one 16-byte access
+    // The prefetch registers are native vectors: staged through arrays of
+    // a struct type, the global load and its later LDS store were turned
+    // into one global-to-LDS copy at the store, after the matrix-core
+    // work, so the next tile's loads were not in flight during it.
+    const std::string RV = f64 ? "cc_d2v" : "cc_f4v";
+    const int64_t NR = PER / VEC;
     std::ostringstream k;
     // Global -> registers for one operand tile. `base` is the tile's first
     // row (m for A, n for B) along MN; kt the tile's first k.
@@ -2651,13 +2659,13 @@ struct Lowering {
             std::string idx = is_a ? "(" + mnb + " + r) * " + std::to_string(K) + " + kt + kk + " + std::to_string(c)
                                    : "(kt + kk + " + std::to_string(c) + ") * " + std::to_string(N) + " + " + mnb +
                                          " + r";
-            l << "      " << reg << "[" << c << "] = " << o.fn.call_scalar(idx) << ";\n";
+            l << "      " << reg << "[" << c / VEC << "][" << c % VEC << "] = " << o.fn.call_scalar(idx) << ";\n";
           }
         } else {
           // direct A ([M][K]) or transposed B (source [N][K]): row length K
           l << "      const " << T << "* s = b" << o.buf << " + (size_t)(" << mnb << " + r) * " << K << " + kt + kk;\n";
           for (int64_t c = 0; c < PER; c += VEC)
-            l << "      *(" << V << "*)&" << reg << "[" << c << "] = *(const " << V << "*)(s + " << c << ");\n";
+            l << "      " << reg << "[" << c / VEC << "] = *(const " << RV << "*)(s + " << c << ");\n";
         }
         l << "    }\n";
       } else {
@@ -2667,7 +2675,7 @@ struct Lowering {
           << "      const " << T << "* s = b" << o.buf << " + (size_t)(kt + kk) * " << MNtot << " + " << mnb
           << " + c0;\n";
         for (int64_t c = 0; c < PER; c += VEC)
-          l << "      *(" << V << "*)&" << reg << "[" << c << "] = *(const " << V << "*)(s + " << c << ");\n";
+          l << "      " << reg << "[" << c / VEC << "] = *(const " << RV << "*)(s + " << c << ");\n";
         l << "    }\n";
       }
       return l.str();
@@ -2683,7 +2691,7 @@ struct Lowering {
           << PER << ";\n"
           << "      " << T << "* d = " << lds << " + kk * " << MP << " + c0;\n";
       for (int64_t c = 0; c < PER; c += VEC)
-        l << "      *(" << V << "*)(d + " << c << ") = *(const " << V << "*)&" << reg << "[" << c << "];\n";
+        l << "      *(" << RV << "*)(d + " << c << ") = " << reg << "[" << c / VEC << "];\n";
       l << "    }\n";
       return l.str();
     };
@@ -2726,7 +2734,7 @@ struct Lowering {
       << "  for (int i = 0; i < " << RT << "; i++)\n"
       << "#pragma unroll\n"
       << "    for (int j = 0; j < " << RT << "; j++) acc[i][j] = (" << accT << ")(0);\n"
-      << "  __attribute__((aligned(16))) " << T << " ra[" << PER << "], rb[" << PER << "];\n";
+      << "  " << RV << " ra[" << NR << "], rb[" << NR << "];\n";
     // Two-level accumulation (f32): the matrix cores sum KC-deep chunks into
     // `acc`, which is folded into `tot` with plain adds and cleared. Error
     // then grows with sqrt(KC) + sqrt(K / KC) instead of sqrt(K): for N(0,1)
@@ -2749,6 +2757,9 @@ struct Lowering {
       << "    kt = (it + 1) * " << BK << ";\n"
       << "    if (it + 1 < " << K / BK << ") {\n"
       << gload(A, true, "ra") << gload(B, false, "rb") << "    }\n"
+      // keeps the scheduler from sinking the next tile's loads to their
+      // LDS stores (to save registers), which left them unhidden
+      << "    __builtin_amdgcn_sched_barrier(0);\n"
       << "    {\n"
       << "      __attribute__((aligned(16))) " << T << " fa[" << RT << "][" << S << "], fb[" << RT << "][" << S << "];\n"
       << "      const " << T << "* const al = As[buf];\n"
