@@ -603,7 +603,7 @@ __device__ __forceinline__ float cc_erfinvf(float x) {
   const float t = __builtin_fmaf(-x, x, 1.0f);
   const float L = __builtin_amdgcn_logf(t);  // log2(1 - x^2), one v_log_f32
   float u, q, c0;
-  if (L > -0x1.cda994p+2f) {  // w = -ln2 * L < 5
+  if (L > -0x1.cda994p+2f) {  // w = -ln2 * L < 5, so |x| < 1: no edge cases here
     u = __builtin_fmaf(L, -0x1.62e43p-1f, -1.0f);
     q = -0x1.333982p-27f;
     q = __builtin_fmaf(q, u, 0x1.352e7cp-23f);
@@ -615,6 +615,8 @@ __device__ __forceinline__ float cc_erfinvf(float x) {
     q = __builtin_fmaf(q, u, 0x1.16922p-8f);
     q = __builtin_fmaf(q, u, 0x1.fb8fcep-3f);
     c0 = 0x1.209b9cp+0f;
+    // x's sign, also for -0 (the products make +0 there)
+    return __builtin_copysignf(__builtin_fmaf(x, c0, x * (u * q)), x);
   } else {
     u = __builtin_sqrtf(L * -0x1.62e43p-1f) - 2.5f;
     q = -0x1.e0580ap-16f;
@@ -629,7 +631,7 @@ __device__ __forceinline__ float cc_erfinvf(float x) {
     q = __builtin_fmaf(q, u, 0x1.f6ec82p-1f);
     c0 = 0x1.2b0042p+1f;
   }
-  // x's sign, also for -0 (the products make +0 there)
+  // the tail also takes |x| >= 1 (log of 0 or of a negative) and NaN
   const float y = __builtin_copysignf(__builtin_fmaf(x, c0, x * (u * q)), x);
   const float ax = __builtin_fabsf(x);
   return ax < 1.0f ? y : (ax == 1.0f ? __builtin_copysignf(__builtin_inff(), x) : __builtin_nanf(""));
@@ -664,7 +666,7 @@ __device__ __forceinline__ double cc_erfinv(double x) {
   const double de = (double)e;
   const double w = -__builtin_fma(de, 0x1.62e42fefa39efp-1, __builtin_fma(de, 0x1.abc9e3b39803fp-56, lnm));
   double u, q, c0;
-  if (w < 5.0) {
+  if (t > 0x1.b993fe00d5376p-8) {  // t > e^-5, so w < 5 and |x| < 1: no edge cases here
     u = w - 1.0;
     q = 0x1.5fd4a83d5303fp-50;
     q = __builtin_fma(q, u, -0x1.441d7737d7005p-45);
@@ -684,6 +686,7 @@ __device__ __forceinline__ double cc_erfinv(double x) {
     q = __builtin_fma(q, u, 0x1.16931130fc047p-8);
     q = __builtin_fma(q, u, 0x1.fb8fccc6063e1p-3);
     c0 = 0x1.209b9bb73e397p+0;
+    return __builtin_copysign(__builtin_fma(x, c0, x * (u * q)), x);
   } else if (w < 16.0) {
     u = __builtin_sqrt(w) - 3.0;
     q = -0x1.f6f78b1e45962p-28;
@@ -722,6 +725,7 @@ __device__ __forceinline__ double cc_erfinv(double x) {
     q = __builtin_fma(q, u, 0x1.02a30d1fb9c75p+0);
     c0 = 0x1.3664ddd1ad7fcp+2;
   }
+  // the tails also take |x| >= 1 (w is then not finite or garbage) and NaN
   const double y = __builtin_copysign(__builtin_fma(x, c0, x * (u * q)), x);
   const double ax = __builtin_fabs(x);
   return ax < 1.0 ? y : (ax == 1.0 ? __builtin_copysign(__builtin_inf(), x) : __builtin_nan(""));
