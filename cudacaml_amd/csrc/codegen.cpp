@@ -1929,6 +1929,7 @@ struct Lowering {
           << "          }\n"
           << "        }\n"
           << "        int P;\n"
+          << (selfsched ? "        for (;;) {\n        bool timedout = false;\n" : "")
           << "        while (true) {\n"
           << "          int mine = " << sK << ";\n"
           << "#pragma unroll\n"
@@ -1944,20 +1945,7 @@ struct Lowering {
         if (selfsched) {
           // The nearest word still unpublished: its tile is folded here.
           const int64_t spin = std::max<int64_t>(1, tune("lb_spin", 1 << 14));
-          k << "          if (++spins > " << spin << "u) {\n"
-            << "            int mz = " << sK << ";\n"
-            << "#pragma unroll\n"
-            << "            for (int c = " << K - 1 << "; c >= 0; c--) if (fl[c] == 0 && " << sK << " * lane + c < P) mz = c;\n"
-            << "            const int Lz = __ffsll((long long)__ballot(mz < " << sK << ")) - 1;\n"
-            << "            const int cz = __shfl(mz, Lz);\n"
-            << "            const int q = j - (" << sK << " * Lz + cz);\n"
-            << tile_fold(f, cmb, ini, T, U, tpr, len, tile)
-            << "#pragma unroll\n"
-            << "            for (int c = 0; c < " << sK << "; c++)\n"
-            << "              if (lane == Lz && c == cz) { fl[c] = tq == 0 ? 2 : 1; val[c] = agg; }\n"
-            << "            spins = " << spin << "u - 8u;\n"
-            << "            continue;\n"
-            << "          }\n";
+          k << "          if (++spins > " << spin << "u) { timedout = true; break; }\n";
         } else {
           k << "          if (++spins > (1u << 24)) { cc_flag(err, 4); P = 0;\n"
             << "#pragma unroll\n"
@@ -1971,7 +1959,31 @@ struct Lowering {
           << "              const cc_u64 w = __hip_atomic_load(&st[q0 - c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
           << "              fl[c] = (int)(w >> 32); val[c] = cc_from_bits<" << T << ">(w & 0xffffffffull);\n"
           << "            }\n"
-          << "        }\n"
+          << "        }\n";
+        if (selfsched) {
+          // Out of the polling loop on the spin limit: the nearest word still
+          // unpublished has its tile folded here, then polling resumes.
+          const int64_t spin = std::max<int64_t>(1, tune("lb_spin", 1 << 14));
+          // Taken only when the polling loop stopped on the limit, which it
+          // checks after finding a word still awaited: some lane then has
+          // one (mz < K), so Lz is a lane.
+          k << "        if (!timedout) break;\n"
+            << "        {\n"
+            << "            int mz = " << sK << ";\n"
+            << "#pragma unroll\n"
+            << "            for (int c = " << K - 1 << "; c >= 0; c--) if (fl[c] == 0 && " << sK << " * lane + c < P) mz = c;\n"
+            << "            const int Lz = __ffsll((long long)__ballot(mz < " << sK << ")) - 1;\n"
+            << "            const int cz = __shfl(mz, Lz);\n"
+            << "            const int q = j - (" << sK << " * Lz + cz);\n"
+            << tile_fold(f, cmb, ini, T, U, tpr, len, tile)
+            << "#pragma unroll\n"
+            << "            for (int c = 0; c < " << sK << "; c++)\n"
+            << "              if (lane == Lz && c == cz) { fl[c] = tq == 0 ? 2 : 1; val[c] = agg; }\n"
+            << "            spins = " << std::max<int64_t>(0, spin - 8) << "u;\n"
+            << "        }\n"
+            << "        }\n";
+        }
+        k
           // lane-local fold, farthest word first, of the positions <= P
           << "        " << T << " w = " << ini << "();\n"
           << "        bool hw = false;\n"
