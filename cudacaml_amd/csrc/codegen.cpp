@@ -1284,7 +1284,7 @@ struct Lowering {
     // LDS bytes per tile and the fewest workgroups to aim for; reductions
     // (no stores) and scans measure best at different points.
     int64_t elems = (scan ? tune("rs_bytes", 32768) : tune("rr_bytes", 65536)) / dt_size(n.dt);
-    int64_t min_groups = scan ? tune("rs_groups", 512) : tune("rr_groups", 256);
+    int64_t min_groups = scan ? tune("rs_groups", 256) : tune("rr_groups", 256);
     int64_t R = 1;
     while (R < 64 && rows / (R * 2) >= min_groups) R *= 2;
     int64_t W = std::min<int64_t>(elems / R, std::max<int64_t>(4, pow2ceil(len)));

@@ -305,6 +305,7 @@ KNOB_CASES = [
     ("map_nt=2", lambda: P.chain(5000).graph(), lambda: P.chain(5000).inputs(), "map"),
     ("scatter_slice_bins=16384", lambda: scatter_graph(300001, 70000, F32),
      lambda: [("idx", scatter_idx(51, 300001, 70000)), ("src", data(F32, (300001,), 52))], "scatter_partition"),
+    ("rs_groups=512", lambda: C.rows(8192, 1000), lambda: [("x", data(F32, (8192, 1000), 77))], "scan_rowseq"),
     ("rs_bytes=8192,rs_groups=64", lambda: C.rows(1024, 3000),
      lambda: [("x", data(F32, (1024, 3000), 53))], "scan_rowseq"),
     ("mm_splitk_groups=7", lambda: C.matmul(3, F64, k=65536, m=3),
