@@ -1737,8 +1737,11 @@ struct Lowering {
     // a tile only waits on tiles whose workgroups are already running.
     int64_t Umax = tune(wide ? "lb_slices8" : "lb_slices4", wide ? 8 : 22);
     if (Umax < 1) throw InvalidArgument("CCHIP_TUNE: look-back slices must be >= 1");
-    int64_t U = std::min<int64_t>(Umax, std::max<int64_t>(1, cdiv(len, 1024)));
-    int64_t tile = 1024 * U;
+    // waves per workgroup (4 or 8); a slice is 4 elements per thread
+    const int64_t NW = tune("lb_waves", 4) == 8 ? 8 : 4;
+    const int64_t SL = 256 * NW, NT = 64 * NW;
+    int64_t U = std::min<int64_t>(Umax, std::max<int64_t>(1, cdiv(len, SL)));
+    int64_t tile = SL * U;
     int64_t tpr = cdiv(len, tile);
     int64_t tiles = rows * tpr;
     bool chained = tpr > 1;
@@ -1819,11 +1822,11 @@ struct Lowering {
     std::ostringstream k;
     // Four waves per SIMD (at most 128 VGPRs): the fallback's registers
     // must not cost the main path its occupancy.
-    k << "extern \"C\" __global__ __launch_bounds__(256) "
+    k << "extern \"C\" __global__ __launch_bounds__(" << NT << ") "
       << (selfsched ? "__attribute__((amdgpu_waves_per_eu(4))) " : "") << "void " << kname << "(" << params;
     if (chained) k << ", cc_u64* __restrict__ st" << (selfsched ? "" : ", int* __restrict__ ctr");
     k << ") {\n"
-      << "  __shared__ " << T << " wsum[" << U << "][4];\n"
+      << "  __shared__ " << T << " wsum[" << U << "][" << NW << "];\n"
       << "  __shared__ " << T << " s_prefix;\n"
       << "  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;\n";
     if (chained && !selfsched) {
@@ -1846,7 +1849,7 @@ struct Lowering {
     k << "  " << T << " v[" << U << "][4];\n"
       << "#pragma unroll\n"
       << "  for (int u = 0; u < " << U << "; u++) {\n"
-      << "    const int e = threadIdx.x * 4 + 1024 * u;\n";
+      << "    const int e = threadIdx.x * 4 + " << SL << " * u;\n";
     // Groups past the tile read the tile's first group (always valid) and
     // take init: no load sits behind a branch.
     if (vec) {
@@ -1855,7 +1858,7 @@ struct Lowering {
       if (bufx) {
         for (int b : f.ident)
           k << "    const cc_v4<" << ty(b) << "> l" << b << " = cc_bld4<" << ty(b) << ", " << ((scan_nt & 2) ? 2 : 0)
-            << ">(r" << b << ", threadIdx.x * 16, (base + 1024 * u) * 4);\n";
+            << ">(r" << b << ", threadIdx.x * 16, (base + " << SL << " * u) * 4);\n";
       } else {
         k << vec_loads(f, "i", "    ", tyof(), (scan_nt & 2) != 0);
       }
@@ -1894,7 +1897,9 @@ struct Lowering {
       << "      v[u][0] = " << cmb << "(pf, v[u][0]); v[u][1] = " << cmb << "(pf, v[u][1]);\n"
       << "      v[u][2] = " << cmb << "(pf, v[u][2]); v[u][3] = " << cmb << "(pf, v[u][3]);\n"
       << "    }\n"
-      << "    " << T << " su = " << cmb << "(" << cmb << "(" << cmb << "(wsum[u][0], wsum[u][1]), wsum[u][2]), wsum[u][3]);\n"
+      << "    " << T << " su = wsum[u][0];\n"
+      << "#pragma unroll\n"
+      << "    for (int w = 1; w < " << NW << "; w++) su = " << cmb << "(su, wsum[u][w]);\n"
       << "    run = u > 0 ? " << cmb << "(run, su) : su;\n"
       << "  }\n";
     if (chained) {
@@ -2043,14 +2048,14 @@ struct Lowering {
     }
     k << "#pragma unroll\n"
       << "  for (int u = 0; u < " << U << "; u++) {\n"
-      << "    const int e = threadIdx.x * 4 + 1024 * u;\n";
+      << "    const int e = threadIdx.x * 4 + " << SL << " * u;\n";
     if (vec) {
       k << "    if (e < tl) {\n"
         << "      cc_v4<" << T << "> o;\n";
       for (int c = 0; c < 4; c++) k << "      o." << comp[c] << " = v[u][" << c << "];\n";
       if (bufx)
         k << "      cc_bst4<" << T << ", " << ((scan_nt & 1) ? 2 : 0)
-          << ">(ro, threadIdx.x * 16, (base + 1024 * u) * 4, o);\n";
+          << ">(ro, threadIdx.x * 16, (base + " << SL << " * u) * 4, o);\n";
       else if (scan_nt & 1)
         k << "      cc_st4_nt(b" << out << " + base + e, o);\n";
       else
@@ -2063,7 +2068,7 @@ struct Lowering {
     k << "  }\n"
       << "}\n";
     src << k.str();
-    int kscan = add_kernel(kname, args, (int)tiles, 256, chained ? "scan_lookback" : "scan_tile");
+    int kscan = add_kernel(kname, args, (int)tiles, (int)NT, chained ? "scan_lookback" : "scan_tile");
     if (chained) return {kinit, kscan};
     return {kscan};
   }
