@@ -10,7 +10,9 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libcchip.so")
+# CCHIP_LIB selects another build of the same library (the host-sanitized
+# one of build.py); by default the in-tree libcchip.so.
+LIB_PATH = os.environ.get("CCHIP_LIB") or os.path.join(HERE, "libcchip.so")
 
 OK = 0
 INVALID_ARGUMENT = 1
