@@ -1735,12 +1735,14 @@ struct Lowering {
     // order; with the usual in-order dispatch the fallback is never taken.
     // 8-byte values take tiles in launch order from an atomic counter, so
     // a tile only waits on tiles whose workgroups are already running.
-    // Waves per workgroup (4 or 8); a slice is 4 elements per thread. For
-    // 4-byte values, 8 waves over 13 slices (26624 elements a tile) stream
-    // fastest on gfx950: 2^28 i32 in 381-383 us, against 395-398 us for 4
+    // Waves per workgroup (4 or 8); a slice is 4 elements per thread. 8
+    // waves stream fastest on gfx950. 4-byte values over 13 slices (26624
+    // elements a tile): 2^28 i32 in 381-383 us, against 395-398 us for 4
     // waves over 22 slices, and 386, 396, 392 and 397 us for 8 waves over
-    // 12, 14, 15 and 16 slices.
-    const int64_t NW = tune("lb_waves", wide ? 4 : 8) == 8 ? 8 : 4;
+    // 12, 14, 15 and 16 slices. 8-byte values over 8 slices: 2^27 i64 or
+    // f64 in 472-476 us, against 552 us for 4 waves (6 slices: the same;
+    // 4, 5 and 7 slices: 545, 493-519 and 485 us).
+    const int64_t NW = tune("lb_waves", 8) == 8 ? 8 : 4;
     int64_t Umax = tune(wide ? "lb_slices8" : "lb_slices4", wide ? 8 : (NW == 8 ? 13 : 22));
     if (Umax < 1) throw InvalidArgument("CCHIP_TUNE: look-back slices must be >= 1");
     const int64_t SL = 256 * NW, NT = 64 * NW;

@@ -340,7 +340,7 @@ KNOB_CASES = [
      lambda: [("x", np.abs(data(F32, (2, 200000), 72)))], "scan_lookback"),
     ("lb_spin=1,lb_window=4", lambda: Graph.create("s", [("p", D.scan_rows(D.max, D.const(I32, -5), D.param("x", I32, (2, 300004))))]),
      lambda: [("x", data(I32, (2, 300004), 73))], "scan_lookback"),
-    # four-wave look-back tiles (4-byte values default to eight waves)
+    # four-wave look-back tiles (the default is eight)
     ("lb_waves=4", lambda: Graph.create("s", [("p", D.scan_rows(D.add, D.const(I32, 2), D.param("x", I32, (3, 300001))))]),
      lambda: [("x", data(I32, (3, 300001), 78))], "scan_lookback"),
     ("lb_waves=4,lb_spin=1", lambda: Graph.create("s", [("p", D.scan_rows(D.add, D.const(I32, 1), D.param("x", I32, (2, 200003))))]),
@@ -350,8 +350,7 @@ KNOB_CASES = [
     # sequential one can leave the 1e-4 band
     ("lb_waves=4,lb_spin=1", lambda: Graph.create("s", [("p", D.scan_rows(D.add, D.const(F32, 0.5), D.param("x", F32, (2, 200003))))]),
      lambda: [("x", np.abs(data(F32, (2, 200003), 79)))], "scan_lookback"),
-    # eight-wave tiles of 8-byte values (their default is four waves)
-    ("lb_waves=8", lambda: Graph.create("s", [("p", D.scan_rows(D.add, D.const(I64, 0), D.param("x", I64, (1, 200000))))]),
+    ("lb_waves=4", lambda: Graph.create("s", [("p", D.scan_rows(D.add, D.const(I64, 0), D.param("x", I64, (1, 200000))))]),
      lambda: [("x", data(I64, (1, 200000), 80))], "scan_lookback"),
     # tiles from the atomic counter instead of blockIdx
     ("lb_counter=1", lambda: Graph.create("s", [("p", D.scan_rows(D.add, D.const(I32, 1), D.param("x", I32, (2, 300004))))]),
