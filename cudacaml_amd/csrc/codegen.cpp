@@ -2175,7 +2175,11 @@ struct Lowering {
       if (part >= 0) ks.push_back(scatter_reduce(kname, T, acc, part, out, W, B, B));
       return ks;
     }
-    int64_t W = std::max<int64_t>(1, std::min<int64_t>(16, tune("scatter_slice_wgs", 2048) / P));
+    // Workgroups per slice, about 1024 in all: for 2^26 values into 2^20
+    // bins (128 slices, 8 each) that measures 0.937-0.940 ms a step
+    // against 0.954-0.955 ms with 16 each (accumulate 130 against 138 us,
+    // the fixed-order sum of the partial tables 11 against 17 us).
+    int64_t W = std::max<int64_t>(1, std::min<int64_t>(16, tune("scatter_slice_wgs", 1024) / P));
     while (W > 1 && W * P * S * ES > (int64_t(256) << 20)) W--;
     int part = finish(W, P, P * S);
     std::string sB = std::to_string(B);
