@@ -58,6 +58,12 @@ SCAN_CASES = [
     (5, 300001, I32, "scan_lookback"),
     (8, 100003, F64, "scan_lookback"),
     (2, 77777, I64, "scan_lookback"),
+    # tile boundaries: 26624 elements a tile for 4-byte values, 16384 for
+    # 8-byte ones (one tile and one element; exactly two tiles)
+    (2, 26625, I32, "scan_lookback"),
+    (3, 53248, I32, "scan_lookback"),
+    (2, 16385, I64, "scan_lookback"),
+    (3, 32768, F64, "scan_lookback"),
     (1024, 333, I32, "scan_rowseq"),
     (2048, 64, F32, "scan_rowseq"),
     (1500, 2050, I64, "scan_rowseq"),
