@@ -95,12 +95,42 @@ struct cchip_job {
   cchip_program *prog = nullptr;
   int lane = 0;
   hipEvent_t done = nullptr;
+  // The job's own pinned copy of the device error word, written by its
+  // lane's stream at the end of the job's work: jobs queued on one lane
+  // never see each other's flags.
+  int *err = nullptr;
   bool waited = false;
   int status = 0;
   std::string msg;
 };
 
 namespace {
+
+// Pinned error slots of asynchronous jobs, shared by every program of the
+// process and recycled when a job is freed (a job may outlive its
+// program). Allocated in blocks, never returned to the driver.
+std::mutex g_slot_mu;
+std::vector<int *> g_slot_free;
+constexpr int kSlotBlock = 256;
+
+int *err_slot_get() {
+  std::lock_guard<std::mutex> lk(g_slot_mu);
+  if (g_slot_free.empty()) {
+    int *blk = nullptr;
+    check_hip(hipHostMalloc((void **)&blk, kSlotBlock * sizeof(int), hipHostMallocPortable), "hipHostMalloc");
+    for (int i = kSlotBlock - 1; i >= 0; i--) g_slot_free.push_back(blk + i);
+  }
+  int *s = g_slot_free.back();
+  g_slot_free.pop_back();
+  *s = 0;
+  return s;
+}
+
+void err_slot_put(int *s) {
+  if (!s) return;
+  std::lock_guard<std::mutex> lk(g_slot_mu);
+  g_slot_free.push_back(s);
+}
 
 void release_program(cchip_program *p) {
   if (p->released) return;
@@ -242,23 +272,32 @@ void launch_kernels(cchip_program *p, Executor &e, const std::vector<void *> &pt
   check_hip(hipGraphLaunch(e.graphs.back().exec, e.stream), "hipGraphLaunch");
 }
 
-// Reads the error word after the work already queued; on a flag, clears it
-// and raises the interpreter's error.
-void check_err_after(cchip_program *p, Executor &e, const std::vector<void *> &ptr, bool synced) {
+// The device error word is sticky: kernels only ever set bits in it. A run
+// that reports errors queues, on its own stream and after its kernels, a
+// copy of the word into a host slot (the run's own: the pinned block of a
+// synchronous run, the job's slot of an asynchronous one) and then a reset
+// of the word. Runs on one lane are ordered by its stream, so each run
+// reads exactly the flags of the runs since the previous read; lanes have
+// separate words.
+void queue_err_reset(cchip_program *p, Executor &e) {
   if (p->ir.err_buf < 0) return;
-  if (!synced) check_hip(hipStreamSynchronize(e.stream), "hipStreamSynchronize");
-  int code = *e.err_host;
-  if (code) {
-    *e.err_host = 0;
-    check_hip(hipMemcpy(ptr[p->ir.err_buf], e.err_host, sizeof(int), hipMemcpyHostToDevice), "hipMemcpy");
-    throw InvalidArgument(err_message(code));
-  }
+  check_hip(hipMemsetAsync(e.bufs[p->ir.err_buf], 0, sizeof(int), e.stream), "hipMemsetAsync err");
 }
 
-void queue_err_read(cchip_program *p, Executor &e, const std::vector<void *> &ptr) {
+void queue_err_read(cchip_program *p, Executor &e, int *slot) {
   if (p->ir.err_buf < 0) return;
-  check_hip(hipMemcpyAsync(e.err_host, ptr[p->ir.err_buf], sizeof(int), hipMemcpyDeviceToHost, e.stream),
+  check_hip(hipMemcpyAsync(slot, e.bufs[p->ir.err_buf], sizeof(int), hipMemcpyDeviceToHost, e.stream),
             "hipMemcpyAsync err");
+  queue_err_reset(p, e);
+}
+
+// After the run's stream has been waited on: raise the interpreter's error
+// for the flags its slot received.
+void raise_err_slot(cchip_program *p, int *slot) {
+  if (p->ir.err_buf < 0 || !slot) return;
+  int code = *slot;
+  *slot = 0;
+  if (code) throw InvalidArgument(err_message(code));
 }
 
 // Issues a run from host memory. With `staged` (the synchronous run, which
@@ -267,7 +306,7 @@ void queue_err_read(cchip_program *p, Executor &e, const std::vector<void *> &pt
 // Asynchronous runs copy straight between the caller's memory and the
 // device, since several may be in flight on one lane.
 void issue_host_run(cchip_program *p, int lane, int n, const char *const *names, const void *const *host,
-                    const size_t *bytes, void *const *outputs, bool staged) {
+                    const size_t *bytes, void *const *outputs, bool staged, int *err_slot) {
   if (p->released) throw Failure("Executor.run: this executor has been released");
   std::vector<int> which = bind_inputs(p, n, names, bytes, "Executor.run");
   Executor &e = p->execs[lane];
@@ -296,27 +335,22 @@ void issue_host_run(cchip_program *p, int lane, int n, const char *const *names,
       check_hip(hipMemcpyAsync(e.arena_host + e.arena_in, e.arena + e.arena_in, e.arena_bytes - e.arena_in,
                                hipMemcpyDeviceToHost, e.stream),
                 "download");
+    // the error word travelled with the block when it lives there
+    if (p->ir.err_buf >= 0 && e.off[p->ir.err_buf] >= 0) queue_err_reset(p, e);
+    else queue_err_read(p, e, err_slot);
   } else {
-    queue_err_read(p, e, ptr);
+    queue_err_read(p, e, err_slot);
   }
 }
 
 // After the wait of a staged run: raise the device's error, if any, and
 // copy the small outputs out of the pinned block.
 void finish_staged(cchip_program *p, Executor &e, void *const *outputs) {
-  if (!e.arena) {
-    check_err_after(p, e, e.bufs, true);
-    return;
-  }
   if (p->ir.err_buf >= 0) {
-    int *slot = (int *)(e.arena_host + e.off[p->ir.err_buf]);
-    int code = *slot;
-    if (code) {
-      *slot = 0;
-      check_hip(hipMemcpy(e.bufs[p->ir.err_buf], slot, sizeof(int), hipMemcpyHostToDevice), "hipMemcpy");
-      throw InvalidArgument(err_message(code));
-    }
+    const int64_t at = e.off[p->ir.err_buf];
+    raise_err_slot(p, at >= 0 ? (int *)(e.arena_host + at) : e.err_host);
   }
+  if (!e.arena) return;
   for (size_t o = 0; o < p->ir.outputs.size(); o++) {
     const IOSpec &os = p->ir.outputs[o];
     size_t nb = (size_t)p->ir.bufs[os.buf].bytes();
@@ -363,9 +397,9 @@ void run_resident_impl(cchip_program *p, int n, const char *const *names, void *
       if (nb) check_hip(hipMemcpyAsync(c.second, ptr[c.first], nb, hipMemcpyDeviceToDevice, e.stream), "copy_device");
     }
     if (sync) {
-      queue_err_read(p, e, e.bufs);
+      queue_err_read(p, e, e.err_host);
       check_hip(hipStreamSynchronize(e.stream), "hipStreamSynchronize");
-      check_err_after(p, e, e.bufs, true);
+      raise_err_slot(p, e.err_host);
     }
   } catch (...) {
     if (sync) (void)hipStreamSynchronize(e.stream);
@@ -525,7 +559,7 @@ int cchip_program_run(cchip_program *p, int n, const char *const *names, const v
   return guarded([&] {
     std::lock_guard<std::mutex> lk(p->mu);
     DeviceGuard dg(p->device);
-    issue_host_run(p, 0, n, names, host, bytes, outputs, true);
+    issue_host_run(p, 0, n, names, host, bytes, outputs, true, p->execs.empty() ? nullptr : p->execs[0].err_host);
     Executor &e = p->execs[0];
     check_hip(hipStreamSynchronize(e.stream), "hipStreamSynchronize");
     finish_staged(p, e, outputs);
@@ -538,13 +572,22 @@ int cchip_program_run_async(cchip_program *p, int n, const char *const *names, c
     std::lock_guard<std::mutex> lk(p->mu);
     DeviceGuard dg(p->device);
     int lane = p->next;
-    p->next = (p->next + 1) % (int)p->execs.size();
-    issue_host_run(p, lane, n, names, host, bytes, outputs, false);
     auto j = std::make_unique<cchip_job>();
     j->prog = p;
     j->lane = lane;
-    check_hip(hipEventCreateWithFlags(&j->done, hipEventDisableTiming), "hipEventCreate");
-    check_hip(hipEventRecord(j->done, p->execs[lane].stream), "hipEventRecord");
+    if (p->ir.err_buf >= 0) j->err = err_slot_get();
+    try {
+      issue_host_run(p, lane, n, names, host, bytes, outputs, false, j->err);
+      check_hip(hipEventCreateWithFlags(&j->done, hipEventDisableTiming), "hipEventCreate");
+      check_hip(hipEventRecord(j->done, p->execs[lane].stream), "hipEventRecord");
+    } catch (...) {
+      // work already queued may still write the slot: let it land first
+      (void)hipStreamSynchronize(p->execs[lane].stream);
+      err_slot_put(j->err);
+      if (j->done) (void)hipEventDestroy(j->done);
+      throw;
+    }
+    p->next = (p->next + 1) % (int)p->execs.size();
     *job = j.release();
   });
 }
@@ -560,8 +603,7 @@ int cchip_job_wait(cchip_job *j) {
     check_hip(hipEventSynchronize(j->done), "hipEventSynchronize");
     std::lock_guard<std::mutex> lk(p->mu);
     if (p->released) return;
-    Executor &e = p->execs[j->lane];
-    check_err_after(p, e, e.bufs, true);
+    raise_err_slot(p, j->err);
   });
   j->waited = true;
   j->status = rc;
@@ -571,7 +613,13 @@ int cchip_job_wait(cchip_job *j) {
 
 int cchip_job_free(cchip_job *j) {
   if (!j) return 0;
-  if (j->done) (void)hipEventDestroy(j->done);
+  if (j->done) {
+    // the slot is written by the job's own stream: recycle it only once
+    // that copy has landed
+    (void)hipEventSynchronize(j->done);
+    (void)hipEventDestroy(j->done);
+  }
+  err_slot_put(j->err);
   delete j;
   return 0;
 }

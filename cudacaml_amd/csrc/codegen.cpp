@@ -1730,9 +1730,15 @@ struct Lowering {
     // Nothing then makes a predecessor's workgroup run before its
     // successors, so the look-back never waits unboundedly: after lb_spin
     // polls of a predecessor that has published nothing, the waiting wave
-    // reads that tile's elements and folds them itself, in the tile's own
-    // order, and goes on. Progress is guaranteed whatever the dispatch
-    // order; with the usual in-order dispatch the fallback is never taken.
+    // reads that tile's elements and folds them itself (tile_fold: each
+    // lane a contiguous share, then the lanes in a tree, earlier elements
+    // always on the left) and goes on. Progress is guaranteed whatever the
+    // dispatch order; with the usual in-order dispatch the fallback is
+    // never taken. That grouping is not the tile's own (4 elements per
+    // thread, a wave scan, then wave and slice totals), so for float add
+    // the fallback rounds differently: a float look-back scan is not
+    // bit-reproducible from run to run when the fallback fires. Integer,
+    // min and max scans are exact in any grouping.
     // 8-byte values take tiles in launch order from an atomic counter, so
     // a tile only waits on tiles whose workgroups are already running.
     // Waves per workgroup (4 or 8); a slice is 4 elements per thread. 8

@@ -195,14 +195,19 @@ Graph parse_wire(const std::string &text) {
       };
       int64_t rank = lx.integer();
       need(rank >= 0 && rank <= 8, "rank must be 0..8");
+      // Element counts and every extent stay below 2^31 (device indexes
+      // are 32-bit, lower.ml:27-31); the product is checked before each
+      // multiplication, so no extent list can wrap it.
+      const int64_t kMaxNumel = (int64_t(1) << 31) - 1;
       t.numel = 1;
       for (int64_t i = 0; i < rank; i++) {
         int64_t d = lx.integer();
         need(d >= 0, "negative extent");
+        need(d <= kMaxNumel, "more than 2^31-1 elements in one tensor");
+        need(d == 0 || t.numel <= kMaxNumel / d, "more than 2^31-1 elements in one tensor");
         t.shape.push_back(d);
         t.numel *= d;
       }
-      need(t.numel < (int64_t(1) << 31), "more than 2^31-1 elements in one tensor");
       need(t.dt != DT::BOOL, "bool tensors are not storable");
       auto body_dt = [&](int x) { return g.xs[x].dt; };
       if (kind == "param") {

@@ -110,18 +110,33 @@ static uint64_t fnv1a(const std::string &s, uint64_t h = 1469598103934665603ull)
   return h;
 }
 
+// The on-disk cache directory, or "" when it must not be used: it has to be
+// a real directory owned by this user and writable by nobody else, so code
+// objects are only ever loaded from a directory this process controls.
 static std::string cache_dir() {
   const char *env = getenv("CCHIP_CACHE_DIR");
   std::string d = env && *env ? env : "/tmp/cchip-jit-cache";
   mkdir(d.c_str(), 0700);
+  struct stat st;
+  if (lstat(d.c_str(), &st) != 0 || !S_ISDIR(st.st_mode) || st.st_uid != geteuid() ||
+      (st.st_mode & (S_IWGRP | S_IWOTH)))
+    return "";
   return d;
+}
+
+// What the code objects depend on beyond the source and the options: the
+// hiprtc (compiler) version, so a toolchain update never loads stale code.
+static std::string compiler_tag() {
+  int major = 0, minor = 0;
+  if (hiprtcVersion(&major, &minor) != HIPRTC_SUCCESS) major = minor = -1;
+  return strf("hiprtc %d.%d gfx950", major, minor);
 }
 
 static std::mutex g_jit_mu;
 static std::map<uint64_t, std::vector<char>> g_co_cache;
 
 std::vector<char> jit_code_object(const std::string &name, const std::string &source) {
-  std::string opts;
+  std::string opts = compiler_tag() + " ";
   for (const char *o : kJitOptions) opts += std::string(o) + " ";
   uint64_t key = fnv1a(source, fnv1a(opts));
   {
@@ -130,8 +145,10 @@ std::vector<char> jit_code_object(const std::string &name, const std::string &so
     if (it != g_co_cache.end()) return it->second;
   }
   const char *nocache = getenv("CCHIP_NO_DISK_CACHE");
-  std::string path = cache_dir() + strf("/%016llx.co", (unsigned long long)key);
-  if (!(nocache && *nocache == '1')) {
+  const std::string dir = nocache && *nocache == '1' ? std::string() : cache_dir();
+  const bool disk = !dir.empty();
+  std::string path = dir + strf("/%016llx.co", (unsigned long long)key);
+  if (disk) {
     std::ifstream in(path, std::ios::binary);
     if (in) {
       std::vector<char> co((std::istreambuf_iterator<char>(in)), std::istreambuf_iterator<char>());
@@ -160,7 +177,7 @@ std::vector<char> jit_code_object(const std::string &name, const std::string &so
   std::vector<char> co(cs);
   hiprtcGetCode(prog, co.data());
   hiprtcDestroyProgram(&prog);
-  if (!(nocache && *nocache == '1')) {
+  if (disk) {
     std::string tmp = path + strf(".%d.tmp", (int)getpid());
     std::ofstream out(tmp, std::ios::binary);
     if (out) {

@@ -80,13 +80,15 @@ def call_mc(n_paths, dtype, m=market):
     return Graph.create("bs_mc", [("price", discounted_mean(dtype, n_paths, m, st, rate))])
 
 
-def call_mc_paths(n_paths, n_steps, dtype, m=market):
+def call_mc_paths(n_paths, n_steps, dtype, m=market, draws=None):
+    """``draws`` (a test hook, not in the reference): a tensor of the grid's
+    shape used in place of the Philox normal draws, e.g. a param."""
     grid = (n_paths, n_steps)
     s0, vol, rate, seed = _params(dtype)
     kf = lambda v: D.const(dtype, v)  # noqa: E731
     ki = lambda v: D.const(I32, v)  # noqa: E731
     dt = m.maturity / float(n_steps)
-    z = rng.normal(dtype, seed, grid)
+    z = rng.normal(dtype, seed, grid) if draws is None else draws
     s0b = D.broadcast(grid, s0)
     volb = D.broadcast(grid, vol)
     rateb = D.broadcast(grid, rate)
@@ -103,9 +105,9 @@ def call_greeks(n_paths, dtype, m=market):
     return G.grad(call_mc(n_paths, dtype, m), "price", ["s0", "vol", "rate"])
 
 
-def call_paths_greeks(n_paths, n_steps, dtype, m=market, wrt=("s0", "vol")):
+def call_paths_greeks(n_paths, n_steps, dtype, m=market, wrt=("s0", "vol"), draws=None):
     """The multi-step pricer differentiated: delta and vega (and rho if asked)."""
-    return G.grad(call_mc_paths(n_paths, n_steps, dtype, m), "price", list(wrt))
+    return G.grad(call_mc_paths(n_paths, n_steps, dtype, m, draws), "price", list(wrt))
 
 
 def inputs(dtype, m=market, seed=7):

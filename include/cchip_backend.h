@@ -79,7 +79,10 @@ int cchip_program_run(cchip_program *program, int n_inputs, const char *const *n
 /* run_async / wait: issue on the next executor of the ring and return; the
    host input and output memory must stay valid until cchip_job_wait
    returns. wait may be called more than once (cudacaml_backend_cuda.ml
-   :357-365). */
+   :357-365). Each job reports only the device-side index errors of its own
+   run (and of run_resident_into calls with sync == 0 queued on its lane
+   before it): its lane's stream copies the error word into the job's own
+   pinned slot and then clears it. */
 int cchip_program_run_async(cchip_program *program, int n_inputs, const char *const *names,
                             const void *const *host, const size_t *bytes, void *const *outputs, cchip_job **job);
 int cchip_job_wait(cchip_job *job);

@@ -379,6 +379,9 @@ static void parse_tensor(orc_graph *g, lexer *lx) {
   for (int i = 0; i < t.rank; i++) {
     t.dims[i] = tok_int(lx);
     if (t.dims[i] < 0) fail("oracle: wire line %d: negative extent", lx->line);
+    /* checked before multiplying: no extent list can wrap the count */
+    if (t.dims[i] > ((int64_t)1 << 62) || (t.dims[i] && t.numel > ((int64_t)1 << 62) / t.dims[i]))
+      fail("oracle: wire line %d: too many elements", lx->line);
     t.numel *= t.dims[i];
   }
   t.a = t.b = t.init = t.body = -1;

@@ -359,6 +359,45 @@ def test_small_values_through_the_staging_block(device):
         c.release()
 
 
+@pytest.mark.parametrize("streams", [1, 2])
+def test_async_errors_stay_with_their_job(device, streams):
+    """Jobs queued on one lane (and on a ring of two) each report only
+    their own device-side index error: a clean job queued before a bad one
+    waits cleanly even when the bad one has finished first, the bad one
+    raises, and later runs start from a clear error word."""
+    from cudacaml_amd import dsl as D
+    from cudacaml_amd.ir import I32
+
+    n = 1 << 16
+    x = D.param("x", F32, (n,))
+    i = D.param("i", I32, (n,))
+    g = Graph.create("gx", [("g", D.gather(i, x))])
+    xv = np.arange(n, dtype=np.float32)
+    good = [("x", xv), ("i", (np.arange(n)[::-1] % n).astype(np.int32))]
+    badi = good[1][1].copy()
+    badi[n // 2] = n + 7
+    bad = [("x", xv), ("i", badi)]
+    c = H.compile_with(streams, g)
+    try:
+        jobs = [H.run_async(c, good), H.run_async(c, bad), H.run_async(c, good), H.run_async(c, bad),
+                H.run_async(c, good)]
+        # the last job done first: every earlier job on its lane is done too
+        H.wait(jobs[-1])
+        for k in (0, 2):
+            np.testing.assert_array_equal(dict(H.wait(jobs[k]))["g"], xv[good[1][1]])
+        for k in (1, 3):
+            with pytest.raises(ValueError, match="gather index out of bounds"):
+                H.wait(jobs[k])
+            with pytest.raises(ValueError, match="gather index out of bounds"):
+                H.wait(jobs[k])  # a second wait reports the same outcome
+        np.testing.assert_array_equal(dict(H.run(c, good))["g"], xv[good[1][1]])
+        with pytest.raises(ValueError, match="gather index out of bounds"):
+            H.run(c, bad)
+        np.testing.assert_array_equal(dict(H.wait(H.run_async(c, good)))["g"], xv[good[1][1]])
+    finally:
+        c.release()
+
+
 # ---- recorded launch sequences (HIP graphs) ------------------------------------
 
 

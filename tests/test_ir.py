@@ -135,3 +135,35 @@ def test_greeks_graph_structure():
     assert [n for n, _ in g.outputs] == ["price", "dprice/ds0", "dprice/dvol", "dprice/drate"]
     kernels = [l for l in H.plan(g).splitlines() if l.startswith("kernel")]
     assert len(kernels) < 40
+
+
+@pytest.mark.parametrize("dims", ["2 4294967296 4294967296", "2 65536 65536", "1 2147483648", "2 0 2147483648",
+                                  "3 2048 2048 512"])
+def test_wire_extents_that_wrap_or_exceed_2_31_are_rejected(dims):
+    """Element counts are checked before each multiplication: [2^32; 2^32]
+    (whose 64-bit product wraps to 0) and every tensor of 2^31 elements or
+    more, or with such an extent, is rejected by the backend's parser."""
+    import ctypes
+
+    from cudacaml_amd._lib import check, lib
+
+    wire = "cchip-graph 1 g\nt 1 param f32 %s x\no r 1\nend\n" % dims
+    out = ctypes.c_void_p()
+    with pytest.raises(ValueError, match="2\\^31-1 elements"):
+        check(lib().cchip_backend_plan(wire.encode(), ctypes.byref(out)))
+    lib_o = oracle._load()
+    err = ctypes.create_string_buffer(256)
+    if dims.startswith("2 4294967296"):
+        assert not lib_o.orc_parse(wire.encode(), err, 256)
+        assert b"too many elements" in err.value
+
+
+def test_wire_largest_tensor_is_accepted():
+    import ctypes
+
+    from cudacaml_amd._lib import check, lib
+
+    wire = "cchip-graph 1 g\nt 1 param i32 2 32767 65537 x\no r 1\nend\n"
+    out = ctypes.c_void_p()
+    check(lib().cchip_backend_plan(wire.encode(), ctypes.byref(out)))
+    lib().cchip_free(out)
