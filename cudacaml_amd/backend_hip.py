@@ -286,12 +286,7 @@ def run_resident(c, inputs):
     return [(o.name, Resident(Buffer(outs[i], o.nbytes), o.dtype, o.shape)) for i, o in enumerate(c.outputs)]
 
 
-def run_resident_into(c, inputs, outputs, sync=True):
-    """Extension (no reference counterpart): like ``run_resident`` but into
-    caller-owned output residents, optionally without synchronising."""
-    if c.released:
-        raise RuntimeError("Executor.run_resident: this executor has been released")
-    n, names, ptrs, sizes = _bind_resident(c, inputs, "Executor.run_resident")
+def _bind_outputs(c, outputs):
     by_name = dict(_items(outputs))
     ptr_out = []
     for o in c.outputs:
@@ -301,8 +296,30 @@ def run_resident_into(c, inputs, outputs, sync=True):
         if r.buf.nbytes != o.nbytes:
             raise ValueError("Executor.run_resident: output %s is %d bytes, needs %d" % (o.name, r.buf.nbytes, o.nbytes))
         ptr_out.append(r.buf.ptr)
-    arr = (ctypes.c_void_p * max(1, len(ptr_out)))(*ptr_out)
+    return (ctypes.c_void_p * max(1, len(ptr_out)))(*ptr_out)
+
+
+def run_resident_into(c, inputs, outputs, sync=True):
+    """Extension (no reference counterpart): like ``run_resident`` but into
+    caller-owned output residents, optionally without synchronising."""
+    if c.released:
+        raise RuntimeError("Executor.run_resident: this executor has been released")
+    n, names, ptrs, sizes = _bind_resident(c, inputs, "Executor.run_resident")
+    arr = _bind_outputs(c, outputs)
     check(lib().cchip_program_run_resident_into(c.handle, n, names, ptrs, sizes, arr, 1 if sync else 0))
+
+
+def run_resident_noalloc(c, inputs, outputs, stream=None):
+    """Extension (no reference counterpart), for callers that cannot
+    allocate device memory: ``run_resident_into`` without synchronising, on
+    ``stream`` (a raw HIP stream pointer; None is the default stream), with
+    the template scratch taken from the library's static 32 MiB array.
+    Only issues the work: synchronise the stream before reading outputs."""
+    if c.released:
+        raise RuntimeError("Executor.run_resident: this executor has been released")
+    n, names, ptrs, sizes = _bind_resident(c, inputs, "Executor.run_resident")
+    arr = _bind_outputs(c, outputs)
+    check(lib().cchip_program_run_resident_noalloc(c.handle, n, names, ptrs, sizes, arr, stream))
 
 
 def time_kernel(c, kernel_name):

@@ -2,7 +2,9 @@
 
 The library is host code over the HIP runtime and hiprtc; the kernels it
 runs are generated per graph and compiled by hiprtc for gfx950 at
-``compile`` time. ``check_templates`` JIT-compiles a representative set of
+``compile`` time. Its own device code (``csrc/*.hip``, built for gfx950
+here) is the static scratch of the allocation-free entry point and the
+kernel that clears it. ``check_templates`` JIT-compiles a representative set of
 generated modules without a GPU, so template errors surface at build time.
 """
 
@@ -23,11 +25,12 @@ ASAN_RUNTIME = os.path.join(ROCM, "llvm", "lib", "clang", "*", "lib", "linux", "
 
 def build(verbose=False, asan=False):
     """``asan=True`` builds ``libcchip_asan.so`` with AddressSanitizer on
-    the host code only (the library holds no device code; the kernels are
-    compiled by hiprtc at run time). It is for CPU runs: load it with
+    the host code only (the generated kernels are compiled by hiprtc at run
+    time; the library's own device code is one fill kernel and the static
+    scratch array of the allocation-free entry point). It is for CPU runs: load it with
     ``CCHIP_LIB`` pointing at it and the sanitizer runtime preloaded (see
     ``asan_env``)."""
-    srcs = sorted(glob.glob(os.path.join(HERE, "csrc", "*.cpp")))
+    srcs = sorted(glob.glob(os.path.join(HERE, "csrc", "*.cpp"))) + sorted(glob.glob(os.path.join(HERE, "csrc", "*.hip")))
     out = ASAN_LIB if asan else LIB
     tmp = out + ".tmp%d" % os.getpid()
     cmd = [

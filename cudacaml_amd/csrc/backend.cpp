@@ -89,6 +89,15 @@ struct cchip_program {
   // timing hook
   int timed = -1;
   std::vector<std::pair<hipEvent_t, hipEvent_t>> ev_used, ev_free;
+  // Allocation-free runs (cchip_program_run_resident_noalloc): each scratch
+  // buffer's offset in the static scratch (-1 for other buffers) and their
+  // total, which outputs are copied rather than written in place, and host
+  // arrays sized here so that such a run allocates no memory at all.
+  std::vector<int64_t> na_off;
+  int64_t na_bytes = 0;
+  std::vector<char> na_out_copy;
+  std::vector<int> na_which;
+  std::vector<void *> na_ptr, na_vals, na_args;
 };
 
 struct cchip_job {
@@ -408,6 +417,41 @@ void run_resident_impl(cchip_program *p, int n, const char *const *names, void *
   }
 }
 
+// Host-side layout of an allocation-free run, fixed at compile time:
+// scratch buffers packed 256-byte aligned into the static scratch, in
+// buffer order (all of them at once, as the pool holds them).
+void prepare_noalloc(cchip_program *p) {
+  const ProgramIR &ir = p->ir;
+  p->na_off.assign(ir.bufs.size(), -1);
+  int64_t at = 0;
+  for (size_t b = 0; b < ir.bufs.size(); b++)
+    if (ir.bufs[b].role == BufRole::Scratch) {
+      p->na_off[b] = at;
+      at += (std::max<int64_t>(ir.bufs[b].bytes(), 1) + 255) & ~int64_t(255);
+    }
+  p->na_bytes = at;
+  p->na_out_copy.assign(ir.outputs.size(), 0);
+  std::vector<char> bound(ir.bufs.size(), 0);
+  for (auto &ps : ir.params) bound[ps.buf] = 1;
+  for (size_t o = 0; o < ir.outputs.size(); o++) {
+    int b = ir.outputs[o].buf;
+    if (bound[b]) p->na_out_copy[o] = 1;
+    bound[b] = 1;
+  }
+  p->na_which.assign(ir.params.size(), -1);
+  p->na_ptr.assign(ir.bufs.size(), nullptr);
+  size_t maxargs = 1;
+  for (auto &k : ir.kernels) maxargs = std::max(maxargs, k.args.size());
+  p->na_vals.assign(maxargs, nullptr);
+  p->na_args.assign(maxargs, nullptr);
+  // the static scratch's address on this device (current here), looked up
+  // now, at set-up; a failure surfaces on the first allocation-free run
+  try {
+    (void)noalloc_scratch(p->device);
+  } catch (...) {
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -455,6 +499,7 @@ int cchip_backend_compile(const char *graph, int device, int streams, cchip_prog
     // eager launches for resident steps, and slower for short host runs.
     p->graphs = tune_knob("graphs", 0) != 0 && nlaunch >= tune_knob("graph_min_kernels", 2);
     for (auto &k : p->ir.kernels) p->kfn.push_back(module_kernel(*p->mod, k.name));
+    prepare_noalloc(p.get());
     p->execs.resize(streams);
     try {
       for (int s = 0; s < streams; s++) {
@@ -639,6 +684,62 @@ int cchip_program_run_resident_into(cchip_program *p, int n, const char *const *
     std::lock_guard<std::mutex> lk(p->mu);
     DeviceGuard dg(p->device);
     run_resident_impl(p, n, names, dev_inputs, bytes, nullptr, dev_outputs, sync != 0);
+  });
+}
+
+int cchip_program_run_resident_noalloc(cchip_program *p, int n, const char *const *names, void *const *dev_inputs,
+                                       const size_t *bytes, void *const *dev_outputs, void *stream) {
+  return guarded([&] {
+    std::lock_guard<std::mutex> lk(p->mu);
+    if (p->released) throw Failure("Executor.run_resident: this executor has been released");
+    const ProgramIR &ir = p->ir;
+    const size_t cap = noalloc_scratch_capacity();
+    if (p->na_bytes > (int64_t)cap)
+      throw InvalidArgument(strf("run_resident_noalloc: program %s needs %lld bytes of scratch, more than the "
+                                 "%zu bytes of the static scratch",
+                                 ir.name.c_str(), (long long)p->na_bytes, cap));
+    // inputs by name, exact byte sizes, before any device work
+    for (size_t k = 0; k < ir.params.size(); k++) {
+      const IOSpec &ps = ir.params[k];
+      int w = -1;
+      for (int i = 0; i < n && w < 0; i++)
+        if (names[i] && ps.name == names[i]) w = i;
+      if (w < 0) throw InvalidArgument("Executor.run_resident: missing input " + ps.name);
+      if (bytes[w] != (size_t)ir.bufs[ps.buf].bytes())
+        throw InvalidArgument(strf("Executor.run_resident: input %s is %zu bytes, parameter %s needs %lld",
+                                   ps.name.c_str(), bytes[w], ir.bufs[ps.buf].name.c_str(),
+                                   (long long)ir.bufs[ps.buf].bytes()));
+      p->na_which[k] = w;
+    }
+    DeviceGuard dg(p->device);
+    char *base = (char *)noalloc_scratch(p->device);
+    const Executor &e = p->execs[0];
+    for (size_t b = 0; b < ir.bufs.size(); b++)
+      p->na_ptr[b] = p->na_off[b] >= 0 ? (void *)(base + p->na_off[b]) : e.bufs[b];
+    for (size_t k = 0; k < ir.params.size(); k++) p->na_ptr[ir.params[k].buf] = dev_inputs[p->na_which[k]];
+    for (size_t o = 0; o < ir.outputs.size(); o++)
+      if (!p->na_out_copy[o]) p->na_ptr[ir.outputs[o].buf] = dev_outputs[o];
+    hipStream_t st = (hipStream_t)stream;
+    // the scratch starts at zero, as a fresh pool does
+    noalloc_scratch_clear(base, (size_t)p->na_bytes, stream);
+    for (auto &op : ir.plan) {
+      if (op.kind != OpK::Launch) continue;
+      const KernelSpec &k = ir.kernels[op.kernel];
+      for (size_t i = 0; i < k.args.size(); i++) {
+        p->na_vals[i] = p->na_ptr[k.args[i]];
+        p->na_args[i] = &p->na_vals[i];
+      }
+      check_hip(hipModuleLaunchKernel((hipFunction_t)p->kfn[op.kernel], k.grid, k.grid_y, 1, k.block, k.block_y, 1,
+                                      k.shared_bytes, st, p->na_args.data(), nullptr),
+                "hipModuleLaunchKernel");
+    }
+    for (size_t o = 0; o < ir.outputs.size(); o++) {
+      if (!p->na_out_copy[o]) continue;
+      size_t nb = (size_t)ir.bufs[ir.outputs[o].buf].bytes();
+      if (nb)
+        check_hip(hipMemcpyAsync(dev_outputs[o], p->na_ptr[ir.outputs[o].buf], nb, hipMemcpyDeviceToDevice, st),
+                  "copy_device");
+    }
   });
 }
 

@@ -190,4 +190,9 @@ std::shared_ptr<Module> jit_compile(const std::string &name, const std::string &
 void *module_kernel(Module &m, const std::string &name);
 std::vector<char> jit_code_object(const std::string &name, const std::string &source);
 
+// The static scratch of the allocation-free entry point (noalloc.hip).
+size_t noalloc_scratch_capacity();
+void *noalloc_scratch(int device);
+void noalloc_scratch_clear(void *base, size_t bytes, void *stream);
+
 }  // namespace cchip

@@ -104,6 +104,26 @@ int cchip_program_run_resident_into(cchip_program *program, int n_inputs, const 
                                     void *const *dev_inputs, const size_t *bytes, void *const *dev_outputs,
                                     int sync);
 
+/* No counterpart in the reference. For callers that cannot allocate device
+   memory: code under HIP graph capture, serving loops, harnesses that
+   forbid hipMalloc. Runs like run_resident_into with sync == 0, but on
+   `stream` (NULL: the default stream), and calls no hipMalloc, hipFree or
+   other allocating routine. The template scratch (look-back status words,
+   split partials, scatter counts and staged pairs) comes from a static
+   device array of 32 MiB per GPU inside this library instead of the
+   program's pool; it is cleared by a kernel at the start of every call.
+   A program whose scratch exceeds 32 MiB is CCHIP_INVALID_ARGUMENT before
+   any device work. All calls on one GPU share that array, and each uses the
+   program's executor-0 pool for its intermediates: calls that overlap on
+   one GPU (any program), or that overlap another run of the same program,
+   race. Device-side index errors are reported by the program's next
+   synchronising run on executor 0, after the caller has synchronised
+   `stream`. Work is only issued; synchronise `stream` before reading the
+   outputs. */
+int cchip_program_run_resident_noalloc(cchip_program *program, int n_inputs, const char *const *names,
+                                       void *const *dev_inputs, const size_t *bytes, void *const *dev_outputs,
+                                       void *stream);
+
 /* The stream executor `lane` issues its work on (NULL for lane 0). */
 int cchip_program_stream(const cchip_program *program, int lane, void **stream);
 

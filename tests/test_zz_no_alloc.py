@@ -1,0 +1,133 @@
+"""The allocation-free entry point, cchip_program_run_resident_noalloc: the
+template scratch comes from the library's static device array, the work
+runs on a stream the caller chooses, and no device memory is allocated.
+
+Every call is checked against the existing run_resident_into on the same
+program and the same inputs, bit for bit (the outputs here are integer
+scans and scatters, a max scan and a fixed-order split reduction, all
+exactly reproducible), over calls in a row whose programs lay the static
+scratch out differently: a program that uses 28 of its 32 MiB (two
+look-back scans, a split reduction, a sliced scatter), then a smaller one
+(the direct scatter), then the first again with other inputs."""
+
+import math
+
+import numpy as np
+import pytest
+
+from cudacaml_amd import backend_hip as H
+from cudacaml_amd import dsl as D
+from cudacaml_amd.ir import F32, I32, Graph
+from cudacaml_amd.runtime import Buffer, Stream
+
+pytestmark = pytest.mark.gpu
+
+
+def program(n, bins):
+    v = D.param("v", I32, (n,))
+    x = D.param("x", F32, (n,))
+    idx = D.param("idx", I32, (n,))
+    w = D.param("w", I32, (n,))
+    p = D.scan(D.add, D.const(I32, 0), v)
+    return Graph.create("noalloc", [
+        ("p", p),
+        ("m", D.scan(D.max, D.const(F32, -math.inf), x)),
+        ("t", D.reduce(D.add, D.const(F32, 0.0), x)),
+        ("h", D.scatter_add(idx, w, (bins,))),
+        ("v", v),    # an output that is a param: copied
+        ("p2", p),   # one buffer under two names: copied
+    ])
+
+
+def inputs(n, bins, seed):
+    r = np.random.default_rng(seed)
+    return [("v", r.integers(-9, 17, n, dtype=np.int32)),
+            ("x", r.standard_normal(n).astype(np.float32)),
+            ("idx", r.integers(0, bins, n, dtype=np.int32)),
+            ("w", r.integers(-3, 8, n, dtype=np.int32))]
+
+
+def scratch_bytes(g):
+    size = {"f32": 4, "i32": 4, "f64": 8, "i64": 8}
+    tot = 0
+    for line in H.plan(g).splitlines():
+        f = line.split()
+        if f[0] == "buffer" and f[5] == "scratch":
+            tot += (max(int(f[4]) * size[f[3]], 1) + 255) // 256 * 256
+    return tot
+
+
+def outputs_of(c):
+    return [(o.name, H.Resident(Buffer.alloc(o.nbytes), o.dtype, o.shape)) for o in c.outputs]
+
+
+def free_all(rs):
+    for _, r in rs:
+        H.free_resident(r)
+
+
+def check_call(c, ins, stream):
+    """One allocation-free call against run_resident_into on the same
+    inputs; also against numpy for the integer outputs."""
+    res = [(n, H.upload(v)) for n, v in ins]
+    want_o, got_o = outputs_of(c), outputs_of(c)
+    try:
+        H.run_resident_into(c, res, want_o, sync=True)
+        live = Buffer.live_count()
+        H.run_resident_noalloc(c, res, got_o, stream.ptr)
+        stream.synchronize()
+        assert Buffer.live_count() == live
+        want = {n: H.download(r) for n, r in want_o}
+        got = {n: H.download(r) for n, r in got_o}
+        for name in want:
+            np.testing.assert_array_equal(got[name], want[name], err_msg=name)
+        v = dict(ins)
+        np.testing.assert_array_equal(got["p"], np.cumsum(v["v"], dtype=np.int64).astype(np.int32))
+        np.testing.assert_array_equal(got["p2"], got["p"])
+        np.testing.assert_array_equal(got["v"], v["v"])
+        np.testing.assert_array_equal(got["m"], np.maximum.accumulate(v["x"]))
+        bins = c.outputs[3].shape[0]
+        np.testing.assert_array_equal(got["h"], np.bincount(v["idx"], weights=v["w"], minlength=bins).astype(np.int32))
+    finally:
+        free_all(res)
+        free_all(want_o)
+        free_all(got_o)
+
+
+@pytest.mark.parametrize("on", ["created", "default"])
+def test_noalloc_calls_in_a_row_match_run_resident_into(device, on):
+    big, small = ((1 << 22), 1 << 16), ((1 << 20) + 3, 1 << 12)
+    ga, gb = program(*big), program(*small)
+    assert 24 << 20 < scratch_bytes(ga) <= 32 << 20
+    assert 0 < scratch_bytes(gb) < scratch_bytes(ga)
+    stream = Stream.create() if on == "created" else Stream.default
+    ca, cb = H.compile(ga), H.compile(gb)
+    try:
+        check_call(ca, inputs(*big, seed=1), stream)
+        check_call(cb, inputs(*small, seed=2), stream)
+        check_call(ca, inputs(*big, seed=3), stream)
+    finally:
+        ca.release()
+        cb.release()
+
+
+def test_noalloc_rejects_programs_beyond_the_static_scratch(device):
+    n, bins = 1 << 23, 1 << 20
+    g = program(n, bins)
+    assert scratch_bytes(g) > 32 << 20
+    c = H.compile(g)
+    res = [(nm, H.upload(v)) for nm, v in inputs(n, bins, seed=4)]
+    outs = outputs_of(c)
+    try:
+        live = Buffer.live_count()
+        with pytest.raises(ValueError, match="static scratch"):
+            H.run_resident_noalloc(c, res, outs)
+        assert Buffer.live_count() == live
+        with pytest.raises(ValueError, match="missing input"):
+            H.run_resident_noalloc(c, res[:2], outs)
+    finally:
+        free_all(res)
+        free_all(outs)
+        c.release()
+    with pytest.raises(RuntimeError, match="released"):
+        H.run_resident_noalloc(c, res, outs)
