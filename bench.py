@@ -232,44 +232,93 @@ def step(H, w, sync=False):
         H.run_resident_into(c, ins, outs, sync=sync)
 
 
-def cpu_baseline(name, C, H=None):
-    """The oracle on a bounded sample of the workload; returns (value, unit,
-    sample description, seconds). The sample's inputs are the leading part
-    of the benchmark's own inputs (same generator, same seeds), drawn on the
-    device when one is given."""
+def host_cpu():
+    """The host's CPU model and the cores this process may use."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count()
+    return {"model": model, "nproc": os.cpu_count(), "usable": usable}
+
+
+def cpu_baseline(name, C, H, w):
+    """The oracle (one thread) on the whole workload or a bounded sample of
+    it, over the benchmark's own inputs (downloaded from the device, or the
+    leading part of the same generator stream). Returns (value in the
+    config's unit, unit, sample description, seconds)."""
+    import numpy as np
+
     import oracle
+    from cudacaml_amd.examples import black_scholes as bs
+    from cudacaml_amd.ir import F32, F64
+
+    def timed(g, ins):
+        c = oracle.Interp.compile(g)
+        t0 = time.perf_counter()
+        oracle.Interp.run(c, ins)
+        return time.perf_counter() - t0
+
+    def host_inputs(k=0):
+        return [(n, H.download(r)) for n, r in w.programs[k][2]]
+
+    def plan_total(g):
+        return sum(b for _, (_, b) in plan_bytes(H, g).items())
 
     if name in ("poly", "poly64"):
         from cudacaml_amd.examples import refbench as RB
-        from cudacaml_amd.ir import F32, F64
 
         dt = F64 if name == "poly64" else F32
         n = 1 << 22
-        g = RB.poly_graph(n, dt)
-        c = oracle.Interp.compile(g)
-        x = RB.x_input(n, dt)
-        t0 = time.perf_counter()
-        oracle.Interp.run(c, [("x", x)])
-        secs = time.perf_counter() - t0
+        secs = timed(RB.poly_graph(n, dt), [("x", RB.x_input(n, dt))])
         return (n * RB.poly_flops() / secs / 1e9, "GFLOP/s",
                 "poly graph on the first 2^22 of the 2^24 elements (a quarter of the workload)", secs)
     if name == "rows":
-        r = C.ROWS2
-        n = C.SCAN2
-        if H is not None:
-            x = H.download(device_inputs(H, C.gen_uniform_pm1((r, C.ROWS2)), 3))
-            v = H.download(device_inputs(H, C.gen_small_ints((n,)), 4))
-        else:
-            x = C.uniform_pm1(3, (r, C.ROWS2))
-            v = C.small_ints(4, (n,))
-        g1, g2 = C.rows(r, C.ROWS2), C.global_scan(n)
-        c1, c2 = oracle.Interp.compile(g1), oracle.Interp.compile(g2)
-        t0 = time.perf_counter()
-        oracle.Interp.run(c1, [("x", x)])
-        oracle.Interp.run(c2, [("v", v)])
-        dt = time.perf_counter() - t0
-        nbytes = 3 * x.nbytes + 2 * r * 4 + x.nbytes + 2 * v.nbytes
-        return nbytes / dt / 1e9, "GB/s", "the whole workload: rows graph on f32[8192,8192] + global scan on i32[2^28]", dt
+        x, v = host_inputs(0)[0][1], host_inputs(1)[0][1]
+        secs = timed(C.rows(), [("x", x)]) + timed(C.global_scan(), [("v", v)])
+        nbytes = plan_total(C.rows()) + plan_total(C.global_scan())
+        return nbytes / secs / 1e9, "GB/s", "the whole workload: rows graph on f32[8192,8192] + global scan on i32[2^28]", secs
+    if name in ("saxpy", "chain", "scatter", "scatter_perm"):
+        g, ins = w.programs[0][0], host_inputs(0)
+        secs = timed(g, ins)
+        return plan_total(g) / secs / 1e9, "GB/s", "the whole workload", secs
+    if name in ("matmul", "matmul64", "matmul_grad"):
+        # The interpreter's matmul is one sequential k-loop per output
+        # (R9), so its rate is the same for every row: time the leading
+        # rows of the benchmark's own product and report that rate.
+        ins = dict(host_inputs(0))
+        a, b = ins["a"], ins["b"]
+        n = b.shape[1]
+        rows = 64 if a.dtype == np.float64 else 32
+        dt = F64 if a.dtype == np.float64 else F32
+        secs = timed(C.matmul(n, dt, k=a.shape[1], m=rows), [("a", np.ascontiguousarray(a[:rows])), ("b", b)])
+        what = "the first %d rows of A@B (%s %dx%d), %.2f%% of the product's flops" % (
+            rows, dt.name, n, n, 100.0 * rows / a.shape[0])
+        if name == "matmul_grad":
+            what += "; the rate applies to the grad graph's three %d^3 products (extrapolated)" % n
+        return 2 * rows * a.shape[1] * n / secs / 1e12, "TFLOP/s", what, secs
+    if name in ("mc", "mc64", "mc_greeks"):
+        # Draw counters are flat indices (path * steps + step), so the
+        # first P paths of the workload see exactly the same draws.
+        dt = F64 if name == "mc64" else F32
+        p = 1 << 14
+        g = C.mc_greeks(p, C.STEPS5, dt) if name == "mc_greeks" else C.mc_paths(p, C.STEPS5, dt)
+        secs = timed(g, bs.inputs(dt, seed=7))
+        return p / secs, "paths/s", "the first 2^14 of the 2^22 paths (same draws), 64 steps", secs
+    if name in BS_CONFIGS:
+        dt = F64 if name.endswith("64") else F32
+        p = 1 << 20
+        g = bs.call_greeks(p, dt) if name.startswith("bs_greeks") else bs.call_mc(p, dt)
+        secs = timed(g, bs.inputs(dt, seed=1))
+        return p / secs, "paths/s", "the first 2^20 of the 2^22 paths (same draws)", secs
     raise SystemExit("no CPU baseline for %s" % name)
 
 
@@ -296,20 +345,43 @@ COPY_BYTES = (1 << 28) * 4  # read once and written once by the calibration kern
 
 
 # Configs whose dominant kernel is bound by instruction issue rather than
-# HBM: a third counter pass counts its VALU instructions.
+# HBM: a third counter pass counts its VALU instructions and clocks. The
+# issue limit is one wave64 VALU instruction per SIMD every 4 clocks
+# (packed FP32 is off in every build here, so it is not counted).
 VALU_CONFIGS = ("poly", "poly64", "mc", "mc64", "mc_greeks", "bs", "bs64", "bs_greeks", "bs_greeks64")
-# One wave64 VALU instruction per SIMD every 4 clocks: 256 CUs x 64 lanes
-# x 2.4 GHz lane-instructions per second (packed FP32 is off in every
-# build here, so it is not counted).
-VALU_ISSUE_PEAK = 256 * 64 * 2.4e9
+
+
+# Matmul configs: one more counter pass for the matrix cores.
+MFMA_CONFIGS = ("matmul", "matmul64", "matmul_grad")
+# GRBM_GUI_ACTIVE is counted per XCC and the csv sums the 8 of them; a
+# dispatch that covers every XCC runs for (sum / 8) cycles.
+XCC_COUNT = 8
+SIMDS_PER_CU = 4
+# Published MI355X matrix peaks at the 2.4 GHz they are quoted for, as
+# flops per clock for the whole chip.
+MFMA_CLOCK_HZ = 2.4e9
+
+
+def counter_passes(config):
+    """The rocprofv3 --pmc passes for a config, each a list of counters
+    collected together: the two traffic counters, then the VALU
+    instructions with the same dispatches' cycle count (issue-bound
+    configs), or the matrix-core busy cycles and math operations with the
+    cycle count (matmul configs)."""
+    passes = [["FETCH_SIZE"], ["WRITE_SIZE"]]
+    if config in VALU_CONFIGS:
+        passes.append(["SQ_INSTS_VALU", "GRBM_GUI_ACTIVE"])
+    if config in MFMA_CONFIGS:
+        passes.append(["SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_F32", "SQ_INSTS_VALU_MFMA_MOPS_F64",
+                       "GRBM_GUI_ACTIVE"])
+    return passes
 
 
 def measure_counters(config, steps=2):
-    """rocprofv3 counter passes over the workload (FETCH_SIZE, then
-    WRITE_SIZE, KiB per dispatch; SQ_INSTS_VALU, wave instructions per
-    dispatch, for the VALU-bound configs), each run as a child process
-    before this process touches the GPU. Returns ({kernel: {counter:
-    median}}, copy kernel name) or (None, reason)."""
+    """rocprofv3 counter passes over the workload (counter_passes), each
+    run as a child process before this process touches the GPU. Values are
+    per dispatch (the csv's sum over the counter's instances). Returns
+    ({kernel: {counter: median}}, copy kernel name) or (None, reason)."""
     import csv
     import glob
     import shutil
@@ -322,33 +394,38 @@ def measure_counters(config, steps=2):
         return None, "rocprofv3 not found"
     per = {}
     copy_name = None
-    for counter in ("FETCH_SIZE", "WRITE_SIZE") + (("SQ_INSTS_VALU",) if config in VALU_CONFIGS else ()):
+    for group in counter_passes(config):
         out = tempfile.mkdtemp(prefix="cchip_pmc_", dir="/tmp")
-        cmd = [exe, "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "p", "--",
-               sys.executable, os.path.abspath(__file__), "--config", config, "--steps", str(steps),
-               "--pmc-child"]
+        cmd = [exe, "--pmc"] + group + ["--output-format", "csv", "-d", out, "-o", "p", "--",
+                                         sys.executable, os.path.abspath(__file__), "--config", config, "--steps",
+                                         str(steps), "--pmc-child"]
         env = dict(os.environ, TMPDIR="/tmp")
-        log("traffic: %s pass" % counter)
+        log("counters: %s pass" % " ".join(group))
         try:
             r = subprocess.run(cmd, cwd="/tmp", env=env, stdout=subprocess.PIPE, stderr=subprocess.PIPE,
                                timeout=180, start_new_session=True)
         except subprocess.TimeoutExpired:
-            return None, "rocprofv3 %s pass timed out" % counter
+            return None, "rocprofv3 %s pass timed out" % " ".join(group)
         lines = [l for l in r.stdout.decode(errors="replace").splitlines() if l.startswith("{")]
         if r.returncode != 0 or not lines:
-            return None, "rocprofv3 %s pass failed (rc %d)" % (counter, r.returncode)
+            return None, "rocprofv3 %s pass failed (rc %d)" % (" ".join(group), r.returncode)
         copy_name = json.loads(lines[-1])["copy"]
         files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
         if not files:
-            return None, "no counter file from the %s pass" % counter
+            return None, "no counter file from the %s pass" % " ".join(group)
         vals = {}
         with open(files[0]) as f:
-            for row in csv.DictReader(f):
-                if row["Counter_Name"] == counter:
-                    vals.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+            for i, row in enumerate(csv.DictReader(f)):
+                if row["Counter_Name"] not in group:
+                    continue
+                # rows of one dispatch (one per counter instance, if the
+                # csv splits them) are summed
+                d = row.get("Dispatch_Id") or row.get("Correlation_Id") or str(i)
+                by = vals.setdefault((row["Kernel_Name"], row["Counter_Name"]), {})
+                by[d] = by.get(d, 0.0) + float(row["Counter_Value"])
         shutil.rmtree(out, ignore_errors=True)
-        for k, v in vals.items():
-            per.setdefault(k, {})[counter] = statistics.median(v)
+        for (k, cn), by_dispatch in vals.items():
+            per.setdefault(k, {})[cn] = statistics.median(by_dispatch.values())
     return per, copy_name
 
 
@@ -535,21 +612,44 @@ def main():
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic}
     per = counters[0] or {}
-    if args.config in VALU_CONFIGS and "SQ_INSTS_VALU" in per.get(dom, {}):
-        # Issue-bound kernels: VALU lane-instructions per second (wave
-        # instructions counted by SQ_INSTS_VALU, times 64 lanes) against
-        # the issue peak, and per element of the kernel's output.
-        winst = per[dom]["SQ_INSTS_VALU"]
+    simds = info.multiprocessors * SIMDS_PER_CU
+    dc = per.get(dom, {})
+    if args.config in VALU_CONFIGS and "SQ_INSTS_VALU" in dc and dc.get("GRBM_GUI_ACTIVE"):
+        # Issue-bound kernels: wave64 VALU instructions (SQ_INSTS_VALU)
+        # against the issue limit of one per SIMD every 4 clocks, over the
+        # clocks of the same dispatches (GRBM_GUI_ACTIVE, same pass), so no
+        # clock rate is assumed; lane-instructions per element of the
+        # kernel's output; the clock those cycles imply over this run's
+        # HIP-event time, for reference.
+        winst = dc["SQ_INSTS_VALU"]
+        cycles = dc["GRBM_GUI_ACTIVE"] / XCC_COUNT
         n_el = kernel_elements(H, w, dom)
-        rate = winst * 64 / (dom_avg_ms * 1e-3)
-        roof["valu"] = {"wave_instructions": int(winst),
+        roof["valu"] = {"wave_instructions": int(winst), "cycles": int(cycles),
                         "lane_instructions_per_element": round(winst * 64 / max(1, n_el), 1),
-                        "achieved_lane_instr_per_s": float("%.4g" % rate),
-                        "issue_peak": float("%.4g" % VALU_ISSUE_PEAK), "frac": round(rate / VALU_ISSUE_PEAK, 4)}
+                        "issue_limit_wave_instructions": int(simds * cycles / 4),
+                        "frac": round(winst / (simds * cycles / 4), 4),
+                        "clock_ghz_implied": round(cycles / (dom_avg_ms * 1e-3) / 1e9, 3),
+                        "how": "SQ_INSTS_VALU / (SIMDs x GRBM_GUI_ACTIVE/8 / 4), one rocprofv3 pass"}
         if args.config in ("poly", "poly64"):
             from cudacaml_amd.examples import refbench as RB
 
             roof["valu"]["achieved_tflops"] = round(RB.N * RB.poly_flops() / (dom_avg_ms * 1e-3) / 1e12, 2)
+    if args.config in MFMA_CONFIGS and "SQ_VALU_MFMA_BUSY_CYCLES" in dc and dc.get("GRBM_GUI_ACTIVE"):
+        # Matrix cores: busy cycles per SIMD over the dispatch's cycles
+        # (rocprofv3's MfmaUtil), and the math operations the matrix cores
+        # counted (512 flops per MOPS unit) per clock against the peak per
+        # clock, both from one pass.
+        cycles = dc["GRBM_GUI_ACTIVE"] / XCC_COUNT
+        mops = dc.get("SQ_INSTS_VALU_MFMA_MOPS_F32", 0.0) + dc.get("SQ_INSTS_VALU_MFMA_MOPS_F64", 0.0)
+        cflops = mops * 512
+        peak_tf = roof["peak"]
+        roof["mfma"] = {"busy_frac": round(dc["SQ_VALU_MFMA_BUSY_CYCLES"] / (simds * cycles), 4),
+                        "counter_flops": int(cflops), "cycles": int(cycles),
+                        "counter_flops_vs_2mnk": round(cflops / roof["flops_per_launch"], 4),
+                        "frac_per_clock": round(cflops / cycles / (peak_tf * 1e12 / MFMA_CLOCK_HZ), 4),
+                        "clock_ghz_implied": round(cycles / (dom_avg_ms * 1e-3) / 1e9, 3),
+                        "how": "busy = SQ_VALU_MFMA_BUSY_CYCLES / (SIMDs x GRBM_GUI_ACTIVE/8); flops = 512 x "
+                               "SQ_INSTS_VALU_MFMA_MOPS_F32/F64; frac_per_clock against peak / 2.4 GHz; one pass"}
     roof["kernel"] = dom
     roof["template"] = dom_role
     roof["algorithmic_bytes"] = dom_bytes
@@ -592,10 +692,11 @@ def main():
                  "what": "host arrays in, host arrays out: upload + kernels + download, pageable memory"}
 
     cpu = None
-    if not args.no_cpu and args.config in ("rows", "poly", "poly64"):
-        v, unit, sample, secs = cpu_baseline(args.config, C, H)
-        cpu = {"value": round(v, 3), "unit": unit, "cores": 1, "kind": "port",
-               "sample": sample + " (%.1fs, C restatement of the OCaml interpreter, one thread)" % secs}
+    if not args.no_cpu:
+        v, unit, sample, secs = cpu_baseline(args.config, C, H, w)
+        cpu = {"value": float("%.4g" % v), "unit": unit, "cores": 1, "kind": "port",
+               "sample": sample + " (%.1fs, C restatement of the OCaml interpreter, one thread)" % secs,
+               "host_cpu": host_cpu()}
 
     line = {
         "metric": "HBM GB/s & % peak (fused map/reduce/scan); matmul TFLOP/s; MC paths/s",
