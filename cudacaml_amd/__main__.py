@@ -8,8 +8,9 @@
     python -m cudacaml_amd info             the device description
 
 The reference's ``check`` compares against Backend_interp. Here that
-interpreter is test infrastructure, so the same check is the parity suite:
-``python -m pytest tests/test_gpu_parity.py -k <example>``.
+interpreter is test infrastructure, which the product never loads, so the
+same command lives with the tests: ``python tests/check.py <example>``
+(or ``all``), with the reference's output and exit codes.
 """
 
 import sys
@@ -80,7 +81,7 @@ def main(argv):
             c.release()
     elif cmd == "check":
         print("check compares with the reference interpreter, which is test infrastructure here; run:\n"
-              "  python -m pytest tests/test_gpu_parity.py -k %s" % name, file=sys.stderr)
+              "  python tests/check.py %s" % name, file=sys.stderr)
         return 2
     else:
         return _usage()
