@@ -926,6 +926,33 @@ struct Lowering {
   Gen gen;
   bool need_err = false;
 
+  // One partition pass of the LDS scatter: per-chunk bucket offsets
+  // (`cnt`), bucket starts (`start`), the pairs grouped by bucket (`key`,
+  // `val`), and, kept for a gather back, each element's slot within its
+  // tile (`slot`) and per tile its runs' starts (`meta`).
+  struct PassOut {
+    int cnt = -1, start = -1, key = -1, val = -1, slot = -1, meta = -1, nbuf = -1;
+    int64_t G = 0, C = 0, TILE = 0, TPC = 0, PB = 0;
+    std::string nvalid;
+    bool first = false;
+    // per tile: K, the K + 1 tile-local starts of its non-empty buckets
+    // (the last is the tile's total), their K run starts in the pair arrays
+    int64_t kmax() const { return std::min(TILE, PB); }
+    int64_t meta_stride() const { return 2 * kmax() + 2; }
+  };
+  // A scatter_add whose partition a later gather(idx, h) root reads back
+  // through: scatter tensor -> gather root (found before lowering), and the
+  // scatter's passes once it has been lowered that way.
+  struct GatherBack {
+    PassOut fin, coarse;
+    int64_t S = 0, P = 0, B = 0, N = 0;
+    int h = -1;
+  };
+  std::map<int, int> gbp_root_of;
+  std::map<int, GatherBack> gather_back;
+  // scratch buffers freed after a later root than the one that made them
+  std::map<int, int> free_after;
+
   explicit Lowering(const Graph &gr) : g(gr), plan(fusion_plan(gr)), gen(gr, plan, buf_of) {
     gen.bufdt_ = [this](int b) { return prog.bufs[b].dt; };
   }
@@ -1163,7 +1190,7 @@ struct Lowering {
     }
     static const char *helpers[] = {"scan_init",          "scatter_zero",   "scatter_count",  "scatter_colscan",
                                     "scatter_bscan",      "scatter_accumulate", "scatter_reduce", "matmul_ksum",
-                                    "reduce_split_fold",  "scatter_coarse"};
+                                    "reduce_split_fold",  "scatter_coarse",     "gather_slices"};
     int main = ks.back();
     for (int k : ks) {
       bool helper = false;
@@ -2189,7 +2216,16 @@ struct Lowering {
     while (W > 1 && W * P * S * ES > (int64_t(256) << 20)) W--;
     int part = finish(W, P, P * S);
     std::string sB = std::to_string(B);
-    const int64_t TILE = 4096, E = TILE / 256;
+    // Partition tile, per pass: 8192 elements where a pass has at most 1024
+    // buckets (runs twice as long per bucket as with 4096, at half the
+    // occupancy: config 3's partition 323 -> 278 us, config 3b's coarse
+    // pass 302 -> 269 us), 4096 above (config 3b's fine pass: 339 against
+    // 409 us); scatter_tile forces one size.
+    auto tile_of = [&](int64_t PB) -> int64_t {
+      const int64_t t = tune("scatter_tile", 0);
+      if (t == 4096 || t == 8192) return t;
+      return PB <= 1024 ? 8192 : 4096;
+    };
 
     // One partition pass: elements [0, nvalid) of an input stream are
     // grouped by bucket (j >> SH, PB buckets) into key/val arrays in bucket
@@ -2199,22 +2235,37 @@ struct Lowering {
       Params p;
       std::function<std::string(const std::string &)> jx, xx;
       std::string nvalid;
+      int nbuf = -1;  // buffer `nvalid` reads, if any
       bool check;
     };
-    struct PassOut {
-      int cnt, start, key, val;
-    };
     auto pass = [&](const std::string &sfx, const PassIn &in, int SH, int64_t PB, bool staged, bool final_keys,
-                    const std::string &part_role) {
+                    const std::string &part_role, bool keep) {
+      const int64_t TILE = tile_of(PB), E = TILE / 256;
       int64_t G = std::max<int64_t>(1, std::min<int64_t>(tune("scatter_chunks", 1024), cdiv(N, 4096)));
       int64_t C = cdiv(cdiv(N, G), 256) * 256;
       G = cdiv(N, C);
       PassOut o;
+      o.G = G;
+      o.C = C;
+      o.TILE = TILE;
+      o.TPC = cdiv(C, TILE);
+      o.PB = PB;
+      o.nvalid = in.nvalid;
+      o.nbuf = in.nbuf;
+      o.first = in.check;
       o.cnt = add_buf("t" + id + "_cnt" + sfx, DT::I32, G * PB, BufRole::Scratch);
       o.start = add_buf("t" + id + "_start" + sfx, DT::I32, PB + 1, BufRole::Scratch);
       o.key = final_keys ? add_buf("t" + id + "_key" + sfx, DT::I32, cdiv(N, 2), BufRole::Scratch)  // 16-bit keys
                          : add_buf("t" + id + "_key" + sfx, DT::I32, N, BufRole::Scratch);
       o.val = add_buf("t" + id + "_val" + sfx, n.dt, N, BufRole::Scratch);
+      if (keep) {
+        // for a gather back through this partition: each element's slot in
+        // its tile's bucket-grouped order (16 bits, 0xffff where the element
+        // was skipped), and per tile the bucket runs' starts in the pair
+        // arrays and within the tile
+        o.slot = add_buf("t" + id + "_slot" + sfx, DT::I32, cdiv(N, 2), BufRole::Scratch);
+        o.meta = add_buf("t" + id + "_tiles" + sfx, DT::I32, G * o.TPC * o.meta_stride(), BufRole::Scratch);
+      }
       const std::string sh = std::to_string(SH), spb = std::to_string(PB);
       auto bounds = [&](const std::string &v) { return in.check ? "(unsigned)" + v + " < " + sB + "u" : std::string("true"); };
       auto chunk_head = [&]() {
@@ -2251,26 +2302,34 @@ struct Lowering {
       };
       std::string key_decl = final_keys ? "  unsigned short* const keys = (unsigned short*)b" + std::to_string(o.key) + ";\n"
                                         : "  int* const keys = b" + std::to_string(o.key) + ";\n";
-      {  // count
+      {  // count: each wave into its own copy of the bucket counters (fewer
+         // same-address LDS atomics), the copies summed at the end
+        int64_t NC = std::max<int64_t>(1, std::min<int64_t>(tune("scatter_count_copies", 4), 4));
+        while (NC > 1 && NC * PB * 4 > 32768) NC /= 2;
         Params p = in.p;
         p.out.push_back(o.cnt);
         std::vector<int> args;
         std::string params = param_list(p, args);
         std::ostringstream k;
         k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_count" << sfx << "(" << params << ") {\n"
-          << "  __shared__ int lc[" << PB << "];\n"
-          << "  for (int q = threadIdx.x; q < " << PB << "; q += 256) lc[q] = 0;\n"
+          << "  __shared__ int lc[" << NC * PB << "];\n"
+          << "  for (int q = threadIdx.x; q < " << NC * PB << "; q += 256) lc[q] = 0;\n"
           << "  __syncthreads();\n"
+          << "  int* const mine = lc + (int)(threadIdx.x >> 6) % " << NC << " * " << PB << ";\n"
           << chunk_head()
-          << loop8(false, "      if (in && " + bounds("j") + ") cc_lds_add(&lc[j >> " + sh + "], 1);\n")
+          << loop8(false, "      if (in && " + bounds("j") + ") cc_lds_add(&mine[j >> " + sh + "], 1);\n")
           << "  __syncthreads();\n"
-          << "  for (int q = threadIdx.x; q < " << PB << "; q += 256) b" << o.cnt << "[(size_t)blockIdx.x * " << PB
-          << " + q] = lc[q];\n"
+          << "  for (int q = threadIdx.x; q < " << PB << "; q += 256) {\n"
+          << "    int c = lc[q];\n"
+          << "    for (int w = 1; w < " << NC << "; w++) c += lc[w * " << PB << " + q];\n"
+          << "    b" << o.cnt << "[(size_t)blockIdx.x * " << PB << " + q] = c;\n"
+          << "  }\n"
           << "}\n";
         src << k.str();
         ks.push_back(add_kernel(kname + "_count" + sfx, args, (int)G, 256, "scatter_count"));
       }
-      {  // colscan: per bucket, running offsets over the chunks
+      if (PB >= 1024) {  // colscan, many buckets: a thread per bucket walks
+                         // the chunks (loads coalesced across threads)
         std::ostringstream k;
         k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_colscan" << sfx << "(int* __restrict__ b"
           << o.cnt << ", int* __restrict__ b" << o.start << ") {\n"
@@ -2286,6 +2345,32 @@ struct Lowering {
           << "}\n";
         src << k.str();
         ks.push_back(add_kernel(kname + "_colscan" + sfx, {o.cnt, o.start}, (int)cdiv(PB, 256), 256, "scatter_colscan"));
+      } else {  // colscan, few buckets: one workgroup per bucket turns its
+                // column of chunk counts into running offsets (each thread a
+                // contiguous run of chunks, then a workgroup scan); start[q]
+                // gets the bucket's total
+        const int64_t per = cdiv(G, 256);
+        std::ostringstream k;
+        k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_colscan" << sfx << "(int* __restrict__ b"
+          << o.cnt << ", int* __restrict__ b" << o.start << ") {\n"
+          << "  __shared__ int ws[4];\n"
+          << "  const int q = blockIdx.x;\n"
+          << "  const int c0 = threadIdx.x * " << per << ";\n"
+          << "  int v[" << per << "], s = 0;\n"
+          << "#pragma unroll\n"
+          << "  for (int u = 0; u < " << per << "; u++) {\n"
+          << "    v[u] = c0 + u < " << G << " ? b" << o.cnt << "[(size_t)(c0 + u) * " << PB << " + q] : 0;\n"
+          << "    s += v[u];\n"
+          << "  }\n"
+          << "  int tot;\n"
+          << "  int run = cc_wg_exscan(s, ws, &tot);\n"
+          << "#pragma unroll\n"
+          << "  for (int u = 0; u < " << per << "; u++)\n"
+          << "    if (c0 + u < " << G << ") { b" << o.cnt << "[(size_t)(c0 + u) * " << PB << " + q] = run; run += v[u]; }\n"
+          << "  if (threadIdx.x == 0) b" << o.start << "[q] = tot;\n"
+          << "}\n";
+        src << k.str();
+        ks.push_back(add_kernel(kname + "_colscan" + sfx, {o.cnt, o.start}, (int)PB, 256, "scatter_colscan"));
       }
       {  // bscan: one workgroup, exclusive prefix of the bucket totals
         int64_t per = cdiv(PB, 256);
@@ -2316,6 +2401,10 @@ struct Lowering {
       for (int b : {o.cnt, o.start}) p.in.push_back(b);
       p.out.push_back(o.key);
       p.out.push_back(o.val);
+      if (keep && staged) {
+        p.out.push_back(o.slot);
+        p.out.push_back(o.meta);
+      }
       if (in.check) p.err = true;
       std::vector<int> args;
       std::string params = param_list(p, args);
@@ -2323,8 +2412,8 @@ struct Lowering {
       k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_partition" << sfx << "(" << params
         << ") {\n";
       if (staged) {
-        // each 4096-element tile is grouped by bucket in LDS, then written
-        // as contiguous runs
+        // each tile is grouped by bucket in LDS, then written as contiguous
+        // runs
         int64_t PP = cdiv(PB, 256);
         k << "  __shared__ int cur[" << PB << "];\n"
           << "  __shared__ int tc[" << PB + 1 << "];\n"
@@ -2372,25 +2461,77 @@ struct Lowering {
           << "      else { " << (in.check ? "cc_flag(err, 2); " : "") << "jj[u] = -1; }\n"
           << "    }\n"
           << "    __syncthreads();\n"
-          << "    {\n"
-          << "      int loc[" << PP << "], s = 0;\n"
-          << "#pragma unroll\n"
-          << "      for (int c = 0; c < " << PP << "; c++) {\n"
-          << "        const int q = threadIdx.x * " << PP << " + c;\n"
-          << "        loc[c] = s;\n"
-          << "        s += q < " << PB << " ? tc[q] : 0;\n"
-          << "      }\n"
-          << "      int tot;\n"
-          << "      const int base = cc_wg_exscan(s, ws, &tot);\n"
-          << "#pragma unroll\n"
-          << "      for (int c = 0; c < " << PP << "; c++) {\n"
-          << "        const int q = threadIdx.x * " << PP << " + c;\n"
-          << "        if (q < " << PB << ") tc[q] = base + loc[c];\n"
-          << "      }\n"
-          << "      if (threadIdx.x == 0) tc[" << PB << "] = tot;\n"
-          << "    }\n"
-          << "    __syncthreads();\n"
-          << "#pragma unroll\n"
+          << "    {\n";
+        if (!keep)
+          k << "      int loc[" << PP << "], s = 0;\n"
+            << "#pragma unroll\n"
+            << "      for (int c = 0; c < " << PP << "; c++) {\n"
+            << "        const int q = threadIdx.x * " << PP << " + c;\n"
+            << "        loc[c] = s;\n"
+            << "        s += q < " << PB << " ? tc[q] : 0;\n"
+            << "      }\n"
+            << "      int tot;\n"
+            << "      const int base = cc_wg_exscan(s, ws, &tot);\n"
+            << "#pragma unroll\n"
+            << "      for (int c = 0; c < " << PP << "; c++) {\n"
+            << "        const int q = threadIdx.x * " << PP << " + c;\n"
+            << "        if (q < " << PB << ") tc[q] = base + loc[c];\n"
+            << "      }\n"
+            << "      if (threadIdx.x == 0) tc[" << PB << "] = tot;\n";
+        else
+          // The same scan also numbers the tile's non-empty buckets: the low
+          // 16 bits carry the counts (a tile holds at most 8192 elements),
+          // the high bits one per non-empty bucket (at most 4096). The
+          // tile's record for the gather back: its number of non-empty
+          // buckets K, their K tile-local starts and the tile's total, their
+          // K run starts in the pair arrays.
+          k << "      int loc[" << PP << "], cn[" << PP << "], s = 0;\n"
+            << "#pragma unroll\n"
+            << "      for (int c = 0; c < " << PP << "; c++) {\n"
+            << "        const int q = threadIdx.x * " << PP << " + c;\n"
+            << "        loc[c] = s;\n"
+            << "        cn[c] = q < " << PB << " ? tc[q] : 0;\n"
+            << "        s += cn[c] + (cn[c] > 0 ? 0x10000 : 0);\n"
+            << "      }\n"
+            << "      int tot;\n"
+            << "      const int base = cc_wg_exscan(s, ws, &tot);\n"
+            << "      const size_t mt = ((size_t)blockIdx.x * " << o.TPC << " + (t0 - lo) / " << TILE << ") * "
+            << o.meta_stride() << ";\n"
+            << "#pragma unroll\n"
+            << "      for (int c = 0; c < " << PP << "; c++) {\n"
+            << "        const int q = threadIdx.x * " << PP << " + c;\n"
+            << "        const int pk = base + loc[c];\n"
+            << "        if (q < " << PB << ") tc[q] = pk & 0xffff;\n"
+            << "        if (cn[c] > 0) {\n"
+            << "          b" << o.meta << "[mt + 1 + (pk >> 16)] = pk & 0xffff;\n"
+            << "          b" << o.meta << "[mt + " << o.kmax() + 2 << " + (pk >> 16)] = cur[q];\n"
+            << "        }\n"
+            << "      }\n"
+            << "      if (threadIdx.x == 0) {\n"
+            << "        tc[" << PB << "] = tot & 0xffff;\n"
+            << "        b" << o.meta << "[mt] = tot >> 16;\n"
+            << "        b" << o.meta << "[mt + 1 + (tot >> 16)] = tot & 0xffff;\n"
+            << "      }\n";
+        k << "    }\n"
+          << "    __syncthreads();\n";
+        if (keep)
+          k << "    {\n"
+            << "      unsigned short* const slots = (unsigned short*)b" << o.slot << ";\n"
+
+            // two slots per 32-bit store: even lanes (even i, t0 being a
+            // multiple of 256) take their odd neighbour's slot
+            << "#pragma unroll\n"
+            << "      for (int u = 0; u < " << E << "; u++) {\n"
+            << "        const int i = t0 + u * 256 + (int)threadIdx.x;\n"
+            << "        const unsigned v = jj[u] >= 0 ? (unsigned)(tc[jj[u] >> " << sh << "] + rk[u]) : 0xffffu;\n"
+            << "        const unsigned w = __shfl_down(v, 1);\n"
+            << "        if ((threadIdx.x & 1) == 0 && i < hi) {\n"
+            << "          if (i + 1 < hi) *(unsigned*)(slots + i) = v | (w << 16);\n"
+            << "          else slots[i] = (unsigned short)v;\n"
+            << "        }\n"
+            << "      }\n"
+            << "    }\n";
+        k << "#pragma unroll\n"
           << "    for (int u = 0; u < " << E << "; u++)\n"
           << "      if (jj[u] >= 0) {\n"
           << "        const int slot = tc[jj[u] >> " << sh << "] + rk[u];\n"
@@ -2434,24 +2575,41 @@ struct Lowering {
     first.nvalid = std::to_string(N);
     first.check = true;
     const int64_t STAGE_P = tune("scatter_stage_p", 512);
-    PassOut fin;
+    // A gather back through this scatter's partition (a later root
+    // gather(idx, h) over the same index) keeps the staged passes' slots.
+    const bool keep = gbp_root_of.count(t) > 0;
+    PassOut fin, coarse;
     if (P <= STAGE_P) {
-      fin = pass("", first, shift, P, true, true, "scatter_partition");
+      fin = pass("", first, shift, P, true, true, "scatter_partition", keep);
     } else if (!tune("scatter_two_level", 1)) {
-      fin = pass("", first, shift, P, false, true, "scatter_partition");  // single level, element-wise stores
+      // single level, element-wise stores
+      fin = pass("", first, shift, P, false, true, "scatter_partition", false);
     } else {
       // Two levels: a coarse pass into super-slices of 64 slices (runs of
       // about 64 elements per tile), then the slice pass over the coarse
       // output, whose tiles each touch at most two super-slices.
       const int64_t P1 = cdiv(P, 64);
-      PassOut c1 = pass("1", first, shift + 6, P1, true, false, "scatter_coarse");
+      PassOut c1 = pass("1", first, shift + 6, P1, true, false, "scatter_coarse", keep);
+      coarse = c1;
       PassIn second;
       for (int b : {c1.key, c1.val, c1.start}) second.p.in.push_back(b);
       second.jx = [&, c1](const std::string &i) { return "b" + std::to_string(c1.key) + "[" + i + "]"; };
       second.xx = [&, c1](const std::string &i) { return "b" + std::to_string(c1.val) + "[" + i + "]"; };
       second.nvalid = "b" + std::to_string(c1.start) + "[" + std::to_string(P1) + "]";
+      second.nbuf = c1.start;
       second.check = false;
-      fin = pass("", second, shift, P, true, true, "scatter_partition");
+      fin = pass("", second, shift, P, true, true, "scatter_partition", keep);
+    }
+    if (keep && fin.slot >= 0) {
+      GatherBack gb;
+      gb.fin = fin;
+      gb.coarse = coarse;
+      gb.S = S;
+      gb.P = P;
+      gb.B = B;
+      gb.N = N;
+      gb.h = out;
+      gather_back[t] = gb;
     }
     const int start = fin.start, key = fin.key, val = fin.val;
     {  // accumulate
@@ -2585,6 +2743,206 @@ struct Lowering {
     src << k.str();
     int64_t nvec = std::max<int64_t>(1, N / 4);
     ks.push_back(add_kernel(kname, args, (int)std::min<int64_t>(cdiv(nvec, 256), 65536), 256, "scatter_atomic"));
+    return ks;
+  }
+
+  // ---- Gather back through a scatter's partition ----------------------------
+  // back = gather(idx, h) with h = scatter_add(idx, src, bins) lowered through
+  // the LDS partition: the partition already grouped the index stream by
+  // table slice, so the gather reads the table slice by slice from LDS
+  // instead of making one random L2 request per element (config 3's
+  // 4 MiB-table gather sits at the L2 request ceiling; a 256 MiB table
+  // fetches one HBM line per element).
+  //   slices      each pair's value becomes h at its bin, from an LDS copy
+  //               of its slice (in place, in pair order; the pairs' values
+  //               are dead once accumulated)
+  //   unpartition per tile of a pass: the tile's runs staged through LDS in
+  //               its bucket-grouped order, then each element takes the
+  //               value at its recorded slot; two-level partitions are
+  //               undone level by level
+  // An element the scatter skipped (index out of range) has no slot: it
+  // gets zero and raises the gather's error, as the gather would.
+  std::vector<int> lower_gather_back(int r, const GatherBack &gb) {
+    const TNode &n = g.ts[r];
+    const std::string kname = "k_" + std::to_string(n.id);
+    const std::string T = dt_ctype(n.dt);
+    const int out = buf_of[r];
+    const PassOut &f = gb.fin;
+    std::vector<int> ks;
+    // 8 values of T through 16-byte accesses: two 4-wide vectors
+    const std::string v4 = "__attribute__((ext_vector_type(4))) " + T;
+    {
+      const int64_t S = gb.S, B = gb.B;
+      const int64_t Wg = std::max<int64_t>(1, std::min<int64_t>(16, 1024 / gb.P));
+      std::ostringstream k;
+      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_slices(const int* __restrict__ b"
+        << f.start << ", const int* __restrict__ b" << f.key << ", const " << T << "* __restrict__ b" << gb.h << ", "
+        << T << "* __restrict__ b" << f.val << ") {\n"
+        << "  typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));\n"
+        << "  typedef " << v4 << " v4;\n"
+        << "  __shared__ " << T << " tab[" << S << "];\n"
+        << "  const int q = blockIdx.x / " << Wg << ", w = blockIdx.x % " << Wg << ";\n"
+        << "  const int nb = " << B << " - q * " << S << " < " << S << " ? " << B << " - q * " << S << " : " << S
+        << ";\n"
+        << "  const " << T << "* const hq = b" << gb.h << " + (size_t)q * " << S << ";\n"
+        // the slice into LDS, eight loads in flight per thread
+        << "  for (int b0 = threadIdx.x; b0 < nb; b0 += 2048) {\n"
+        << "    " << T << " t[8];\n"
+        << "#pragma unroll\n"
+        << "    for (int u = 0; u < 8; u++) t[u] = hq[b0 + u * 256 < nb ? b0 + u * 256 : b0];\n"
+        << "#pragma unroll\n"
+        << "    for (int u = 0; u < 8; u++) if (b0 + u * 256 < nb) tab[b0 + u * 256] = t[u];\n"
+        << "  }\n"
+        << "  __syncthreads();\n"
+        << "  const int s0 = b" << f.start << "[q], len = b" << f.start << "[q + 1] - s0;\n"
+        << "  const int lo = s0 + (int)((long long)len * w / " << Wg << ");\n"
+        << "  const int hi = s0 + (int)((long long)len * (w + 1) / " << Wg << ");\n"
+        << "  const unsigned short* const keys = (const unsigned short*)b" << f.key << ";\n"
+        << "  " << T << "* const vals = b" << f.val << ";\n"
+        // 8-aligned body: 8 keys in one 16-byte load, 8 values in two
+        // 16-byte stores; the unaligned head and tail one by one
+        << "  const int up8 = (lo + 7) & ~7, dn8 = hi & ~7;\n"
+        << "  const int lo8 = up8 < hi ? up8 : hi;\n"
+        << "  const int hi8 = dn8 > lo8 ? dn8 : lo8;\n"
+        << "  for (int j = lo + (int)threadIdx.x; j < lo8; j += 256) vals[j] = tab[keys[j]];\n"
+        << "  for (int j = hi8 + (int)threadIdx.x; j < hi; j += 256) vals[j] = tab[keys[j]];\n"
+        << "  for (int j0 = lo8 + 8 * (int)threadIdx.x; j0 < hi8; j0 += 8192) {\n"
+        << "    u16x8 kv[4];\n"
+        << "#pragma unroll\n"
+        << "    for (int u = 0; u < 4; u++) kv[u] = *(const u16x8*)(keys + (j0 + u * 2048 < hi8 ? j0 + u * 2048 : j0));\n"
+        << "#pragma unroll\n"
+        << "    for (int u = 0; u < 4; u++)\n"
+        << "      if (j0 + u * 2048 < hi8) {\n"
+        << "        const v4 a = {tab[kv[u][0]], tab[kv[u][1]], tab[kv[u][2]], tab[kv[u][3]]};\n"
+        << "        const v4 c = {tab[kv[u][4]], tab[kv[u][5]], tab[kv[u][6]], tab[kv[u][7]]};\n"
+        << "        *(v4*)(vals + j0 + u * 2048) = a;\n"
+        << "        *(v4*)(vals + j0 + u * 2048 + 4) = c;\n"
+        << "      }\n"
+        << "  }\n"
+        << "}\n";
+      src << k.str();
+      ks.push_back(add_kernel(kname + "_slices", {f.start, f.key, gb.h, f.val}, (int)(gb.P * Wg), 256,
+                              "gather_slices"));
+    }
+    auto unpartition = [&](const std::string &sfx, const PassOut &o, int from, int to, bool flag) {
+      std::vector<int> args = {o.meta, o.slot, from, to};
+      std::ostringstream k;
+      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_unpartition" << sfx
+        << "(const int* __restrict__ b" << o.meta << ", const int* __restrict__ b" << o.slot << ", const " << T
+        << "* __restrict__ b" << from << ", " << T << "* __restrict__ b" << to;
+      if (o.nbuf >= 0) {
+        k << ", const int* __restrict__ b" << o.nbuf;
+        args.push_back(o.nbuf);
+      }
+      if (flag) {
+        k << ", int* __restrict__ err";
+        args.push_back(err_buf());
+      }
+      const int64_t KM = o.kmax();
+      const int64_t E = o.TILE / 256, VB = o.TILE / 2048;  // slots, 8-element groups per thread
+      const std::string zero = zero_of(n.dt);
+      k << ") {\n"
+        << "  typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));\n"
+        << "  typedef " << v4 << " v4;\n"
+        << "  __shared__ int mt[" << KM + 1 << "];\n"
+        << "  __shared__ int mc[" << KM << "];\n"
+        << "  __shared__ " << T << " st[" << o.TILE << "];\n"
+        << "  const int g = blockIdx.x / " << o.TPC << ", kt = blockIdx.x - g * " << o.TPC << ";\n"
+        << "  const int nv_ = " << o.nvalid << ";\n"
+        << "  const int lo = g * " << o.C << ";\n"
+        << "  const int hc = lo + " << o.C << " < nv_ ? lo + " << o.C << " : nv_;\n"
+        << "  const int t0 = lo + kt * " << o.TILE << ";\n"
+        << "  if (t0 >= hc) return;  // a tile the partition never had: the whole workgroup leaves\n"
+        << "  const int hi = t0 + " << o.TILE << " < hc ? t0 + " << o.TILE << " : hc;\n"
+        << "  const int* const meta = b" << o.meta << " + (size_t)blockIdx.x * " << o.meta_stride() << ";\n"
+        << "  const unsigned short* const sl = (const unsigned short*)b" << o.slot << ";\n"
+        << "  " << T << "* const dst = b" << to << ";\n"
+        // this thread's element slots, 8 per group in one 16-byte load (t0 is
+        // a multiple of 256), requested before anything else; a group that
+        // runs past hi is read one by one later
+        << "  u16x8 sv[" << VB << "];\n"
+        << "#pragma unroll\n"
+        << "  for (int u = 0; u < " << VB << "; u++) {\n"
+        << "    const int i = t0 + 8 * ((int)threadIdx.x + 256 * u);\n"
+        << "    if (i + 8 <= hi) sv[u] = *(const u16x8*)(sl + i);\n"
+        << "    else sv[u] = (u16x8)(unsigned short)0xffffu;\n"
+        << "  }\n"
+        << "  const int nk = meta[0];\n"
+        << "  for (int c = threadIdx.x; c <= nk; c += 256) mt[c] = meta[1 + c];\n"
+        << "  for (int c = threadIdx.x; c < nk; c += 256) mc[c] = meta[" << KM + 2 << " + c];\n"
+        << "  __syncthreads();\n"
+        << "  const int tot = mt[nk];\n"
+        // the tile's runs into LDS in its bucket-grouped order: slot s lies in
+        // the last non-empty bucket whose tile-local start is <= s; all of a
+        // thread's slots searched, then all their loads issued together
+        << "  if (tot > 0) {\n"
+        // Each wave takes a contiguous quarter of the slots, 64 at a time;
+        // a lane's bucket is the last one starting at or before its slot:
+        // one search for the wave's first slot (the same for every lane),
+        // then each lane probes forward from where lane 63 stopped the
+        // previous time (runs are about as long as a wave, so one or two
+        // probes). All addresses first, then all loads together.
+        << "    const int lane = threadIdx.x & 63;\n"
+        << "    const int sw = (int)(threadIdx.x >> 6) * " << E * 64 << ";\n"
+        << "    int aw = 0;\n"
+        << "    for (int step = nk > 1 ? 1 << (31 - __clz(nk - 1)) : 0; step >= 1; step >>= 1) {\n"
+        << "      const int m = aw + step;\n"
+        << "      if (m < nk && mt[m] <= sw) aw = m;\n"
+        << "    }\n"
+        << "    int at[" << E << "];\n"
+        << "#pragma unroll\n"
+        << "    for (int u = 0; u < " << E << "; u++) {\n"
+        << "      const int s = sw + u * 64 + lane;\n"
+        << "      int a = aw;\n"
+        << "      while (a + 1 < nk && mt[a + 1] <= s) a++;\n"
+        << "      at[u] = s < tot ? mc[a] + (s - mt[a]) : mc[0];\n"
+        << "      aw = __shfl(a, 63);\n"
+        << "    }\n"
+        << "    " << T << " v[" << E << "];\n"
+        << "#pragma unroll\n"
+        << "    for (int u = 0; u < " << E << "; u++) v[u] = b" << from << "[at[u]];\n"
+        << "#pragma unroll\n"
+        << "    for (int u = 0; u < " << E << "; u++)\n"
+        << "      if (sw + u * 64 + lane < tot) st[sw + u * 64 + lane] = v[u];\n"
+        << "  }\n"
+        << "  __syncthreads();\n"
+        << "  bool bad = false;\n"
+        << "#pragma unroll\n"
+        << "  for (int u = 0; u < " << VB << "; u++) {\n"
+        << "    const int i = t0 + 8 * ((int)threadIdx.x + 256 * u);\n"
+        << "    if (i + 8 <= hi) {\n"
+        << "      " << T << " x[8];\n"
+        << "#pragma unroll\n"
+        << "      for (int e = 0; e < 8; e++) {\n"
+        << "        const unsigned v = sv[u][e];\n"
+        << "        x[e] = v != 0xffffu ? st[v] : " << zero << ";\n"
+        << "        bad = bad || v == 0xffffu;\n"
+        << "      }\n"
+        << "      const v4 a = {x[0], x[1], x[2], x[3]}, c = {x[4], x[5], x[6], x[7]};\n"
+        << "      *(v4*)(dst + i) = a;\n"
+        << "      *(v4*)(dst + i + 4) = c;\n"
+        << "    } else {\n"
+        << "      for (int e = i; e < hi; e++) {\n"
+        << "        const unsigned v = sl[e];\n"
+        << "        dst[e] = v != 0xffffu ? st[v] : " << zero << ";\n"
+        << "        bad = bad || v == 0xffffu;\n"
+        << "      }\n"
+        << "    }\n"
+        << "  }\n";
+      if (flag) k << "  if (bad) cc_flag(err, 1);\n";
+      k << "}\n";
+      src << k.str();
+      ks.push_back(add_kernel(kname + "_unpartition" + sfx, args, (int)(o.G * o.TPC), 256, "gather_unpartition"));
+    };
+    if (gb.coarse.slot >= 0) {
+      unpartition("2", f, f.val, gb.coarse.val, false);
+      unpartition("", gb.coarse, gb.coarse.val, out, true);
+    } else {
+      unpartition("", f, f.val, out, true);
+    }
+    for (const PassOut *o : {&gb.fin, &gb.coarse})
+      for (int b : {o->start, o->key, o->val, o->slot, o->meta, o->nbuf})
+        if (b >= 0) free_after[b] = r;
     return ks;
   }
 
@@ -2997,16 +3355,32 @@ struct Lowering {
         buf_of[i] = add_buf("t" + std::to_string(g.ts[i].id), g.ts[i].dt, g.ts[i].numel, BufRole::Computed);
     int ncomputed = (int)prog.bufs.size();
     src << kPrelude;
+    // Roots gather(idx, h) over h = scatter_add(idx, ...) with the very same
+    // index tensor read back through the scatter's partition
+    // (scatter_gather_back=0 keeps them plain gathers).
+    if (tune("scatter_gather_back", 1))
+      for (int r : plan.roots) {
+        const TNode &n = g.ts[r];
+        if (n.kind != TK::Gather) continue;
+        const int S = n.b;
+        if (g.ts[S].kind == TK::Scatter && g.ts[S].a == n.a && !gbp_root_of.count(S)) gbp_root_of[S] = r;
+      }
     std::vector<std::vector<int>> launches;
     std::vector<std::vector<int>> scratch_of;
     for (int r : plan.roots) {
       size_t before = prog.bufs.size();
       std::vector<int> ks;
       switch (g.ts[r].kind) {
+        case TK::Gather: {
+          auto it = gather_back.find(g.ts[r].b);
+          auto ro = gbp_root_of.find(g.ts[r].b);
+          ks = it != gather_back.end() && ro != gbp_root_of.end() && ro->second == r ? lower_gather_back(r, it->second)
+                                                                                    : lower_map(r);
+          break;
+        }
         case TK::Map:
         case TK::Map2:
         case TK::Iota:
-        case TK::Gather:
         case TK::Reshape:
         case TK::Broadcast: ks = lower_map(r); break;
         case TK::Reduce: ks = lower_reduce(r); break;
@@ -3033,7 +3407,10 @@ struct Lowering {
     for (size_t r = 0; r < launches.size(); r++) {
       for (int b : scratch_of[r]) prog.plan.push_back({OpK::Alloc, b, -1, ""});
       for (int k : launches[r]) prog.plan.push_back({OpK::Launch, -1, k, ""});
-      for (int b : scratch_of[r]) prog.plan.push_back({OpK::Free, b, -1, ""});
+      for (int b : scratch_of[r])
+        if (!free_after.count(b)) prog.plan.push_back({OpK::Free, b, -1, ""});
+      for (auto &fa : free_after)
+        if (fa.second == plan.roots[r]) prog.plan.push_back({OpK::Free, fa.first, -1, ""});
     }
     for (auto &o : prog.outputs) prog.plan.push_back({OpK::Download, o.buf, -1, o.name});
     for (int b = 0; b < ncomputed; b++) prog.plan.push_back({OpK::Free, b, -1, ""});

@@ -216,6 +216,76 @@ def test_scatter_permutation_two_level(device, dtype, tune, monkeypatch):
     check(g, [("idx", idx), ("src", data(dtype, (n,), 32))], ["scatter_partition", "scatter_accumulate"])
 
 
+GATHER_BACK_CASES = [
+    # (n, bins, dtype, two levels)
+    ((1 << 20) + 37, 1 << 16, F32, False),
+    (300001, 100003, I32, False),
+    ((1 << 19) + 5, 1 << 17, F64, False),
+    ((1 << 22) + 3, 1 << 23, F32, True),
+    ((1 << 21) + 11, (1 << 22) + 1, I32, True),
+    ((1 << 20) + 1, 1 << 23, F64, True),
+]
+
+
+@pytest.mark.parametrize("n,bins,dtype,two", GATHER_BACK_CASES)
+def test_gather_back_through_the_partition(device, n, bins, dtype, two, monkeypatch):
+    """gather(idx, h) over h = scatter_add(idx, src, bins) reads h back
+    through the scatter's partition (one level, or two above 512 slices):
+    back is exactly h[idx], bit for bit, on ragged sizes and every dtype; h
+    and back against the oracle under the policy; the same outputs as with
+    the plain gather (scatter_gather_back=0), integers bit for bit."""
+    g = C.scatter_gather(n, bins, dtype)
+    t = templates(g)
+    assert t[-3 if two else -2:] == ["gather_slices"] + ["gather_unpartition"] * (2 if two else 1)
+    assert ("scatter_coarse" in t) == two
+    if two:
+        idx = C.permutation(31, bins)[:n].astype(np.int32)
+        idx[::7] = idx[3]  # and one crowded bin
+    else:
+        idx = scatter_idx(7, n, bins)
+    inputs = [("idx", idx), ("src", data(dtype, (n,), 8))]
+    check(g, inputs, ["gather_unpartition"])
+    c = H.compile(g)
+    try:
+        o = dict(H.run(c, inputs))
+    finally:
+        c.release()
+    np.testing.assert_array_equal(o["back"], o["h"][idx])
+    monkeypatch.setenv("CCHIP_TUNE", "scatter_gather_back=0")
+    assert templates(g)[-1] == "map"
+    c = H.compile(g)
+    try:
+        plain = dict(H.run(c, inputs))
+    finally:
+        c.release()
+    np.testing.assert_array_equal(plain["back"], plain["h"][idx])
+    if dtype is I32:
+        np.testing.assert_array_equal(o["h"], plain["h"])
+        np.testing.assert_array_equal(o["back"], plain["back"])
+
+
+@pytest.mark.parametrize("two", [False, True])
+def test_gather_back_out_of_range_raises(device, two):
+    """An index out of range is skipped by the scatter's partition, so it
+    has no slot: the run raises the gather's error, and the next run with
+    good indices is clean."""
+    n, bins = (1 << 20) + 3, (1 << 22 if two else 1 << 16)
+    g = C.scatter_gather(n, bins, F32)
+    idx = scatter_idx(9, n, bins)
+    bad = idx.copy()
+    bad[n // 2] = bins + 5
+    bad[7] = -1
+    src = data(F32, (n,), 10)
+    c = H.compile(g)
+    try:
+        with pytest.raises(ValueError, match="gather index out of bounds"):
+            H.run(c, [("idx", bad), ("src", src)])
+        o = dict(H.run(c, [("idx", idx), ("src", src)]))
+        np.testing.assert_array_equal(o["back"], o["h"][idx])
+    finally:
+        c.release()
+
+
 @pytest.mark.parametrize("dtype", [F32, I32])
 def test_scatter_atomic_path(device, dtype, monkeypatch):
     """The global-atomic template, still used where the slices would not

@@ -127,11 +127,39 @@ def test_scan_template_choice(rows, n, tpls):
 
 def test_config_plans():
     assert [t for _, t in kernels_of(C.rows())] == ["reduce_rowseq", "reduce_rowseq", "scan_rowseq"]
+    # the gather back reads the scatter's partition: the table slice by
+    # slice from LDS, then each tile's values back in element order
     assert [t for _, t in kernels_of(C.scatter_gather())] == ["scatter_count", "scatter_colscan", "scatter_bscan",
                                                                "scatter_partition", "scatter_accumulate",
-                                                               "scatter_reduce", "map"]
-    # 2^26 bins: one workgroup per slice stores its table, no partials
-    assert "scatter_reduce" not in [t for _, t in kernels_of(C.scatter_gather(C.N3, C.N3))]
+                                                               "scatter_reduce", "gather_slices", "gather_unpartition"]
+    # 2^26 bins: one workgroup per slice stores its table, no partials; two
+    # partition levels, undone level by level
+    perm = [t for _, t in kernels_of(C.scatter_gather(C.N3, C.N3))]
+    assert "scatter_reduce" not in perm and perm[-3:] == ["gather_slices", "gather_unpartition", "gather_unpartition"]
+
+
+def test_gather_back_only_over_the_same_index(monkeypatch):
+    """A gather root reads back through the scatter's partition only when
+    its index is the scatter's own index tensor and the partition is staged;
+    scatter_gather_back=0 keeps the plain gather."""
+    n, bins = 1 << 20, 1 << 16
+    idx, idx2 = D.param("idx", I32, (n,)), D.param("idx2", I32, (n,))
+    src = D.param("src", F32, (n,))
+    h = D.scatter_add(idx, src, (bins,))
+    roles = lambda g: [t for _, t in kernels_of(g)]  # noqa: E731
+    assert roles(Graph.create("a", [("h", h), ("b", D.gather(idx, h))]))[-2:] == ["gather_slices", "gather_unpartition"]
+    assert roles(Graph.create("a", [("h", h), ("b", D.gather(idx2, h))]))[-1] == "map"
+    # one slice (no partition): the plain gather
+    small = D.scatter_add(idx, src, (4096,))
+    assert roles(Graph.create("a", [("h", small), ("b", D.gather(idx, small))]))[-1] == "map"
+    monkeypatch.setenv("CCHIP_TUNE", "scatter_gather_back=0")
+    assert roles(Graph.create("a", [("h", h), ("b", D.gather(idx, h))]))[-1] == "map"
+    # the partition's buffers live until the gather back has run
+    monkeypatch.delenv("CCHIP_TUNE")
+    plan = H.plan(Graph.create("a", [("h", h), ("b", D.gather(idx, h))])).splitlines()
+    last_launch = max(i for i, l in enumerate(plan) if l.startswith("launch"))
+    frees = [l.split()[1] for l in plan[last_launch:] if l.startswith("free")]
+    assert any(b.endswith("_slot") for b in frees) and any(b.endswith("_val") for b in frees)
     ks = kernels_of(C.mc_paths())
     assert "scan_rowseq" in [t for _, t in ks]
 
@@ -188,7 +216,8 @@ def test_algorithmic_bytes_per_kernel():
     b = _bytes(C.scatter_gather(n, 1 << 14))
     assert b["scatter_partition"] == 8 * n + 4 * (1 << 14)
     assert b["scatter_count"] == 0 and b["scatter_accumulate"] == 0
-    assert b["map"] == 4 * n + 4 * (1 << 14) + 4 * n  # idx, the table (once), out
+    # the gather back: idx, the table (once), out, on its last kernel
+    assert b["gather_unpartition"] == 4 * n + 4 * (1 << 14) + 4 * n and b["gather_slices"] == 0
     # the price reduces the gathered last column only, not the whole path matrix
     b = _bytes(C.mc_paths(4096, 64))
     assert b["reduce_split"] < 4 * 4096 + 64
