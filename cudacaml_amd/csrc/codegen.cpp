@@ -2139,8 +2139,10 @@ struct Lowering {
     int out = buf_of[t];
     int shift = 0;
     while ((int64_t(1) << shift) < S) shift++;
-    ElemFn fi = gen.element_fn("fi_" + id, n.a, false, false);
-    ElemFn fs = gen.element_fn("fs_" + id, n.b, false, false);
+    // inputs read at the element's own index come in by value, so whole
+    // 4-element groups can be loaded with 16-byte accesses
+    ElemFn fi = gen.element_fn("fi_" + id, n.a, false, true);
+    ElemFn fs = gen.element_fn("fs_" + id, n.b, false, true);
     src << fi.code << fs.code;
     std::string acc = n.dt == DT::I32 ? "cc_u32" : T;  // partial sums wrap for i32
     std::vector<int> ks;
@@ -2234,6 +2236,11 @@ struct Lowering {
     struct PassIn {
       Params p;
       std::function<std::string(const std::string &)> jx, xx;
+      // 4-element groups at a multiple of 4: the loads of a group at i (the
+      // indices only, or indices and values), then element k's index and
+      // value from them
+      std::function<std::string(const std::string &)> vload_j, vload_jx;
+      std::function<std::string(const std::string &, int)> jv, xv;
       std::string nvalid;
       int nbuf = -1;  // buffer `nvalid` reads, if any
       bool check;
@@ -2317,7 +2324,28 @@ struct Lowering {
           << "  __syncthreads();\n"
           << "  int* const mine = lc + (int)(threadIdx.x >> 6) % " << NC << " * " << PB << ";\n"
           << chunk_head()
-          << loop8(false, "      if (in && " + bounds("j") + ") cc_lds_add(&mine[j >> " + sh + "], 1);\n")
+          // 16 indices a thread per iteration in four 16-byte groups (lo is a
+          // multiple of 256), the chunk's last partial group one by one
+          << "  const int hi4 = lo + ((hi - lo) & ~3);\n"
+          << "  for (int g0 = lo + 4 * (int)threadIdx.x; g0 < hi4; g0 += 4096) {\n"
+          << "    int jj[16];\n"
+          << "#pragma unroll\n"
+          << "    for (int u = 0; u < 4; u++) {\n"
+          << "      const int i = g0 + u * 1024 < hi4 ? g0 + u * 1024 : g0;\n"
+          << "      " << in.vload_j("i") << "\n"
+          << "      jj[4 * u] = " << in.jv("i", 0) << "; jj[4 * u + 1] = " << in.jv("i", 1) << ";\n"
+          << "      jj[4 * u + 2] = " << in.jv("i", 2) << "; jj[4 * u + 3] = " << in.jv("i", 3) << ";\n"
+          << "    }\n"
+          << "#pragma unroll\n"
+          << "    for (int u = 0; u < 16; u++) {\n"
+          << "      const int j = jj[u];\n"
+          << "      if (g0 + (u >> 2) * 1024 < hi4 && " << bounds("j") << ") cc_lds_add(&mine[j >> " << sh << "], 1);\n"
+          << "    }\n"
+          << "  }\n"
+          << "  for (int i = hi4 + (int)threadIdx.x; i < hi; i += 256) {\n"
+          << "    const int j = " << in.jx("i") << ";\n"
+          << "    if (" << bounds("j") << ") cc_lds_add(&mine[j >> " << sh << "], 1);\n"
+          << "  }\n"
           << "  __syncthreads();\n"
           << "  for (int q = threadIdx.x; q < " << PB << "; q += 256) {\n"
           << "    int c = lc[q];\n"
@@ -2426,17 +2454,33 @@ struct Lowering {
         // The next tile's indices and values are loaded into a second set of
         // registers before this tile's LDS work starts (scatter_prefetch).
         const bool pf = tune("scatter_prefetch", 1) != 0;
+        // A thread's E elements of a tile: E/4 groups of 4 consecutive
+        // elements, group v at t + 1024 v + 4 threadIdx.x (a multiple of 4:
+        // tiles start at multiples of 256), each loaded with 16-byte
+        // accesses; a group that runs past hi one by one, clamped.
         auto tile_load = [&](const std::string &t, const std::string &jv, const std::string &xvv) {
           std::ostringstream l;
           l << "#pragma unroll\n"
-            << "    for (int u = 0; u < " << E << "; u++) {\n"
-            << "      const int i = " << t << " + u * 256 + (int)threadIdx.x < hi ? " << t
-            << " + u * 256 + (int)threadIdx.x : lo;\n"
-            << "      " << jv << "[u] = " << in.jx("i") << ";\n"
-            << "      " << xvv << "[u] = " << in.xx("i") << ";\n"
+            << "    for (int v = 0; v < " << E / 4 << "; v++) {\n"
+            << "      const int g = " << t << " + v * 1024 + 4 * (int)threadIdx.x;\n"
+            << "      if (g + 4 <= hi) {\n"
+            << "        " << in.vload_jx("g") << "\n";
+          for (int kk = 0; kk < 4; kk++)
+            l << "        " << jv << "[4 * v + " << kk << "] = " << in.jv("g", kk) << "; " << xvv << "[4 * v + " << kk
+              << "] = " << in.xv("g", kk) << ";\n";
+          l << "      } else {\n"
+            << "#pragma unroll\n"
+            << "        for (int c = 0; c < 4; c++) {\n"
+            << "          const int i = g + c < hi ? g + c : lo;\n"
+            << "          " << jv << "[4 * v + c] = " << in.jx("i") << ";\n"
+            << "          " << xvv << "[4 * v + c] = " << in.xx("i") << ";\n"
+            << "        }\n"
+            << "      }\n"
             << "    }\n";
           return l.str();
         };
+        // element u of the thread's tile (the layout above)
+        const std::string eidx = "(t0 + ((u >> 2) << 10) + 4 * (int)threadIdx.x + (u & 3))";
         if (pf)
           k << "  int jn[" << E << "];\n"
             << "  " << T << " xn[" << E << "];\n"
@@ -2456,7 +2500,7 @@ struct Lowering {
           << "#pragma unroll\n"
           << "    for (int u = 0; u < " << E << "; u++) {\n"
           << "      rk[u] = 0;\n"
-          << "      if (t0 + u * 256 + (int)threadIdx.x >= hi) { jj[u] = -1; continue; }\n"
+          << "      if (" << eidx << " >= hi) { jj[u] = -1; continue; }\n"
           << "      if (" << bounds("jj[u]") << ") rk[u] = atomicAdd(&tc[jj[u] >> " << sh << "], 1);\n"
           << "      else { " << (in.check ? "cc_flag(err, 2); " : "") << "jj[u] = -1; }\n"
           << "    }\n"
@@ -2518,16 +2562,19 @@ struct Lowering {
           k << "    {\n"
             << "      unsigned short* const slots = (unsigned short*)b" << o.slot << ";\n"
 
-            // two slots per 32-bit store: even lanes (even i, t0 being a
-            // multiple of 256) take their odd neighbour's slot
+            // a group's four slots in one 8-byte store
             << "#pragma unroll\n"
-            << "      for (int u = 0; u < " << E << "; u++) {\n"
-            << "        const int i = t0 + u * 256 + (int)threadIdx.x;\n"
-            << "        const unsigned v = jj[u] >= 0 ? (unsigned)(tc[jj[u] >> " << sh << "] + rk[u]) : 0xffffu;\n"
-            << "        const unsigned w = __shfl_down(v, 1);\n"
-            << "        if ((threadIdx.x & 1) == 0 && i < hi) {\n"
-            << "          if (i + 1 < hi) *(unsigned*)(slots + i) = v | (w << 16);\n"
-            << "          else slots[i] = (unsigned short)v;\n"
+            << "      for (int v = 0; v < " << E / 4 << "; v++) {\n"
+            << "        const int g = t0 + v * 1024 + 4 * (int)threadIdx.x;\n"
+            << "        unsigned sv[4];\n"
+            << "#pragma unroll\n"
+            << "        for (int c = 0; c < 4; c++)\n"
+            << "          sv[c] = jj[4 * v + c] >= 0 ? (unsigned)(tc[jj[4 * v + c] >> " << sh << "] + rk[4 * v + c]) : 0xffffu;\n"
+            << "        if (g + 4 <= hi) {\n"
+            << "          *(uint2*)(slots + g) = make_uint2(sv[0] | (sv[1] << 16), sv[2] | (sv[3] << 16));\n"
+            << "        } else {\n"
+            << "#pragma unroll\n"
+            << "          for (int c = 0; c < 4; c++) if (g + c < hi) slots[g + c] = (unsigned short)sv[c];\n"
             << "        }\n"
             << "      }\n"
             << "    }\n";
@@ -2572,6 +2619,19 @@ struct Lowering {
     add_in(first.p, fs);
     first.jx = [&](const std::string &i) { return fi.call_scalar(i); };
     first.xx = [&](const std::string &i) { return fs.call_scalar(i); };
+    ElemFn fboth;  // identity loads shared by both functions, once
+    fboth.ident = fi.ident;
+    for (int b : fs.ident)
+      if (std::find(fboth.ident.begin(), fboth.ident.end(), b) == fboth.ident.end()) fboth.ident.push_back(b);
+    auto oneline = [](std::string t) {
+      for (char &c : t)
+        if (c == '\n') c = ' ';
+      return t;
+    };
+    first.vload_j = [&, oneline](const std::string &i) { return oneline(vec_loads(fi, i, "", tyof())); };
+    first.vload_jx = [&, oneline](const std::string &i) { return oneline(vec_loads(fboth, i, "", tyof())); };
+    first.jv = [&](const std::string &i, int k) { return lane_call(fi, i, k); };
+    first.xv = [&](const std::string &i, int k) { return lane_call(fs, i, k); };
     first.nvalid = std::to_string(N);
     first.check = true;
     const int64_t STAGE_P = tune("scatter_stage_p", 512);
@@ -2595,6 +2655,16 @@ struct Lowering {
       for (int b : {c1.key, c1.val, c1.start}) second.p.in.push_back(b);
       second.jx = [&, c1](const std::string &i) { return "b" + std::to_string(c1.key) + "[" + i + "]"; };
       second.xx = [&, c1](const std::string &i) { return "b" + std::to_string(c1.val) + "[" + i + "]"; };
+      const std::string kb = "b" + std::to_string(c1.key), vb = "b" + std::to_string(c1.val);
+      second.vload_j = [kb](const std::string &i) {
+        return "const cc_v4<int> lk_ = *(const cc_v4<int>*)(" + kb + " + " + i + ");";
+      };
+      second.vload_jx = [kb, vb, T](const std::string &i) {
+        return "const cc_v4<int> lk_ = *(const cc_v4<int>*)(" + kb + " + " + i + "); const cc_v4<" + T +
+               "> lv_ = *(const cc_v4<" + T + ">*)(" + vb + " + " + i + ");";
+      };
+      second.jv = [](const std::string &, int k) { return std::string("lk_.") + "xyzw"[k]; };
+      second.xv = [](const std::string &, int k) { return std::string("lv_.") + "xyzw"[k]; };
       second.nvalid = "b" + std::to_string(c1.start) + "[" + std::to_string(P1) + "]";
       second.nbuf = c1.start;
       second.check = false;
@@ -2626,22 +2696,36 @@ struct Lowering {
         << "  const int lo = s0 + (int)((long long)len * w / " << W << ");\n"
         << "  const int hi = s0 + (int)((long long)len * (w + 1) / " << W << ");\n"
         << "  const unsigned short* const keys = (const unsigned short*)b" << key << ";\n"
-        << "  for (int i0 = lo + (int)threadIdx.x; i0 < hi; i0 += 1024) {\n"
-        << "    int kk[4];\n"
-        << "    " << T << " xx[4];\n"
+        << "  const " << T << "* const vals = b" << val << ";\n"
+        // the 8-aligned body: 8 keys in one 16-byte load and 8 values in
+        // 16-byte vectors, two groups a thread in flight; the unaligned head
+        // and tail one by one
+        << "  typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));\n"
+        << "  typedef __attribute__((ext_vector_type(4))) " << T << " v4;\n"
+        << "  const int up8 = (lo + 7) & ~7, dn8 = hi & ~7;\n"
+        << "  const int lo8 = up8 < hi ? up8 : hi;\n"
+        << "  const int hi8 = dn8 > lo8 ? dn8 : lo8;\n"
+        << "  for (int i = lo + (int)threadIdx.x; i < lo8; i += 256) cc_lds_add(&h[keys[i]], vals[i]);\n"
+        << "  for (int i = hi8 + (int)threadIdx.x; i < hi; i += 256) cc_lds_add(&h[keys[i]], vals[i]);\n"
+        << "  for (int j0 = lo8 + 8 * (int)threadIdx.x; j0 < hi8; j0 += 4096) {\n"
+        << "    u16x8 kv[2];\n"
+        << "    v4 xa[2], xb[2];\n"
         << "#pragma unroll\n"
-        << "    for (int u = 0; u < 4; u++) {\n"
-        << "      const int i = i0 + u * 256 < hi ? i0 + u * 256 : lo;\n"
-        << "      kk[u] = keys[i];\n"
-        << "      xx[u] = b" << val << "[i];\n"
+        << "    for (int u = 0; u < 2; u++) {\n"
+        << "      const int j = j0 + u * 2048 < hi8 ? j0 + u * 2048 : j0;\n"
+        << "      kv[u] = *(const u16x8*)(keys + j);\n"
+        << "      xa[u] = *(const v4*)(vals + j);\n"
+        << "      xb[u] = *(const v4*)(vals + j + 4);\n"
         << "    }\n"
-        // past the end: +0 into bin 0, which leaves every bin unchanged
-        // (tables start at +0, so no bin holds -0) and keeps the use of the
-        // loads unconditional
+        // a group past the end adds +0 into bin 0, which leaves every bin
+        // unchanged (tables start at +0, so no bin holds -0) and keeps the
+        // use of the loads unconditional
         << "#pragma unroll\n"
-        << "    for (int u = 0; u < 4; u++) {\n"
-        << "      const bool in = i0 + u * 256 < hi;\n"
-        << "      cc_lds_add(&h[in ? kk[u] : 0], in ? xx[u] : " << zero_of(n.dt) << ");\n"
+        << "    for (int u = 0; u < 2; u++) {\n"
+        << "      const bool in = j0 + u * 2048 < hi8;\n"
+        << "#pragma unroll\n"
+        << "      for (int e = 0; e < 8; e++)\n"
+        << "        cc_lds_add(&h[in ? kv[u][e] : 0], in ? (e < 4 ? xa[u][e] : xb[u][e - 4]) : " << zero_of(n.dt) << ");\n"
         << "    }\n"
         << "  }\n"
         << "  __syncthreads();\n";
