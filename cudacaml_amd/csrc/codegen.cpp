@@ -778,9 +778,10 @@ __device__ __forceinline__ void cc_lds_add(double* p, double v) {
     seen = cur;
   }
 }
-// Exclusive prefix of v over a 256-thread workgroup; *total gets the sum.
-// ws: 4 ints of LDS. Every thread of the workgroup must call it.
-__device__ __forceinline__ int cc_wg_exscan(int v, int* ws, int* total) {
+// Exclusive prefix of v over a workgroup of NW wave64s; *total gets the
+// sum. ws: NW ints of LDS. Every thread of the workgroup must call it.
+template <int NW>
+__device__ __forceinline__ int cc_wg_exscan_n(int v, int* ws, int* total) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   int incl = v;
 #pragma unroll
@@ -792,7 +793,7 @@ __device__ __forceinline__ int cc_wg_exscan(int v, int* ws, int* total) {
   __syncthreads();
   int base = 0, tot = 0;
 #pragma unroll
-  for (int w = 0; w < 4; w++) {
+  for (int w = 0; w < NW; w++) {
     const int t = ws[w];
     if (w < wv) base += t;
     tot += t;
@@ -801,6 +802,8 @@ __device__ __forceinline__ int cc_wg_exscan(int v, int* ws, int* total) {
   __syncthreads();
   return base + incl - v;
 }
+// The same over a 256-thread workgroup.
+__device__ __forceinline__ int cc_wg_exscan(int v, int* ws, int* total) { return cc_wg_exscan_n<4>(v, ws, total); }
 __device__ __forceinline__ cc_u64 cc_bits(float v) { return (cc_u64)__float_as_uint(v); }
 __device__ __forceinline__ cc_u64 cc_bits(int v) { return (cc_u64)(cc_u32)v; }
 __device__ __forceinline__ cc_u64 cc_bits(double v) { return (cc_u64)__double_as_longlong(v); }
@@ -935,6 +938,13 @@ struct Lowering {
     int64_t G = 0, C = 0, TILE = 0, TPC = 0, PB = 0;
     std::string nvalid;
     bool first = false;
+    // Tile-local layout: each tile's pairs stay in the tile's own region of
+    // RS elements, grouped by bucket, every bucket's run starting at a
+    // multiple of 8; `meta` holds per bucket and tile {run start within the
+    // region, count} ([PB + 1][NTT] int2, row PB: {the region's used
+    // length, 0}). No count or offset passes.
+    bool local = false;
+    int64_t RS = 0, NTT = 0;
     // per tile: K, the K + 1 tile-local starts of its non-empty buckets
     // (the last is the tile's total), their K run starts in the pair arrays
     int64_t kmax() const { return std::min(TILE, PB); }
@@ -2130,6 +2140,52 @@ struct Lowering {
   // and flag error 2, as the atomic path does. Within a slice the order of
   // the additions depends on LDS arrival order, so float sums are not
   // bit-reproducible (the atomic path's are not either).
+  // The runs of slice q over tiles [t_lo, t_hi) of a tile-local partition (`o`),
+  // 8 elements a lane, two groups of 8 a lane in flight. Each wave takes 64
+  // tiles at a time: their run lengths in groups of 8 are summed across the
+  // wave, and a lane finds its group's tile by a binary search over those
+  // sums, so that consecutive lanes read consecutive groups. `loads` then
+  // `body` are emitted with pos_[u] (the group's first element) and nv_[u]
+  // (its valid elements; 0 for a lane without a group, whose pos_ still
+  // points into the pair arrays) for u = 0, 1 in scope.
+  static std::string runs_walk(const PassOut &o, int64_t threads, const std::string &loads, const std::string &body) {
+    std::ostringstream l;
+    l << "  {\n"
+      << "    const int2* const runs_ = (const int2*)b" << o.meta << " + (size_t)q * " << o.NTT << ";\n"
+      << "    const int lane_ = threadIdx.x & 63;\n"
+      << "    for (int tb = t_lo + (int)(threadIdx.x >> 6) * 64; tb < t_hi; tb += " << threads << ") {\n"
+      << "      const int2 m_ = tb + lane_ < t_hi ? runs_[tb + lane_] : make_int2(0, 0);\n"
+      << "      const int ng_ = (m_.y + 7) >> 3;\n"
+      << "      int in_ = ng_;\n"
+      << "#pragma unroll\n"
+      << "      for (int d = 1; d < 64; d <<= 1) {\n"
+      << "        const int o_ = __shfl_up(in_, d);\n"
+      << "        if (lane_ >= d) in_ += o_;\n"
+      << "      }\n"
+      << "      const int tot_ = __shfl(in_, 63), ex_ = in_ - ng_;\n"
+      << "      for (int k0 = 0; k0 < tot_; k0 += 128) {\n"
+      << "        size_t pos_[2];\n"
+      << "        int nv_[2];\n"
+      << "#pragma unroll\n"
+      << "        for (int u = 0; u < 2; u++) {\n"
+      << "          const int j = k0 + u * 64 + lane_;\n"
+      << "          int i = 0;\n"
+      << "#pragma unroll\n"
+      << "          for (int st = 32; st >= 1; st >>= 1) {\n"
+      << "            const int c = __shfl(in_, i + st - 1);\n"
+      << "            if (c <= j) i += st;\n"
+      << "          }\n"
+      << "          const int e0 = __shfl(ex_, i), off = __shfl(m_.x, i), cnt = __shfl(m_.y, i);\n"
+      << "          const bool ok = j < tot_;\n"
+      << "          pos_[u] = (size_t)(ok ? tb + i : tb) * " << o.RS << " + (ok ? off + 8 * (j - e0) : 0);\n"
+      << "          nv_[u] = ok ? min(8, cnt - 8 * (j - e0)) : 0;\n"
+      << "        }\n"
+      << loads << body << "      }\n"
+      << "    }\n"
+      << "  }\n";
+    return l.str();
+  }
+
   std::vector<int> lower_scatter_lds(int t, int64_t B, int64_t N, int64_t S, int64_t P) {
     const TNode &n = g.ts[t];
     std::string id = std::to_string(n.id);
@@ -2223,6 +2279,11 @@ struct Lowering {
     // occupancy: config 3's partition 323 -> 278 us, config 3b's coarse
     // pass 302 -> 269 us), 4096 above (config 3b's fine pass: 339 against
     // 409 us); scatter_tile forces one size.
+    // 1024 threads per staged partition workgroup (config 3's partition
+    // 320 -> 288 us, config 3b's passes 313 / 370 -> 282 / 295 us, against
+    // 256; 512 is in between); 256 and 512 by scatter_part_threads.
+    const int64_t part_threads = tune("scatter_part_threads", 1024) == 256 ? 256
+                                 : tune("scatter_part_threads", 1024) == 512 ? 512 : 1024;
     auto tile_of = [&](int64_t PB) -> int64_t {
       const int64_t t = tune("scatter_tile", 0);
       if (t == 4096 || t == 8192) return t;
@@ -2246,8 +2307,8 @@ struct Lowering {
       bool check;
     };
     auto pass = [&](const std::string &sfx, const PassIn &in, int SH, int64_t PB, bool staged, bool final_keys,
-                    const std::string &part_role, bool keep) {
-      const int64_t TILE = tile_of(PB), E = TILE / 256;
+                    const std::string &part_role, bool keep, bool local) {
+      const int64_t TILE = tile_of(PB);
       int64_t G = std::max<int64_t>(1, std::min<int64_t>(tune("scatter_chunks", 1024), cdiv(N, 4096)));
       int64_t C = cdiv(cdiv(N, G), 256) * 256;
       G = cdiv(N, C);
@@ -2260,12 +2321,24 @@ struct Lowering {
       o.nvalid = in.nvalid;
       o.nbuf = in.nbuf;
       o.first = in.check;
-      o.cnt = add_buf("t" + id + "_cnt" + sfx, DT::I32, G * PB, BufRole::Scratch);
-      o.start = add_buf("t" + id + "_start" + sfx, DT::I32, PB + 1, BufRole::Scratch);
-      o.key = final_keys ? add_buf("t" + id + "_key" + sfx, DT::I32, cdiv(N, 2), BufRole::Scratch)  // 16-bit keys
-                         : add_buf("t" + id + "_key" + sfx, DT::I32, N, BufRole::Scratch);
-      o.val = add_buf("t" + id + "_val" + sfx, n.dt, N, BufRole::Scratch);
-      if (keep) {
+      o.local = local;
+      if (local) {
+        // regions of RS elements: the tile plus at most 7 of padding per
+        // bucket, rounded to a multiple of 8
+        o.NTT = G * o.TPC;
+        o.RS = TILE + 8 * PB;
+        o.key = add_buf("t" + id + "_key" + sfx, DT::I32, cdiv(o.NTT * o.RS, 2), BufRole::Scratch);  // 16-bit keys
+        o.val = add_buf("t" + id + "_val" + sfx, n.dt, o.NTT * o.RS, BufRole::Scratch);
+        o.meta = add_buf("t" + id + "_runs" + sfx, DT::I32, 2 * (PB + 1) * o.NTT, BufRole::Scratch);
+        if (keep) o.slot = add_buf("t" + id + "_slot" + sfx, DT::I32, cdiv(N, 2), BufRole::Scratch);
+      } else {
+        o.cnt = add_buf("t" + id + "_cnt" + sfx, DT::I32, G * PB, BufRole::Scratch);
+        o.start = add_buf("t" + id + "_start" + sfx, DT::I32, PB + 1, BufRole::Scratch);
+        o.key = final_keys ? add_buf("t" + id + "_key" + sfx, DT::I32, cdiv(N, 2), BufRole::Scratch)  // 16-bit keys
+                           : add_buf("t" + id + "_key" + sfx, DT::I32, N, BufRole::Scratch);
+        o.val = add_buf("t" + id + "_val" + sfx, n.dt, N, BufRole::Scratch);
+      }
+      if (keep && !local) {
         // for a gather back through this partition: each element's slot in
         // its tile's bucket-grouped order (16 bits, 0xffff where the element
         // was skipped), and per tile the bucket runs' starts in the pair
@@ -2309,8 +2382,9 @@ struct Lowering {
       };
       std::string key_decl = final_keys ? "  unsigned short* const keys = (unsigned short*)b" + std::to_string(o.key) + ";\n"
                                         : "  int* const keys = b" + std::to_string(o.key) + ";\n";
-      {  // count: each wave into its own copy of the bucket counters (fewer
-         // same-address LDS atomics), the copies summed at the end
+      if (!local) {  // count: each wave into its own copy of the bucket
+                     // counters (fewer same-address LDS atomics), the copies
+                     // summed at the end
         int64_t NC = std::max<int64_t>(1, std::min<int64_t>(tune("scatter_count_copies", 4), 4));
         while (NC > 1 && NC * PB * 4 > 32768) NC /= 2;
         Params p = in.p;
@@ -2356,8 +2430,10 @@ struct Lowering {
         src << k.str();
         ks.push_back(add_kernel(kname + "_count" + sfx, args, (int)G, 256, "scatter_count"));
       }
-      if (PB >= 1024) {  // colscan, many buckets: a thread per bucket walks
-                         // the chunks (loads coalesced across threads)
+      if (local) {
+      } else if (PB >= 1024) {  // colscan, many buckets: a thread per bucket
+                                // walks the chunks (loads coalesced across
+                                // threads)
         std::ostringstream k;
         k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_colscan" << sfx << "(int* __restrict__ b"
           << o.cnt << ", int* __restrict__ b" << o.start << ") {\n"
@@ -2400,7 +2476,7 @@ struct Lowering {
         src << k.str();
         ks.push_back(add_kernel(kname + "_colscan" + sfx, {o.cnt, o.start}, (int)PB, 256, "scatter_colscan"));
       }
-      {  // bscan: one workgroup, exclusive prefix of the bucket totals
+      if (!local) {  // bscan: one workgroup, exclusive prefix of the bucket totals
         int64_t per = cdiv(PB, 256);
         std::ostringstream k;
         k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_bscan" << sfx << "(int* __restrict__ b"
@@ -2426,43 +2502,57 @@ struct Lowering {
         ks.push_back(add_kernel(kname + "_bscan" + sfx, {o.start}, 1, 256, "scatter_bscan"));
       }
       Params p = in.p;
-      for (int b : {o.cnt, o.start}) p.in.push_back(b);
+      if (!local)
+        for (int b : {o.cnt, o.start}) p.in.push_back(b);
       p.out.push_back(o.key);
       p.out.push_back(o.val);
-      if (keep && staged) {
-        p.out.push_back(o.slot);
-        p.out.push_back(o.meta);
-      }
+      if (keep && staged) p.out.push_back(o.slot);
+      if ((keep && staged) || local) p.out.push_back(o.meta);
       if (in.check) p.err = true;
       std::vector<int> args;
       std::string params = param_list(p, args);
       std::ostringstream k;
-      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_partition" << sfx << "(" << params
-        << ") {\n";
+      // Threads of a staged partition workgroup (scatter_part_threads): its
+      // LDS tile caps the workgroups per CU at two, so more threads per
+      // workgroup keep more memory work in flight.
+      const int64_t NT = staged ? part_threads : 256;
+      const std::string snt = std::to_string(NT);
+      k << "extern \"C\" __global__ __launch_bounds__(" << NT << ") void " << kname << "_partition" << sfx << "("
+        << params << ") {\n";
       if (staged) {
         // each tile is grouped by bucket in LDS, then written as contiguous
         // runs
-        int64_t PP = cdiv(PB, 256);
-        k << "  __shared__ int cur[" << PB << "];\n"
-          << "  __shared__ int tc[" << PB + 1 << "];\n"
-          << "  __shared__ int sj[" << TILE << "];\n"
-          << "  __shared__ " << T << " sx[" << TILE << "];\n"
-          << "  __shared__ int ws[4];\n"
-          << "  for (int q = threadIdx.x; q < " << PB << "; q += 256) cur[q] = b" << o.start << "[q] + b" << o.cnt
-          << "[(size_t)blockIdx.x * " << PB << " + q];\n"
-          << key_decl << chunk_head();
+        const int64_t E = TILE / NT;
+        int64_t PP = cdiv(PB, NT);
+        if (local)
+          // keys staged as 16 bits (the key within the slice), values beside
+          k << "  __shared__ int tc[" << PB + 1 << "];\n"
+            << "  __shared__ __align__(16) unsigned short sj[" << o.RS << "];\n"
+            << "  __shared__ __align__(16) " << T << " sx[" << o.RS << "];\n"
+            << "  __shared__ int ws[" << NT / 64 << "];\n"
+            << "  int2* const runs = (int2*)b" << o.meta << ";\n"
+            << key_decl << chunk_head();
+        else
+          k << "  __shared__ int cur[" << PB << "];\n"
+            << "  __shared__ int tc[" << PB + 1 << "];\n"
+            << "  __shared__ int sj[" << TILE << "];\n"
+            << "  __shared__ " << T << " sx[" << TILE << "];\n"
+            << "  __shared__ int ws[" << NT / 64 << "];\n"
+            << "  for (int q = threadIdx.x; q < " << PB << "; q += " << NT << ") cur[q] = b" << o.start << "[q] + b"
+            << o.cnt << "[(size_t)blockIdx.x * " << PB << " + q];\n"
+            << key_decl << chunk_head();
         // The next tile's indices and values are loaded into a second set of
         // registers before this tile's LDS work starts (scatter_prefetch).
         const bool pf = tune("scatter_prefetch", 1) != 0;
         // A thread's E elements of a tile: E/4 groups of 4 consecutive
-        // elements, group v at t + 1024 v + 4 threadIdx.x (a multiple of 4:
+        // elements, group v at t + 4 NT v + 4 threadIdx.x (a multiple of 4:
         // tiles start at multiples of 256), each loaded with 16-byte
         // accesses; a group that runs past hi one by one, clamped.
         auto tile_load = [&](const std::string &t, const std::string &jv, const std::string &xvv) {
           std::ostringstream l;
           l << "#pragma unroll\n"
             << "    for (int v = 0; v < " << E / 4 << "; v++) {\n"
-            << "      const int g = " << t << " + v * 1024 + 4 * (int)threadIdx.x;\n"
+            << "      const int g = " << t << " + v * " << 4 * NT << " + 4 * (int)threadIdx.x;\n"
             << "      if (g + 4 <= hi) {\n"
             << "        " << in.vload_jx("g") << "\n";
           for (int kk = 0; kk < 4; kk++)
@@ -2480,13 +2570,14 @@ struct Lowering {
           return l.str();
         };
         // element u of the thread's tile (the layout above)
-        const std::string eidx = "(t0 + ((u >> 2) << 10) + 4 * (int)threadIdx.x + (u & 3))";
+        const std::string eidx = "(t0 + (u >> 2) * " + std::to_string(4 * NT) + " + 4 * (int)threadIdx.x + (u & 3))";
         if (pf)
           k << "  int jn[" << E << "];\n"
             << "  " << T << " xn[" << E << "];\n"
             << "  if (lo < hi) {\n" << tile_load("lo", "jn", "xn") << "  }\n";
         k << "  for (int t0 = lo; t0 < hi; t0 += " << TILE << ") {\n"
-          << "    for (int q = threadIdx.x; q < " << PB << "; q += 256) tc[q] = 0;\n"
+          << "    const int tt = blockIdx.x * " << o.TPC << " + (t0 - lo) / " << TILE << ";\n"
+          << "    for (int q = threadIdx.x; q < " << PB << "; q += " << NT << ") tc[q] = 0;\n"
           << "    int jj[" << E << "], rk[" << E << "];\n"
           << "    " << T << " xv[" << E << "];\n";
         if (pf)
@@ -2506,7 +2597,32 @@ struct Lowering {
           << "    }\n"
           << "    __syncthreads();\n"
           << "    {\n";
-        if (!keep)
+        if (local)
+          // runs padded to multiples of 8 elements; per bucket its run start
+          // and count, and the region's used length
+          k << "      int loc[" << PP << "], cn[" << PP << "], s = 0;\n"
+            << "#pragma unroll\n"
+            << "      for (int c = 0; c < " << PP << "; c++) {\n"
+            << "        const int q = threadIdx.x * " << PP << " + c;\n"
+            << "        loc[c] = s;\n"
+            << "        cn[c] = q < " << PB << " ? tc[q] : 0;\n"
+            << "        s += (cn[c] + 7) & ~7;\n"
+            << "      }\n"
+            << "      int tot;\n"
+            << "      const int base = cc_wg_exscan_n<" << NT / 64 << ">(s, ws, &tot);\n"
+            << "#pragma unroll\n"
+            << "      for (int c = 0; c < " << PP << "; c++) {\n"
+            << "        const int q = threadIdx.x * " << PP << " + c;\n"
+            << "        if (q < " << PB << ") {\n"
+            << "          tc[q] = base + loc[c];\n"
+            << "          runs[(size_t)q * " << o.NTT << " + tt] = make_int2(base + loc[c], cn[c]);\n"
+            << "        }\n"
+            << "      }\n"
+            << "      if (threadIdx.x == 0) {\n"
+            << "        tc[" << PB << "] = tot;\n"
+            << "        runs[(size_t)" << PB * o.NTT << " + tt] = make_int2(tot, 0);\n"
+            << "      }\n";
+        else if (!keep)
           k << "      int loc[" << PP << "], s = 0;\n"
             << "#pragma unroll\n"
             << "      for (int c = 0; c < " << PP << "; c++) {\n"
@@ -2515,7 +2631,7 @@ struct Lowering {
             << "        s += q < " << PB << " ? tc[q] : 0;\n"
             << "      }\n"
             << "      int tot;\n"
-            << "      const int base = cc_wg_exscan(s, ws, &tot);\n"
+            << "      const int base = cc_wg_exscan_n<" << NT / 64 << ">(s, ws, &tot);\n"
             << "#pragma unroll\n"
             << "      for (int c = 0; c < " << PP << "; c++) {\n"
             << "        const int q = threadIdx.x * " << PP << " + c;\n"
@@ -2538,7 +2654,7 @@ struct Lowering {
             << "        s += cn[c] + (cn[c] > 0 ? 0x10000 : 0);\n"
             << "      }\n"
             << "      int tot;\n"
-            << "      const int base = cc_wg_exscan(s, ws, &tot);\n"
+            << "      const int base = cc_wg_exscan_n<" << NT / 64 << ">(s, ws, &tot);\n"
             << "      const size_t mt = ((size_t)blockIdx.x * " << o.TPC << " + (t0 - lo) / " << TILE << ") * "
             << o.meta_stride() << ";\n"
             << "#pragma unroll\n"
@@ -2565,7 +2681,7 @@ struct Lowering {
             // a group's four slots in one 8-byte store
             << "#pragma unroll\n"
             << "      for (int v = 0; v < " << E / 4 << "; v++) {\n"
-            << "        const int g = t0 + v * 1024 + 4 * (int)threadIdx.x;\n"
+            << "        const int g = t0 + v * " << 4 * NT << " + 4 * (int)threadIdx.x;\n"
             << "        unsigned sv[4];\n"
             << "#pragma unroll\n"
             << "        for (int c = 0; c < 4; c++)\n"
@@ -2578,6 +2694,36 @@ struct Lowering {
             << "        }\n"
             << "      }\n"
             << "    }\n";
+        if (local) {
+          // the tile's region written whole, 8 elements a thread: one
+          // 16-byte store of keys, 16-byte stores of values (padding
+          // included; readers stop at each run's count)
+          k << "#pragma unroll\n"
+            << "    for (int u = 0; u < " << E << "; u++)\n"
+            << "      if (jj[u] >= 0) {\n"
+            << "        const int slot = tc[jj[u] >> " << sh << "] + rk[u];\n"
+            << "        sj[slot] = (unsigned short)(jj[u] & " << S - 1 << ");\n"
+            << "        sx[slot] = xv[u];\n"
+            << "      }\n"
+            << "    __syncthreads();\n"
+            << "    {\n"
+            << "      typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));\n"
+            << "      typedef __attribute__((ext_vector_type(4))) " << T << " v4;\n"
+            << "      const size_t rb = (size_t)tt * " << o.RS << ";\n"
+            << "      for (int s = 8 * (int)threadIdx.x; s < tc[" << PB << "]; s += " << 8 * NT << ") {\n"
+            << "        *(u16x8*)(keys + rb + s) = *(const u16x8*)(sj + s);\n"
+            << "        *(v4*)(b" << o.val << " + rb + s) = *(const v4*)(sx + s);\n"
+            << "        *(v4*)(b" << o.val << " + rb + s + 4) = *(const v4*)(sx + s + 4);\n"
+            << "      }\n"
+            << "    }\n"
+            << "    __syncthreads();\n"
+            << "  }\n"
+            // a chunk's tiles past the end of the input: empty runs
+            << "  for (int x = threadIdx.x + (hi - lo + " << TILE - 1 << ") / " << TILE << " * " << PB + 1 << "; x < "
+            << o.TPC * (PB + 1) << "; x += " << NT << ")\n"
+            << "    runs[(size_t)(x % " << PB + 1 << ") * " << o.NTT << " + blockIdx.x * " << o.TPC << " + x / "
+            << PB + 1 << "] = make_int2(0, 0);\n";
+        } else {
         k << "#pragma unroll\n"
           << "    for (int u = 0; u < " << E << "; u++)\n"
           << "      if (jj[u] >= 0) {\n"
@@ -2586,16 +2732,17 @@ struct Lowering {
           << "        sx[slot] = xv[u];\n"
           << "      }\n"
           << "    __syncthreads();\n"
-          << "    for (int s = threadIdx.x; s < tc[" << PB << "]; s += 256) {\n"
+          << "    for (int s = threadIdx.x; s < tc[" << PB << "]; s += " << NT << ") {\n"
           << "      const int j = sj[s], q = j >> " << sh << ";\n"
           << "      const int pos = cur[q] + (s - tc[q]);\n"
           << "      " << key_store("pos", "j") << "\n"
           << "      b" << o.val << "[pos] = sx[s];\n"
           << "    }\n"
           << "    __syncthreads();\n"
-          << "    for (int q = threadIdx.x; q < " << PB << "; q += 256) cur[q] += tc[q + 1] - tc[q];\n"
+          << "    for (int q = threadIdx.x; q < " << PB << "; q += " << NT << ") cur[q] += tc[q + 1] - tc[q];\n"
           << "    __syncthreads();\n"
           << "  }\n";
+        }
       } else {
         k << "  __shared__ int cur[" << PB << "];\n"
           << "  for (int q = threadIdx.x; q < " << PB << "; q += 256) cur[q] = b" << o.start << "[q] + b" << o.cnt
@@ -2610,7 +2757,7 @@ struct Lowering {
       }
       k << "}\n";
       src << k.str();
-      ks.push_back(add_kernel(kname + "_partition" + sfx, args, (int)G, 256, part_role));
+      ks.push_back(add_kernel(kname + "_partition" + sfx, args, (int)G, (int)NT, part_role));
       return o;
     };
 
@@ -2639,17 +2786,21 @@ struct Lowering {
     // gather(idx, h) over the same index) keeps the staged passes' slots.
     const bool keep = gbp_root_of.count(t) > 0;
     PassOut fin, coarse;
+    // Tile-local layout up to 256 slices (runs of 32 elements a tile or
+    // more, on average, for 8192-element tiles): scatter_local_max sets the
+    // limit, 0 turns it off.
+    const bool local = P <= tune("scatter_local_max", 256) && P <= STAGE_P;
     if (P <= STAGE_P) {
-      fin = pass("", first, shift, P, true, true, "scatter_partition", keep);
+      fin = pass("", first, shift, P, true, true, "scatter_partition", keep, local);
     } else if (!tune("scatter_two_level", 1)) {
       // single level, element-wise stores
-      fin = pass("", first, shift, P, false, true, "scatter_partition", false);
+      fin = pass("", first, shift, P, false, true, "scatter_partition", false, false);
     } else {
       // Two levels: a coarse pass into super-slices of 64 slices (runs of
       // about 64 elements per tile), then the slice pass over the coarse
       // output, whose tiles each touch at most two super-slices.
       const int64_t P1 = cdiv(P, 64);
-      PassOut c1 = pass("1", first, shift + 6, P1, true, false, "scatter_coarse", keep);
+      PassOut c1 = pass("1", first, shift + 6, P1, true, false, "scatter_coarse", keep, false);
       coarse = c1;
       PassIn second;
       for (int b : {c1.key, c1.val, c1.start}) second.p.in.push_back(b);
@@ -2668,7 +2819,7 @@ struct Lowering {
       second.nvalid = "b" + std::to_string(c1.start) + "[" + std::to_string(P1) + "]";
       second.nbuf = c1.start;
       second.check = false;
-      fin = pass("", second, shift, P, true, true, "scatter_partition", keep);
+      fin = pass("", second, shift, P, true, true, "scatter_partition", keep, false);
     }
     if (keep && fin.slot >= 0) {
       GatherBack gb;
@@ -2684,15 +2835,50 @@ struct Lowering {
     const int start = fin.start, key = fin.key, val = fin.val;
     {  // accumulate
       int dst = part >= 0 ? part : out;
+      // Threads per workgroup: the LDS table caps the workgroups per CU, so
+      // more threads keep more loads in flight. 1024 (config 3 123 -> 117
+      // us, config 3b 167 -> 154 us, against 256); scatter_acc_threads=256
+      // or 512 for the others.
+      const int64_t AT = tune("scatter_acc_threads", 1024) == 256 ? 256
+                         : tune("scatter_acc_threads", 1024) == 512 ? 512 : 1024;
+      const int lead = fin.local ? fin.meta : start;  // where the slice's pairs are found
       std::ostringstream k;
-      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_accumulate(const int* __restrict__ b"
-        << start << ", const int* __restrict__ b" << key << ", const " << T << "* __restrict__ b" << val << ", " << T
+      k << "extern \"C\" __global__ __launch_bounds__(" << AT << ") void " << kname << "_accumulate(const int* __restrict__ b"
+        << lead << ", const int* __restrict__ b" << key << ", const " << T << "* __restrict__ b" << val << ", " << T
         << "* __restrict__ b" << dst << ") {\n"
         << "  __shared__ " << T << " h[" << S << "];\n"
         << "  const int q = blockIdx.x / " << W << ", w = blockIdx.x % " << W << ";\n"
-        << "  for (int b = threadIdx.x; b < " << S << "; b += 256) h[b] = " << zero_of(n.dt) << ";\n"
-        << "  __syncthreads();\n"
-        << "  const int s0 = b" << start << "[q], len = b" << start << "[q + 1] - s0;\n"
+        << "  for (int b = threadIdx.x; b < " << S << "; b += " << AT << ") h[b] = " << zero_of(n.dt) << ";\n"
+        << "  __syncthreads();\n";
+      if (fin.local) {
+        // the slice's runs in W shares of the tiles; a group's elements past
+        // its run's count add +0 into bin 0 (see below)
+        const std::string z = zero_of(n.dt);
+        k << "  const int t_lo = (int)((long long)" << fin.NTT << " * w / " << W << ");\n"
+          << "  const int t_hi = (int)((long long)" << fin.NTT << " * (w + 1) / " << W << ");\n"
+          << "  const unsigned short* const keys = (const unsigned short*)b" << key << ";\n"
+          << "  const " << T << "* const vals = b" << val << ";\n"
+          << "  typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));\n"
+          << "  typedef __attribute__((ext_vector_type(4))) " << T << " v4;\n"
+          << runs_walk(fin, AT,
+                       "        u16x8 kv[2];\n"
+                       "        v4 xa[2], xb[2];\n"
+                       "#pragma unroll\n"
+                       "        for (int u = 0; u < 2; u++) {\n"
+                       "          kv[u] = *(const u16x8*)(keys + pos_[u]);\n"
+                       "          xa[u] = *(const v4*)(vals + pos_[u]);\n"
+                       "          xb[u] = *(const v4*)(vals + pos_[u] + 4);\n"
+                       "        }\n",
+                       "#pragma unroll\n"
+                       "        for (int u = 0; u < 2; u++)\n"
+                       "#pragma unroll\n"
+                       "          for (int e = 0; e < 8; e++) {\n"
+                       "            const bool in = e < nv_[u];\n"
+                       "            cc_lds_add(&h[in ? kv[u][e] : 0], in ? (e < 4 ? xa[u][e] : xb[u][e - 4]) : " + z + ");\n"
+                       "          }\n")
+          << "  __syncthreads();\n";
+      } else {
+      k << "  const int s0 = b" << start << "[q], len = b" << start << "[q + 1] - s0;\n"
         << "  const int lo = s0 + (int)((long long)len * w / " << W << ");\n"
         << "  const int hi = s0 + (int)((long long)len * (w + 1) / " << W << ");\n"
         << "  const unsigned short* const keys = (const unsigned short*)b" << key << ";\n"
@@ -2705,14 +2891,14 @@ struct Lowering {
         << "  const int up8 = (lo + 7) & ~7, dn8 = hi & ~7;\n"
         << "  const int lo8 = up8 < hi ? up8 : hi;\n"
         << "  const int hi8 = dn8 > lo8 ? dn8 : lo8;\n"
-        << "  for (int i = lo + (int)threadIdx.x; i < lo8; i += 256) cc_lds_add(&h[keys[i]], vals[i]);\n"
-        << "  for (int i = hi8 + (int)threadIdx.x; i < hi; i += 256) cc_lds_add(&h[keys[i]], vals[i]);\n"
-        << "  for (int j0 = lo8 + 8 * (int)threadIdx.x; j0 < hi8; j0 += 4096) {\n"
+        << "  for (int i = lo + (int)threadIdx.x; i < lo8; i += " << AT << ") cc_lds_add(&h[keys[i]], vals[i]);\n"
+        << "  for (int i = hi8 + (int)threadIdx.x; i < hi; i += " << AT << ") cc_lds_add(&h[keys[i]], vals[i]);\n"
+        << "  for (int j0 = lo8 + 8 * (int)threadIdx.x; j0 < hi8; j0 += " << 16 * AT << ") {\n"
         << "    u16x8 kv[2];\n"
         << "    v4 xa[2], xb[2];\n"
         << "#pragma unroll\n"
         << "    for (int u = 0; u < 2; u++) {\n"
-        << "      const int j = j0 + u * 2048 < hi8 ? j0 + u * 2048 : j0;\n"
+        << "      const int j = j0 + u * " << 8 * AT << " < hi8 ? j0 + u * " << 8 * AT << " : j0;\n"
         << "      kv[u] = *(const u16x8*)(keys + j);\n"
         << "      xa[u] = *(const v4*)(vals + j);\n"
         << "      xb[u] = *(const v4*)(vals + j + 4);\n"
@@ -2722,23 +2908,24 @@ struct Lowering {
         // use of the loads unconditional
         << "#pragma unroll\n"
         << "    for (int u = 0; u < 2; u++) {\n"
-        << "      const bool in = j0 + u * 2048 < hi8;\n"
+        << "      const bool in = j0 + u * " << 8 * AT << " < hi8;\n"
         << "#pragma unroll\n"
         << "      for (int e = 0; e < 8; e++)\n"
         << "        cc_lds_add(&h[in ? kv[u][e] : 0], in ? (e < 4 ? xa[u][e] : xb[u][e - 4]) : " << zero_of(n.dt) << ");\n"
         << "    }\n"
         << "  }\n"
         << "  __syncthreads();\n";
+      }
       if (part >= 0)
-        k << "  for (int b = threadIdx.x; b < " << S << "; b += 256) b" << dst << "[(size_t)w * " << P * S
+        k << "  for (int b = threadIdx.x; b < " << S << "; b += " << AT << ") b" << dst << "[(size_t)w * " << P * S
           << " + (size_t)q * " << S << " + b] = h[b];\n";
       else
         k << "  const int nb = " << B << " - q * " << S << " < " << S << " ? " << B << " - q * " << S << " : " << S
           << ";\n"
-          << "  for (int b = threadIdx.x; b < nb; b += 256) b" << dst << "[(size_t)q * " << S << " + b] = h[b];\n";
+          << "  for (int b = threadIdx.x; b < nb; b += " << AT << ") b" << dst << "[(size_t)q * " << S << " + b] = h[b];\n";
       k << "}\n";
       src << k.str();
-      ks.push_back(add_kernel(kname + "_accumulate", {start, key, val, dst}, (int)(P * W), 256, "scatter_accumulate"));
+      ks.push_back(add_kernel(kname + "_accumulate", {lead, key, val, dst}, (int)(P * W), (int)AT, "scatter_accumulate"));
     }
     if (part >= 0) ks.push_back(scatter_reduce(kname, T, acc, part, out, W, B, P * S));
     return ks;
@@ -2855,12 +3042,18 @@ struct Lowering {
     std::vector<int> ks;
     // 8 values of T through 16-byte accesses: two 4-wide vectors
     const std::string v4 = "__attribute__((ext_vector_type(4))) " + T;
+    // Threads per workgroup of both kernels, whose LDS caps the workgroups
+    // per CU: 512 (config 3's unpartition 184 -> 154 us; config 3b's slices
+    // 161 -> 131, unpartition passes 224 / 172 -> 168 / 143 us, against
+    // 256; 1024 is in between); gather_threads=256 or 1024 for the others.
+    const int64_t GT = tune("gather_threads", 512) == 256 ? 256 : tune("gather_threads", 512) == 1024 ? 1024 : 512;
     {
       const int64_t S = gb.S, B = gb.B;
       const int64_t Wg = std::max<int64_t>(1, std::min<int64_t>(16, 1024 / gb.P));
+      const int lead = f.local ? f.meta : f.start;  // where each slice's pairs are found
       std::ostringstream k;
-      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_slices(const int* __restrict__ b"
-        << f.start << ", const int* __restrict__ b" << f.key << ", const " << T << "* __restrict__ b" << gb.h << ", "
+      k << "extern \"C\" __global__ __launch_bounds__(" << GT << ") void " << kname << "_slices(const int* __restrict__ b"
+        << lead << ", const int* __restrict__ b" << f.key << ", const " << T << "* __restrict__ b" << gb.h << ", "
         << T << "* __restrict__ b" << f.val << ") {\n"
         << "  typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));\n"
         << "  typedef " << v4 << " v4;\n"
@@ -2870,15 +3063,37 @@ struct Lowering {
         << ";\n"
         << "  const " << T << "* const hq = b" << gb.h << " + (size_t)q * " << S << ";\n"
         // the slice into LDS, eight loads in flight per thread
-        << "  for (int b0 = threadIdx.x; b0 < nb; b0 += 2048) {\n"
+        << "  for (int b0 = threadIdx.x; b0 < nb; b0 += " << 8 * GT << ") {\n"
         << "    " << T << " t[8];\n"
         << "#pragma unroll\n"
-        << "    for (int u = 0; u < 8; u++) t[u] = hq[b0 + u * 256 < nb ? b0 + u * 256 : b0];\n"
+        << "    for (int u = 0; u < 8; u++) t[u] = hq[b0 + u * " << GT << " < nb ? b0 + u * " << GT << " : b0];\n"
         << "#pragma unroll\n"
-        << "    for (int u = 0; u < 8; u++) if (b0 + u * 256 < nb) tab[b0 + u * 256] = t[u];\n"
+        << "    for (int u = 0; u < 8; u++) if (b0 + u * " << GT << " < nb) tab[b0 + u * " << GT << "] = t[u];\n"
         << "  }\n"
-        << "  __syncthreads();\n"
-        << "  const int s0 = b" << f.start << "[q], len = b" << f.start << "[q + 1] - s0;\n"
+        << "  __syncthreads();\n";
+      if (f.local) {
+        // the slice's runs in Wg shares of the tiles; a group's elements past
+        // its run's count read bin 0 and land in the run's padding
+        k << "  const int t_lo = (int)((long long)" << f.NTT << " * w / " << Wg << ");\n"
+          << "  const int t_hi = (int)((long long)" << f.NTT << " * (w + 1) / " << Wg << ");\n"
+          << "  const unsigned short* const keys = (const unsigned short*)b" << f.key << ";\n"
+          << "  " << T << "* const vals = b" << f.val << ";\n"
+          << runs_walk(f, GT,
+                       "        u16x8 kv[2];\n"
+                       "#pragma unroll\n"
+                       "        for (int u = 0; u < 2; u++) kv[u] = *(const u16x8*)(keys + pos_[u]);\n",
+                       "#pragma unroll\n"
+                       "        for (int u = 0; u < 2; u++)\n"
+                       "          if (nv_[u] > 0) {\n"
+                       "            " + T + " x[8];\n"
+                       "#pragma unroll\n"
+                       "            for (int e = 0; e < 8; e++) x[e] = tab[e < nv_[u] ? kv[u][e] : 0];\n"
+                       "            *(v4*)(vals + pos_[u]) = (v4){x[0], x[1], x[2], x[3]};\n"
+                       "            *(v4*)(vals + pos_[u] + 4) = (v4){x[4], x[5], x[6], x[7]};\n"
+                       "          }\n")
+          << "}\n";
+      } else {
+      k << "  const int s0 = b" << f.start << "[q], len = b" << f.start << "[q + 1] - s0;\n"
         << "  const int lo = s0 + (int)((long long)len * w / " << Wg << ");\n"
         << "  const int hi = s0 + (int)((long long)len * (w + 1) / " << Wg << ");\n"
         << "  const unsigned short* const keys = (const unsigned short*)b" << f.key << ";\n"
@@ -2888,30 +3103,32 @@ struct Lowering {
         << "  const int up8 = (lo + 7) & ~7, dn8 = hi & ~7;\n"
         << "  const int lo8 = up8 < hi ? up8 : hi;\n"
         << "  const int hi8 = dn8 > lo8 ? dn8 : lo8;\n"
-        << "  for (int j = lo + (int)threadIdx.x; j < lo8; j += 256) vals[j] = tab[keys[j]];\n"
-        << "  for (int j = hi8 + (int)threadIdx.x; j < hi; j += 256) vals[j] = tab[keys[j]];\n"
-        << "  for (int j0 = lo8 + 8 * (int)threadIdx.x; j0 < hi8; j0 += 8192) {\n"
+        << "  for (int j = lo + (int)threadIdx.x; j < lo8; j += " << GT << ") vals[j] = tab[keys[j]];\n"
+        << "  for (int j = hi8 + (int)threadIdx.x; j < hi; j += " << GT << ") vals[j] = tab[keys[j]];\n"
+        << "  for (int j0 = lo8 + 8 * (int)threadIdx.x; j0 < hi8; j0 += " << 32 * GT << ") {\n"
         << "    u16x8 kv[4];\n"
         << "#pragma unroll\n"
-        << "    for (int u = 0; u < 4; u++) kv[u] = *(const u16x8*)(keys + (j0 + u * 2048 < hi8 ? j0 + u * 2048 : j0));\n"
+        << "    for (int u = 0; u < 4; u++) kv[u] = *(const u16x8*)(keys + (j0 + u * " << 8 * GT << " < hi8 ? j0 + u * "
+        << 8 * GT << " : j0));\n"
         << "#pragma unroll\n"
         << "    for (int u = 0; u < 4; u++)\n"
-        << "      if (j0 + u * 2048 < hi8) {\n"
+        << "      if (j0 + u * " << 8 * GT << " < hi8) {\n"
         << "        const v4 a = {tab[kv[u][0]], tab[kv[u][1]], tab[kv[u][2]], tab[kv[u][3]]};\n"
         << "        const v4 c = {tab[kv[u][4]], tab[kv[u][5]], tab[kv[u][6]], tab[kv[u][7]]};\n"
-        << "        *(v4*)(vals + j0 + u * 2048) = a;\n"
-        << "        *(v4*)(vals + j0 + u * 2048 + 4) = c;\n"
+        << "        *(v4*)(vals + j0 + u * " << 8 * GT << ") = a;\n"
+        << "        *(v4*)(vals + j0 + u * " << 8 * GT << " + 4) = c;\n"
         << "      }\n"
         << "  }\n"
         << "}\n";
+      }
       src << k.str();
-      ks.push_back(add_kernel(kname + "_slices", {f.start, f.key, gb.h, f.val}, (int)(gb.P * Wg), 256,
+      ks.push_back(add_kernel(kname + "_slices", {lead, f.key, gb.h, f.val}, (int)(gb.P * Wg), (int)GT,
                               "gather_slices"));
     }
     auto unpartition = [&](const std::string &sfx, const PassOut &o, int from, int to, bool flag) {
       std::vector<int> args = {o.meta, o.slot, from, to};
       std::ostringstream k;
-      k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_unpartition" << sfx
+      k << "extern \"C\" __global__ __launch_bounds__(" << GT << ") void " << kname << "_unpartition" << sfx
         << "(const int* __restrict__ b" << o.meta << ", const int* __restrict__ b" << o.slot << ", const " << T
         << "* __restrict__ b" << from << ", " << T << "* __restrict__ b" << to;
       if (o.nbuf >= 0) {
@@ -2923,8 +3140,47 @@ struct Lowering {
         args.push_back(err_buf());
       }
       const int64_t KM = o.kmax();
-      const int64_t E = o.TILE / 256, VB = o.TILE / 2048;  // slots, 8-element groups per thread
+      const int64_t E = o.TILE / GT, VB = cdiv(o.TILE, 8 * GT);  // slots, 8-element groups per thread
       const std::string zero = zero_of(n.dt);
+      if (o.local) {
+        // the tile's region, read whole into LDS, then every element takes
+        // the value at its slot
+        const int64_t VR = cdiv(o.RS, 8 * GT);  // 8-element groups of the region per thread
+        k << ") {\n"
+          << "  typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));\n"
+          << "  typedef " << v4 << " v4;\n"
+          << "  __shared__ __align__(16) " << T << " st[" << o.RS << "];\n"
+          << "  const int g = blockIdx.x / " << o.TPC << ", kt = blockIdx.x - g * " << o.TPC << ";\n"
+          << "  const int nv_ = " << o.nvalid << ";\n"
+          << "  const int lo = g * " << o.C << ";\n"
+          << "  const int hc = lo + " << o.C << " < nv_ ? lo + " << o.C << " : nv_;\n"
+          << "  const int t0 = lo + kt * " << o.TILE << ";\n"
+          << "  if (t0 >= hc) return;  // a tile the partition never had: the whole workgroup leaves\n"
+          << "  const int hi = t0 + " << o.TILE << " < hc ? t0 + " << o.TILE << " : hc;\n"
+          << "  const unsigned short* const sl = (const unsigned short*)b" << o.slot << ";\n"
+          << "  " << T << "* const dst = b" << to << ";\n"
+          << "  u16x8 sv[" << VB << "];\n"
+          << "#pragma unroll\n"
+          << "  for (int u = 0; u < " << VB << "; u++) {\n"
+          << "    const int i = t0 + 8 * ((int)threadIdx.x + " << GT << " * u);\n"
+          << "    if (i + 8 <= hi) sv[u] = *(const u16x8*)(sl + i);\n"
+          << "    else sv[u] = (u16x8)(unsigned short)0xffffu;\n"
+          << "  }\n"
+          << "  const int tot = ((const int2*)b" << o.meta << ")[(size_t)" << o.PB * o.NTT << " + blockIdx.x].x;\n"
+          << "  const " << T << "* const rg = b" << from << " + (size_t)blockIdx.x * " << o.RS << ";\n"
+          << "  v4 ra[" << VR << "], rc[" << VR << "];\n"
+          << "#pragma unroll\n"
+          << "  for (int u = 0; u < " << VR << "; u++) {\n"
+          << "    const int s = 8 * ((int)threadIdx.x + " << GT << " * u);\n"
+          << "    if (s < tot) { ra[u] = *(const v4*)(rg + s); rc[u] = *(const v4*)(rg + s + 4); }\n"
+          << "  }\n"
+          << "#pragma unroll\n"
+          << "  for (int u = 0; u < " << VR << "; u++) {\n"
+          << "    const int s = 8 * ((int)threadIdx.x + " << GT << " * u);\n"
+          << "    if (s < tot) { *(v4*)(st + s) = ra[u]; *(v4*)(st + s + 4) = rc[u]; }\n"
+          << "  }\n"
+          << "  __syncthreads();\n";
+      } else {
       k << ") {\n"
         << "  typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));\n"
         << "  typedef " << v4 << " v4;\n"
@@ -2947,13 +3203,13 @@ struct Lowering {
         << "  u16x8 sv[" << VB << "];\n"
         << "#pragma unroll\n"
         << "  for (int u = 0; u < " << VB << "; u++) {\n"
-        << "    const int i = t0 + 8 * ((int)threadIdx.x + 256 * u);\n"
+        << "    const int i = t0 + 8 * ((int)threadIdx.x + " << GT << " * u);\n"
         << "    if (i + 8 <= hi) sv[u] = *(const u16x8*)(sl + i);\n"
         << "    else sv[u] = (u16x8)(unsigned short)0xffffu;\n"
         << "  }\n"
         << "  const int nk = meta[0];\n"
-        << "  for (int c = threadIdx.x; c <= nk; c += 256) mt[c] = meta[1 + c];\n"
-        << "  for (int c = threadIdx.x; c < nk; c += 256) mc[c] = meta[" << KM + 2 << " + c];\n"
+        << "  for (int c = threadIdx.x; c <= nk; c += " << GT << ") mt[c] = meta[1 + c];\n"
+        << "  for (int c = threadIdx.x; c < nk; c += " << GT << ") mc[c] = meta[" << KM + 2 << " + c];\n"
         << "  __syncthreads();\n"
         << "  const int tot = mt[nk];\n"
         // the tile's runs into LDS in its bucket-grouped order: slot s lies in
@@ -2989,11 +3245,12 @@ struct Lowering {
         << "    for (int u = 0; u < " << E << "; u++)\n"
         << "      if (sw + u * 64 + lane < tot) st[sw + u * 64 + lane] = v[u];\n"
         << "  }\n"
-        << "  __syncthreads();\n"
-        << "  bool bad = false;\n"
+        << "  __syncthreads();\n";
+      }
+      k << "  bool bad = false;\n"
         << "#pragma unroll\n"
         << "  for (int u = 0; u < " << VB << "; u++) {\n"
-        << "    const int i = t0 + 8 * ((int)threadIdx.x + 256 * u);\n"
+        << "    const int i = t0 + 8 * ((int)threadIdx.x + " << GT << " * u);\n"
         << "    if (i + 8 <= hi) {\n"
         << "      " << T << " x[8];\n"
         << "#pragma unroll\n"
@@ -3016,7 +3273,7 @@ struct Lowering {
       if (flag) k << "  if (bad) cc_flag(err, 1);\n";
       k << "}\n";
       src << k.str();
-      ks.push_back(add_kernel(kname + "_unpartition" + sfx, args, (int)(o.G * o.TPC), 256, "gather_unpartition"));
+      ks.push_back(add_kernel(kname + "_unpartition" + sfx, args, (int)(o.G * o.TPC), (int)GT, "gather_unpartition"));
     };
     if (gb.coarse.slot >= 0) {
       unpartition("2", f, f.val, gb.coarse.val, false);

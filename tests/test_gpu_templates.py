@@ -189,6 +189,9 @@ SCATTER_CASES = [
     (300001, 50000, F32, ["scatter_partition", "scatter_accumulate", "scatter_reduce"]),
     (300001, 50000, F64, ["scatter_partition", "scatter_accumulate", "scatter_reduce"]),
     (300001, 50001, I32, ["scatter_partition", "scatter_accumulate", "scatter_reduce"]),
+    # tile-local runs up to 256 slices, per-chunk offsets above
+    ((1 << 20) + 3, 256 * 8192, F32, ["scatter_partition", "scatter_accumulate", "scatter_reduce"]),
+    ((1 << 20) + 3, 256 * 8192 + 1, F32, ["scatter_count", "scatter_partition", "scatter_accumulate", "scatter_reduce"]),
     (1 << 20, (1 << 24) + 5, F32, ["scatter_partition", "scatter_accumulate"]),
     (1 << 20, 1 << 24, I32, ["scatter_partition", "scatter_accumulate"]),
 ]
@@ -224,6 +227,9 @@ GATHER_BACK_CASES = [
     ((1 << 22) + 3, 1 << 23, F32, True),
     ((1 << 21) + 11, (1 << 22) + 1, I32, True),
     ((1 << 20) + 1, 1 << 23, F64, True),
+    # three tiles a chunk, the last chunk one short tile (the partition marks
+    # the tiles past the end empty)
+    ((1 << 24) + 5, 1 << 20, F32, False),
 ]
 
 
@@ -405,6 +411,19 @@ KNOB_CASES = [
      lambda: [("x", data(I32, (3, 100001), 65))], "scan_lookback"),
     ("scatter_prefetch=0", lambda: scatter_graph(300001, 70000, F32),
      lambda: [("idx", scatter_idx(68, 300001, 70000)), ("src", data(F32, (300001,), 69))], "scatter_partition"),
+    # threads per workgroup of the partition, accumulate and gather-back
+    # kernels, away from their defaults (1024, 1024, 512), with gather back
+    ("scatter_part_threads=256,scatter_acc_threads=256,gather_threads=256",
+     lambda: C.scatter_gather(300001, 70000, F32),
+     lambda: [("idx", scatter_idx(81, 300001, 70000)), ("src", data(F32, (300001,), 82))], "gather_unpartition"),
+    # per-chunk offsets instead of tile-local runs, with gather back
+    ("scatter_local_max=0", lambda: C.scatter_gather((1 << 20) + 37, 1 << 16, F32),
+     lambda: [("idx", scatter_idx(85, (1 << 20) + 37, 1 << 16)), ("src", data(F32, ((1 << 20) + 37,), 86))],
+     "scatter_count"),
+    ("scatter_part_threads=512,scatter_acc_threads=512,gather_threads=1024",
+     lambda: C.scatter_gather((1 << 20) + 1, 1 << 22, F64),
+     lambda: [("idx", scatter_idx(83, (1 << 20) + 1, 1 << 22)), ("src", data(F64, ((1 << 20) + 1,), 84))],
+     "gather_unpartition"),
     # the look-back's own fold of a predecessor tile that has not published
     # (taken after lb_spin polls; one poll forces it on nearly every wait):
     # row-start tiles with a non-identity init, floats, many small tiles
