@@ -2266,11 +2266,11 @@ struct Lowering {
       if (part >= 0) ks.push_back(scatter_reduce(kname, T, acc, part, out, W, B, B));
       return ks;
     }
-    // Workgroups per slice, about 1024 in all: for 2^26 values into 2^20
-    // bins (128 slices, 8 each) that measures 0.937-0.940 ms a step
-    // against 0.954-0.955 ms with 16 each (accumulate 130 against 138 us,
-    // the fixed-order sum of the partial tables 11 against 17 us).
-    int64_t W = std::max<int64_t>(1, std::min<int64_t>(16, tune("scatter_slice_wgs", 1024) / P));
+    // Workgroups per slice, about 512 in all: for 2^26 values into 2^20
+    // bins (64 slices of 16384, 8 each) the accumulate takes 121 us and the
+    // fixed-order sum of the partial tables 11 us, against 132 and 17 us
+    // with 16 each.
+    int64_t W = std::max<int64_t>(1, std::min<int64_t>(16, tune("scatter_slice_wgs", 512) / P));
     while (W > 1 && W * P * S * ES > (int64_t(256) << 20)) W--;
     int part = finish(W, P, P * S);
     std::string sB = std::to_string(B);
@@ -2323,10 +2323,10 @@ struct Lowering {
       o.first = in.check;
       o.local = local;
       if (local) {
-        // regions of RS elements: the tile plus at most 7 of padding per
-        // bucket, rounded to a multiple of 8
+        // regions of RS elements: the tile (at most a chunk long) plus at
+        // most 7 of padding per bucket, rounded to a multiple of 8
         o.NTT = G * o.TPC;
-        o.RS = TILE + 8 * PB;
+        o.RS = std::min(TILE, C) + 8 * PB;
         o.key = add_buf("t" + id + "_key" + sfx, DT::I32, cdiv(o.NTT * o.RS, 2), BufRole::Scratch);  // 16-bit keys
         o.val = add_buf("t" + id + "_val" + sfx, n.dt, o.NTT * o.RS, BufRole::Scratch);
         o.meta = add_buf("t" + id + "_runs" + sfx, DT::I32, 2 * (PB + 1) * o.NTT, BufRole::Scratch);
@@ -2959,10 +2959,15 @@ struct Lowering {
     int64_t N = g.ts[n.a].numel;
     if (M > 0 && N > 0 && tune("scatter_lds", 1)) {
       const int64_t ES = dt_size(n.dt);
+      // Slices of 16384 bins where the table fits 64 KiB of LDS (8192 for
+      // 8-byte types): the longer a slice, the longer each tile's run of it
+      // (config 3, 2^20 bins: 640 -> 614 us against 8192). A table of 128
+      // KiB a workgroup (scatter_slice_lds=131072) is allowed too.
+      const int64_t lds = tune("scatter_slice_lds", 65536) == 131072 ? 131072 : 65536;
       int64_t S = 4096;
-      const int64_t want = tune("scatter_slice_bins", 8192);
-      while (S < want && S * 2 * ES <= 65536) S *= 2;
-      while (cdiv(M, S) > 4096 && S * ES < 65536) S *= 2;
+      const int64_t want = tune("scatter_slice_bins", 16384);
+      while (S < want && S * 2 * ES <= lds) S *= 2;
+      while (cdiv(M, S) > 4096 && S * ES < lds) S *= 2;
       int64_t P = cdiv(M, S);
       if (P == 1) return lower_scatter_lds(t, M, N, M, 1);
       if (P <= 4096) return lower_scatter_lds(t, M, N, S, P);

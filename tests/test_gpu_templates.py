@@ -190,8 +190,9 @@ SCATTER_CASES = [
     (300001, 50000, F64, ["scatter_partition", "scatter_accumulate", "scatter_reduce"]),
     (300001, 50001, I32, ["scatter_partition", "scatter_accumulate", "scatter_reduce"]),
     # tile-local runs up to 256 slices, per-chunk offsets above
-    ((1 << 20) + 3, 256 * 8192, F32, ["scatter_partition", "scatter_accumulate", "scatter_reduce"]),
-    ((1 << 20) + 3, 256 * 8192 + 1, F32, ["scatter_count", "scatter_partition", "scatter_accumulate", "scatter_reduce"]),
+    ((1 << 20) + 3, 256 * 16384, F32, ["scatter_partition", "scatter_accumulate", "scatter_reduce"]),
+    ((1 << 20) + 3, 256 * 16384 + 1, F32, ["scatter_count", "scatter_partition", "scatter_accumulate"]),
+    ((1 << 20) + 3, 256 * 8192 + 1, F64, ["scatter_count", "scatter_partition", "scatter_accumulate"]),
     (1 << 20, (1 << 24) + 5, F32, ["scatter_partition", "scatter_accumulate"]),
     (1 << 20, 1 << 24, I32, ["scatter_partition", "scatter_accumulate"]),
 ]
@@ -211,7 +212,7 @@ def test_scatter_permutation_two_level(device, dtype, tune, monkeypatch):
     super-slices, then the slice pass (or, with scatter_two_level=0, one
     pass with element-wise stores)."""
     monkeypatch.setenv("CCHIP_TUNE", tune)
-    n, bins = 1 << 22, 1 << 23
+    n, bins = 1 << 22, 1 << (23 if dtype is F64 else 24)
     g = scatter_graph(n, bins, dtype)
     t = templates(g)
     assert ("scatter_coarse" in t) == (tune == "")
@@ -224,12 +225,14 @@ GATHER_BACK_CASES = [
     ((1 << 20) + 37, 1 << 16, F32, False),
     (300001, 100003, I32, False),
     ((1 << 19) + 5, 1 << 17, F64, False),
-    ((1 << 22) + 3, 1 << 23, F32, True),
-    ((1 << 21) + 11, (1 << 22) + 1, I32, True),
+    ((1 << 22) + 3, 1 << 24, F32, True),
+    ((1 << 21) + 11, (1 << 24) + 1, I32, True),
     ((1 << 20) + 1, 1 << 23, F64, True),
     # three tiles a chunk, the last chunk one short tile (the partition marks
     # the tiles past the end empty)
     ((1 << 24) + 5, 1 << 20, F32, False),
+    # 301 slices: one level, per-chunk offsets (no tile-local runs)
+    ((1 << 21) + 7, 301 * 16384 - 5, F32, False),
 ]
 
 
@@ -385,7 +388,7 @@ KNOB_CASES = [
     ("mm_mfma=0", lambda: C.matmul(128, F32, k=64, m=128),
      lambda: [("a", data(F32, (128, 64), 49)), ("b", data(F32, (64, 128), 50))], "matmul_tiled"),
     ("map_nt=2", lambda: P.chain(5000).graph(), lambda: P.chain(5000).inputs(), "map"),
-    ("scatter_slice_bins=16384", lambda: scatter_graph(300001, 70000, F32),
+    ("scatter_slice_bins=8192", lambda: scatter_graph(300001, 70000, F32),
      lambda: [("idx", scatter_idx(51, 300001, 70000)), ("src", data(F32, (300001,), 52))], "scatter_partition"),
     ("rs_groups=512", lambda: C.rows(8192, 1000), lambda: [("x", data(F32, (8192, 1000), 77))], "scan_rowseq"),
     ("rs_bytes=8192,rs_groups=64", lambda: C.rows(1024, 3000),

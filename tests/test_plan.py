@@ -68,23 +68,24 @@ def test_barriers_are_materialised():
 
 
 def test_scatter_template_choice(monkeypatch):
-    """One slice (8192 bins by default): direct LDS fold; up to 256 slices:
-    a partition into tile-local runs, no count or offset passes; more (or
-    scatter_local_max=0): per-chunk counts, offsets, then the partition;
-    tables too large for the slice limit (or scatter_lds=0): global
-    atomics."""
-    def ks(n, bins):
-        i, s = D.param("i", I32, (n,)), D.param("s", F32, (n,))
+    """One slice (16384 bins by default, 8192 for 8-byte types): direct LDS
+    fold; up to 256 slices: a partition into tile-local runs, no count or
+    offset passes; more (or scatter_local_max=0): per-chunk counts, offsets,
+    then the partition; tables too large for the slice limit (or
+    scatter_lds=0): global atomics."""
+    def ks(n, bins, dt=F32):
+        i, s = D.param("i", I32, (n,)), D.param("s", dt, (n,))
         return [t for _, t in kernels_of(Graph.create("h", [("h", D.scatter_add(i, s, (bins,)))]))]
 
     assert ks(1000, 8192) == ["scatter_direct"]
-    assert ks(100000, 8192) == ["scatter_direct", "scatter_reduce"]
-    assert ks(100000, 8193) == ["scatter_partition", "scatter_accumulate", "scatter_reduce"]
-    assert ks(1 << 22, 256 * 8192) == ["scatter_partition", "scatter_accumulate", "scatter_reduce"]
-    assert ks(1 << 22, 256 * 8192 + 1)[:4] == ["scatter_count", "scatter_colscan", "scatter_bscan", "scatter_partition"]
+    assert ks(100000, 16384) == ["scatter_direct", "scatter_reduce"]
+    assert ks(100000, 8193, F64) == ["scatter_partition", "scatter_accumulate", "scatter_reduce"]
+    assert ks(100000, 16385) == ["scatter_partition", "scatter_accumulate", "scatter_reduce"]
+    assert ks(1 << 22, 256 * 16384) == ["scatter_partition", "scatter_accumulate", "scatter_reduce"]
+    assert ks(1 << 22, 256 * 16384 + 1)[:4] == ["scatter_count", "scatter_colscan", "scatter_bscan", "scatter_partition"]
     assert ks(1 << 22, 1 << 28) == ["scatter_zero", "scatter_atomic"]
     monkeypatch.setenv("CCHIP_TUNE", "scatter_local_max=0")
-    assert ks(100000, 8193)[:4] == ["scatter_count", "scatter_colscan", "scatter_bscan", "scatter_partition"]
+    assert ks(100000, 16385)[:4] == ["scatter_count", "scatter_colscan", "scatter_bscan", "scatter_partition"]
     monkeypatch.setenv("CCHIP_TUNE", "scatter_lds=0")
     assert ks(1000, 4096) == ["scatter_zero", "scatter_atomic"]
 
@@ -219,11 +220,11 @@ def test_algorithmic_bytes_per_kernel():
     assert b["map"] == 3 * 4 * n and b["reduce_split"] == 4 * n + 4
     b = _bytes(C.global_scan(n))
     assert b["scan_lookback"] == 8 * n and b["scan_init"] == 0
-    b = _bytes(C.scatter_gather(n, 1 << 14))
-    assert b["scatter_partition"] == 8 * n + 4 * (1 << 14)
+    b = _bytes(C.scatter_gather(n, 1 << 15))
+    assert b["scatter_partition"] == 8 * n + 4 * (1 << 15)
     assert b["scatter_accumulate"] == 0 and b["scatter_reduce"] == 0
     # the gather back: idx, the table (once), out, on its last kernel
-    assert b["gather_unpartition"] == 4 * n + 4 * (1 << 14) + 4 * n and b["gather_slices"] == 0
+    assert b["gather_unpartition"] == 4 * n + 4 * (1 << 15) + 4 * n and b["gather_slices"] == 0
     # the price reduces the gathered last column only, not the whole path matrix
     b = _bytes(C.mc_paths(4096, 64))
     assert b["reduce_split"] < 4 * 4096 + 64
