@@ -474,16 +474,21 @@ def kernel_table(H, w):
 
 
 def dominant(H, w, config, timed=True):
-    """The kernel that takes the most time per step (one timed step per
-    kernel, HIP events around its launches), or, without timing, the one
-    with the most algorithmic bytes (the matmul for matmul configs):
-    (name, role, bytes, compiled, table)."""
+    """Of the kernels that carry a root's algorithmic bytes, the one that
+    takes the most time per step (one timed step per kernel, HIP events
+    around its launches), or, without timing, the one with the most bytes
+    (the matmul for matmul configs): (name, role, bytes, compiled, table).
+    Helper kernels (a scatter's counts and accumulate, a split reduction's
+    fold) carry no bytes of their own, so no roofline can be put on them;
+    the profiles list their times."""
     kinfo = kernel_table(H, w)
     if timed:
         from cudacaml_amd.runtime import Device
 
         best, best_ms = None, -1.0
         for k, (role, b, c) in kinfo.items():
+            if b <= 0:
+                continue
             H.time_kernel(c, k)
             step(H, w)
             Device.synchronize()

@@ -945,6 +945,13 @@ struct Lowering {
     // length, 0}). No count or offset passes.
     bool local = false;
     int64_t RS = 0, NTT = 0;
+    // Windows (the slice pass of two levels, tile-local): a tile is a
+    // window of TILE elements of one super-slice's run in the coarse output
+    // (`wstart`: the coarse pass's super-slice starts, P1 of them), so its
+    // buckets are that super-slice's 64 slices; NTT bounds the windows.
+    bool windows = false;
+    int wstart = -1, wtab = -1;  // wtab: each super-slice's first window, and the total
+    int64_t P1 = 0;
     // per tile: K, the K + 1 tile-local starts of its non-empty buckets
     // (the last is the tile's total), their K run starts in the pair arrays
     int64_t kmax() const { return std::min(TILE, PB); }
@@ -957,6 +964,7 @@ struct Lowering {
     PassOut fin, coarse;
     int64_t S = 0, P = 0, B = 0, N = 0;
     int h = -1;
+    bool fused = false;  // the accumulate already put h[key] in the pairs
   };
   std::map<int, int> gbp_root_of;
   std::map<int, GatherBack> gather_back;
@@ -1200,7 +1208,7 @@ struct Lowering {
     }
     static const char *helpers[] = {"scan_init",          "scatter_zero",   "scatter_count",  "scatter_colscan",
                                     "scatter_bscan",      "scatter_accumulate", "scatter_reduce", "matmul_ksum",
-                                    "reduce_split_fold",  "scatter_coarse",     "gather_slices"};
+                                    "reduce_split_fold",  "scatter_coarse",     "gather_slices",  "scatter_windows"};
     int main = ks.back();
     for (int k : ks) {
       bool helper = false;
@@ -2140,21 +2148,55 @@ struct Lowering {
   // and flag error 2, as the atomic path does. Within a slice the order of
   // the additions depends on LDS arrival order, so float sums are not
   // bit-reproducible (the atomic path's are not either).
-  // The runs of slice q over tiles [t_lo, t_hi) of a tile-local partition (`o`),
-  // 8 elements a lane, two groups of 8 a lane in flight. Each wave takes 64
-  // tiles at a time: their run lengths in groups of 8 are summed across the
-  // wave, and a lane finds its group's tile by a binary search over those
-  // sums, so that consecutive lanes read consecutive groups. `loads` then
-  // `body` are emitted with pos_[u] (the group's first element) and nv_[u]
-  // (its valid elements; 0 for a lane without a group, whose pos_ still
-  // points into the pair arrays) for u = 0, 1 in scope.
-  static std::string runs_walk(const PassOut &o, int64_t threads, const std::string &loads, const std::string &body) {
+  // Emitted code: the windows of super-slice `Q` of a windowed pass are
+  // tiles [ta_, tz_).
+  static std::string windows_of(const PassOut &o, const std::string &Q) {
+    std::ostringstream l;
+    l << "  const int ta_ = b" << o.wtab << "[" << Q << "], tz_ = b" << o.wtab << "[" << Q << " + 1];\n";
+    return l.str();
+  }
+  // Emitted code: window `ft` of a windowed pass: its super-slice Q_ (the
+  // last whose first window is at or before ft, found in LDS), its first
+  // element wb_ and length wn_ in the coarse output. Has a barrier; the
+  // whole workgroup returns for a window past the last one.
+  static std::string window_at(const PassOut &o, const std::string &ft) {
+    std::ostringstream l;
+    l << "  __shared__ int wt_[" << o.P1 + 1 << "];\n"
+      << "  if (threadIdx.x <= " << o.P1 << ") wt_[threadIdx.x] = b" << o.wtab << "[threadIdx.x];\n"
+      << "  __syncthreads();\n"
+      << "  if (" << ft << " >= wt_[" << o.P1 << "]) return;\n"
+      << "  int Q_ = 0;\n"
+      << "#pragma unroll\n"
+      << "  for (int st = 32; st >= 1; st >>= 1)\n"
+      << "    if (Q_ + st < " << o.P1 << " && wt_[Q_ + st] <= " << ft << ") Q_ += st;\n"
+      << "  const int* const s1_ = b" << o.wstart << ";\n"
+      << "  const int wb_ = s1_[Q_] + (" << ft << " - wt_[Q_]) * " << o.TILE << ";\n"
+      << "  const int wn_ = s1_[Q_ + 1] - wb_ < " << o.TILE << " ? s1_[Q_ + 1] - wb_ : " << o.TILE << ";\n";
+    return l.str();
+  }
+
+  // The runs of slice q over tiles [t_lo, t_hi) of a tile-local partition
+  // (`o`), 8 elements a lane, two groups of 8 a lane in flight. Each wave
+  // takes `tpw` tiles at a time (64, or fewer where a workgroup is expected
+  // to have few tiles, so that every wave gets some): their run lengths in
+  // groups of 8 are summed across the wave, and a lane finds its group's
+  // tile by a binary search over those sums, so that consecutive lanes read
+  // consecutive groups. `loads` then `body` are emitted with pos_[u] (the
+  // group's first element) and nv_[u] (its valid elements; 0 for a lane
+  // without a group, whose pos_ still points into the pair arrays) for
+  // u = 0, 1 in scope.
+  static std::string runs_walk(const PassOut &o, int64_t threads, int64_t tiles_per_wg, const std::string &loads,
+                               const std::string &body) {
+    int64_t tpw = 64;
+    while (tpw > 1 && tpw * (threads / 64) > tiles_per_wg) tpw /= 2;
     std::ostringstream l;
     l << "  {\n"
-      << "    const int2* const runs_ = (const int2*)b" << o.meta << " + (size_t)q * " << o.NTT << ";\n"
+      << "    const int2* const runs_ = (const int2*)b" << o.meta << " + (size_t)" << (o.windows ? "(q & 63)" : "q")
+      << " * " << o.NTT << ";\n"
       << "    const int lane_ = threadIdx.x & 63;\n"
-      << "    for (int tb = t_lo + (int)(threadIdx.x >> 6) * 64; tb < t_hi; tb += " << threads << ") {\n"
-      << "      const int2 m_ = tb + lane_ < t_hi ? runs_[tb + lane_] : make_int2(0, 0);\n"
+      << "    for (int tb = t_lo + (int)(threadIdx.x >> 6) * " << tpw << "; tb < t_hi; tb += " << tpw * (threads / 64)
+      << ") {\n"
+      << "      const int2 m_ = lane_ < " << tpw << " && tb + lane_ < t_hi ? runs_[tb + lane_] : make_int2(0, 0);\n"
       << "      const int ng_ = (m_.y + 7) >> 3;\n"
       << "      int in_ = ng_;\n"
       << "#pragma unroll\n"
@@ -2761,6 +2803,120 @@ struct Lowering {
       return o;
     };
 
+    // The slice pass of two levels in windows (PassOut::windows): one
+    // workgroup per window of a super-slice's run in the coarse output,
+    // grouped by its 64 slices into the window's own region, as a
+    // tile-local pass does. No count or offset kernels.
+    auto pass_windows = [&](const PassOut &c1, int64_t P1, bool keep_slots) {
+      const int64_t TILE = 8192, NT = part_threads, E = TILE / NT;
+      PassOut o;
+      o.local = o.windows = true;
+      o.wstart = c1.start;
+      o.P1 = P1;
+      o.PB = 64;
+      o.TILE = TILE;
+      o.first = false;
+      o.NTT = cdiv(N, TILE) + P1;  // each super-slice adds at most one short window
+      o.RS = TILE + 8 * 64;
+      o.key = add_buf("t" + id + "_key", DT::I32, cdiv(o.NTT * o.RS, 2), BufRole::Scratch);  // 16-bit keys
+      o.val = add_buf("t" + id + "_val", n.dt, o.NTT * o.RS, BufRole::Scratch);
+      o.meta = add_buf("t" + id + "_runs", DT::I32, 2 * 65 * o.NTT, BufRole::Scratch);
+      if (keep_slots) o.slot = add_buf("t" + id + "_slot", DT::I32, cdiv(N, 2), BufRole::Scratch);
+      o.wtab = add_buf("t" + id + "_windows", DT::I32, P1 + 1, BufRole::Scratch);
+      {  // each super-slice's first window: one wave, a prefix of window counts
+        std::ostringstream k;
+        k << "extern \"C\" __global__ __launch_bounds__(64) void " << kname << "_windows(const int* __restrict__ b"
+          << c1.start << ", int* __restrict__ b" << o.wtab << ") {\n"
+          << "  const int Q = threadIdx.x;\n"
+          << "  const int nt = Q < " << P1 << " ? (b" << c1.start << "[Q + 1] - b" << c1.start << "[Q] + " << TILE - 1
+          << ") / " << TILE << " : 0;\n"
+          << "  int in = nt;\n"
+          << "#pragma unroll\n"
+          << "  for (int d = 1; d < 64; d <<= 1) {\n"
+          << "    const int o_ = __shfl_up(in, d);\n"
+          << "    if (Q >= d) in += o_;\n"
+          << "  }\n"
+          << "  if (Q < " << P1 << ") b" << o.wtab << "[Q] = in - nt;\n"
+          << "  if (Q == 63) b" << o.wtab << "[" << P1 << "] = in;\n"
+          << "}\n";
+        src << k.str();
+        ks.push_back(add_kernel(kname + "_windows", {c1.start, o.wtab}, 1, 64, "scatter_windows"));
+      }
+      std::vector<int> args = {c1.key, c1.val, c1.start, o.wtab, o.key, o.val, o.meta};
+      if (keep_slots) args.push_back(o.slot);
+      std::ostringstream k;
+      k << "extern \"C\" __global__ __launch_bounds__(" << NT << ") void " << kname << "_partition(const int* __restrict__ b"
+        << c1.key << ", const " << T << "* __restrict__ b" << c1.val << ", const int* __restrict__ b" << c1.start
+        << ", const int* __restrict__ b" << o.wtab << ", int* __restrict__ b" << o.key << ", " << T
+        << "* __restrict__ b" << o.val << ", int* __restrict__ b" << o.meta;
+      if (keep_slots) k << ", int* __restrict__ b" << o.slot;
+      k << ") {\n"
+        << "  __shared__ int tc[65];\n"
+        << "  __shared__ __align__(16) unsigned short sj[" << o.RS << "];\n"
+        << "  __shared__ __align__(16) " << T << " sx[" << o.RS << "];\n"
+        << "  int2* const runs = (int2*)b" << o.meta << ";\n"
+        << "  unsigned short* const keys = (unsigned short*)b" << o.key << ";\n"
+        << "  const int ft = blockIdx.x;\n"
+        << window_at(o, "ft")
+        << "  if (threadIdx.x < 64) tc[threadIdx.x] = 0;\n"
+        << "  int jj[" << E << "], rk[" << E << "];\n"
+        << "  " << T << " xv[" << E << "];\n"
+        << "#pragma unroll\n"
+        << "  for (int u = 0; u < " << E << "; u++) {\n"
+        << "    const int i = (int)threadIdx.x + u * " << NT << ";\n"
+        << "    jj[u] = i < wn_ ? b" << c1.key << "[wb_ + i] : -1;\n"
+        << "    xv[u] = i < wn_ ? b" << c1.val << "[wb_ + i] : " << zero_of(n.dt) << ";\n"
+        << "  }\n"
+        << "  __syncthreads();\n"
+        // the bin's slice within the super-slice (the coarse pass put only
+        // this super-slice's bins here)
+        << "#pragma unroll\n"
+        << "  for (int u = 0; u < " << E << "; u++) rk[u] = jj[u] >= 0 ? atomicAdd(&tc[(jj[u] >> " << shift
+        << ") & 63], 1) : 0;\n"
+        << "  __syncthreads();\n"
+        // one wave: runs padded to multiples of 8, their starts, and per
+        // slice {start, count}; row 64 the region's used length
+        << "  if (threadIdx.x < 64) {\n"
+        << "    const int c = tc[threadIdx.x], pc = (c + 7) & ~7;\n"
+        << "    int in = pc;\n"
+        << "#pragma unroll\n"
+        << "    for (int d = 1; d < 64; d <<= 1) {\n"
+        << "      const int o_ = __shfl_up(in, d);\n"
+        << "      if ((int)threadIdx.x >= d) in += o_;\n"
+        << "    }\n"
+        << "    tc[threadIdx.x] = in - pc;\n"
+        << "    runs[(size_t)threadIdx.x * " << o.NTT << " + ft] = make_int2(in - pc, c);\n"
+        << "    if (threadIdx.x == 63) {\n"
+        << "      tc[64] = in;\n"
+        << "      runs[(size_t)" << 64 * o.NTT << " + ft] = make_int2(in, 0);\n"
+        << "    }\n"
+        << "  }\n"
+        << "  __syncthreads();\n"
+        << "#pragma unroll\n"
+        << "  for (int u = 0; u < " << E << "; u++)\n"
+        << "    if (jj[u] >= 0) {\n"
+        << "      const int slot = tc[(jj[u] >> " << shift << ") & 63] + rk[u];\n";
+      if (keep_slots)
+        k << "      ((unsigned short*)b" << o.slot << ")[wb_ + (int)threadIdx.x + u * " << NT
+          << "] = (unsigned short)slot;\n";
+      k << "      sj[slot] = (unsigned short)(jj[u] & " << S - 1 << ");\n"
+        << "      sx[slot] = xv[u];\n"
+        << "    }\n"
+        << "  __syncthreads();\n"
+        << "  typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));\n"
+        << "  typedef __attribute__((ext_vector_type(4))) " << T << " v4;\n"
+        << "  const size_t rb = (size_t)ft * " << o.RS << ";\n"
+        << "  for (int s = 8 * (int)threadIdx.x; s < tc[64]; s += " << 8 * NT << ") {\n"
+        << "    *(u16x8*)(keys + rb + s) = *(const u16x8*)(sj + s);\n"
+        << "    *(v4*)(b" << o.val << " + rb + s) = *(const v4*)(sx + s);\n"
+        << "    *(v4*)(b" << o.val << " + rb + s + 4) = *(const v4*)(sx + s + 4);\n"
+        << "  }\n"
+        << "}\n";
+      src << k.str();
+      ks.push_back(add_kernel(kname + "_partition", args, (int)o.NTT, (int)NT, "scatter_partition"));
+      return o;
+    };
+
     PassIn first;
     add_in(first.p, fi);
     add_in(first.p, fs);
@@ -2802,6 +2958,10 @@ struct Lowering {
       const int64_t P1 = cdiv(P, 64);
       PassOut c1 = pass("1", first, shift + 6, P1, true, false, "scatter_coarse", keep, false);
       coarse = c1;
+      if (tune("scatter_windows", 1)) {
+        // the slice pass in windows of each super-slice's run
+        fin = pass_windows(c1, P1, keep);
+      } else {
       PassIn second;
       for (int b : {c1.key, c1.val, c1.start}) second.p.in.push_back(b);
       second.jx = [&, c1](const std::string &i) { return "b" + std::to_string(c1.key) + "[" + i + "]"; };
@@ -2820,6 +2980,7 @@ struct Lowering {
       second.nbuf = c1.start;
       second.check = false;
       fin = pass("", second, shift, P, true, true, "scatter_partition", keep, false);
+      }
     }
     if (keep && fin.slot >= 0) {
       GatherBack gb;
@@ -2842,10 +3003,17 @@ struct Lowering {
       const int64_t AT = tune("scatter_acc_threads", 1024) == 256 ? 256
                          : tune("scatter_acc_threads", 1024) == 512 ? 512 : 1024;
       const int lead = fin.local ? fin.meta : start;  // where the slice's pairs are found
+      // With one workgroup a slice its table is final in LDS at the end, so
+      // a gather back's slice step (each pair's value replaced by h at its
+      // bin) runs here, in a second walk over the same pairs.
+      const bool fuse_back = W == 1 && gather_back.count(t) > 0 && tune("scatter_fuse_back", 1) != 0;
+      if (fuse_back) gather_back[t].fused = true;
       std::ostringstream k;
       k << "extern \"C\" __global__ __launch_bounds__(" << AT << ") void " << kname << "_accumulate(const int* __restrict__ b"
-        << lead << ", const int* __restrict__ b" << key << ", const " << T << "* __restrict__ b" << val << ", " << T
-        << "* __restrict__ b" << dst << ") {\n"
+        << lead << ", const int* __restrict__ b" << key << ", " << (fuse_back ? "" : "const ") << T << "* __restrict__ b"
+        << val << ", " << T << "* __restrict__ b" << dst;
+      if (fin.windows) k << ", const int* __restrict__ b" << fin.wtab;
+      k << ") {\n"
         << "  __shared__ " << T << " h[" << S << "];\n"
         << "  const int q = blockIdx.x / " << W << ", w = blockIdx.x % " << W << ";\n"
         << "  for (int b = threadIdx.x; b < " << S << "; b += " << AT << ") h[b] = " << zero_of(n.dt) << ";\n"
@@ -2854,13 +3022,18 @@ struct Lowering {
         // the slice's runs in W shares of the tiles; a group's elements past
         // its run's count add +0 into bin 0 (see below)
         const std::string z = zero_of(n.dt);
-        k << "  const int t_lo = (int)((long long)" << fin.NTT << " * w / " << W << ");\n"
-          << "  const int t_hi = (int)((long long)" << fin.NTT << " * (w + 1) / " << W << ");\n"
-          << "  const unsigned short* const keys = (const unsigned short*)b" << key << ";\n"
+        if (fin.windows)  // the windows of the slice's super-slice
+          k << windows_of(fin, "(q >> 6)")
+            << "  const int t_lo = ta_ + (int)((long long)(tz_ - ta_) * w / " << W << ");\n"
+            << "  const int t_hi = ta_ + (int)((long long)(tz_ - ta_) * (w + 1) / " << W << ");\n";
+        else
+          k << "  const int t_lo = (int)((long long)" << fin.NTT << " * w / " << W << ");\n"
+            << "  const int t_hi = (int)((long long)" << fin.NTT << " * (w + 1) / " << W << ");\n";
+        k << "  const unsigned short* const keys = (const unsigned short*)b" << key << ";\n"
           << "  const " << T << "* const vals = b" << val << ";\n"
           << "  typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));\n"
           << "  typedef __attribute__((ext_vector_type(4))) " << T << " v4;\n"
-          << runs_walk(fin, AT,
+          << runs_walk(fin, AT, fin.windows ? cdiv(cdiv(N, fin.TILE), fin.P1) / W : fin.NTT / W,
                        "        u16x8 kv[2];\n"
                        "        v4 xa[2], xb[2];\n"
                        "#pragma unroll\n"
@@ -2877,6 +3050,21 @@ struct Lowering {
                        "            cc_lds_add(&h[in ? kv[u][e] : 0], in ? (e < 4 ? xa[u][e] : xb[u][e - 4]) : " + z + ");\n"
                        "          }\n")
           << "  __syncthreads();\n";
+        if (fuse_back)
+          k << "  " << T << "* const valw = b" << val << ";\n"
+            << runs_walk(fin, AT, fin.windows ? cdiv(cdiv(N, fin.TILE), fin.P1) / W : fin.NTT / W,
+                         "        u16x8 kv[2];\n"
+                         "#pragma unroll\n"
+                         "        for (int u = 0; u < 2; u++) kv[u] = *(const u16x8*)(keys + pos_[u]);\n",
+                         "#pragma unroll\n"
+                         "        for (int u = 0; u < 2; u++)\n"
+                         "          if (nv_[u] > 0) {\n"
+                         "            " + T + " x[8];\n"
+                         "#pragma unroll\n"
+                         "            for (int e = 0; e < 8; e++) x[e] = h[e < nv_[u] ? kv[u][e] : 0];\n"
+                         "            *(v4*)(valw + pos_[u]) = (v4){x[0], x[1], x[2], x[3]};\n"
+                         "            *(v4*)(valw + pos_[u] + 4) = (v4){x[4], x[5], x[6], x[7]};\n"
+                         "          }\n");
       } else {
       k << "  const int s0 = b" << start << "[q], len = b" << start << "[q + 1] - s0;\n"
         << "  const int lo = s0 + (int)((long long)len * w / " << W << ");\n"
@@ -2915,6 +3103,15 @@ struct Lowering {
         << "    }\n"
         << "  }\n"
         << "  __syncthreads();\n";
+      if (fuse_back)
+        k << "  " << T << "* const valw = b" << val << ";\n"
+          << "  for (int i = lo + (int)threadIdx.x; i < lo8; i += " << AT << ") valw[i] = h[keys[i]];\n"
+          << "  for (int i = hi8 + (int)threadIdx.x; i < hi; i += " << AT << ") valw[i] = h[keys[i]];\n"
+          << "  for (int j0 = lo8 + 8 * (int)threadIdx.x; j0 < hi8; j0 += " << 8 * AT << ") {\n"
+          << "    const u16x8 kv = *(const u16x8*)(keys + j0);\n"
+          << "    *(v4*)(valw + j0) = (v4){h[kv[0]], h[kv[1]], h[kv[2]], h[kv[3]]};\n"
+          << "    *(v4*)(valw + j0 + 4) = (v4){h[kv[4]], h[kv[5]], h[kv[6]], h[kv[7]]};\n"
+          << "  }\n";
       }
       if (part >= 0)
         k << "  for (int b = threadIdx.x; b < " << S << "; b += " << AT << ") b" << dst << "[(size_t)w * " << P * S
@@ -2925,7 +3122,9 @@ struct Lowering {
           << "  for (int b = threadIdx.x; b < nb; b += " << AT << ") b" << dst << "[(size_t)q * " << S << " + b] = h[b];\n";
       k << "}\n";
       src << k.str();
-      ks.push_back(add_kernel(kname + "_accumulate", {lead, key, val, dst}, (int)(P * W), (int)AT, "scatter_accumulate"));
+      std::vector<int> aargs = {lead, key, val, dst};
+      if (fin.windows) aargs.push_back(fin.wtab);
+      ks.push_back(add_kernel(kname + "_accumulate", aargs, (int)(P * W), (int)AT, "scatter_accumulate"));
     }
     if (part >= 0) ks.push_back(scatter_reduce(kname, T, acc, part, out, W, B, P * S));
     return ks;
@@ -3052,14 +3251,16 @@ struct Lowering {
     // 161 -> 131, unpartition passes 224 / 172 -> 168 / 143 us, against
     // 256; 1024 is in between); gather_threads=256 or 1024 for the others.
     const int64_t GT = tune("gather_threads", 512) == 256 ? 256 : tune("gather_threads", 512) == 1024 ? 1024 : 512;
-    {
+    if (!gb.fused) {  // (otherwise the accumulate did this step)
       const int64_t S = gb.S, B = gb.B;
       const int64_t Wg = std::max<int64_t>(1, std::min<int64_t>(16, 1024 / gb.P));
       const int lead = f.local ? f.meta : f.start;  // where each slice's pairs are found
       std::ostringstream k;
       k << "extern \"C\" __global__ __launch_bounds__(" << GT << ") void " << kname << "_slices(const int* __restrict__ b"
         << lead << ", const int* __restrict__ b" << f.key << ", const " << T << "* __restrict__ b" << gb.h << ", "
-        << T << "* __restrict__ b" << f.val << ") {\n"
+        << T << "* __restrict__ b" << f.val;
+      if (f.windows) k << ", const int* __restrict__ b" << f.wtab;
+      k << ") {\n"
         << "  typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));\n"
         << "  typedef " << v4 << " v4;\n"
         << "  __shared__ " << T << " tab[" << S << "];\n"
@@ -3079,11 +3280,16 @@ struct Lowering {
       if (f.local) {
         // the slice's runs in Wg shares of the tiles; a group's elements past
         // its run's count read bin 0 and land in the run's padding
-        k << "  const int t_lo = (int)((long long)" << f.NTT << " * w / " << Wg << ");\n"
-          << "  const int t_hi = (int)((long long)" << f.NTT << " * (w + 1) / " << Wg << ");\n"
-          << "  const unsigned short* const keys = (const unsigned short*)b" << f.key << ";\n"
+        if (f.windows)  // the windows of the slice's super-slice
+          k << windows_of(f, "(q >> 6)")
+            << "  const int t_lo = ta_ + (int)((long long)(tz_ - ta_) * w / " << Wg << ");\n"
+            << "  const int t_hi = ta_ + (int)((long long)(tz_ - ta_) * (w + 1) / " << Wg << ");\n";
+        else
+          k << "  const int t_lo = (int)((long long)" << f.NTT << " * w / " << Wg << ");\n"
+            << "  const int t_hi = (int)((long long)" << f.NTT << " * (w + 1) / " << Wg << ");\n";
+        k << "  const unsigned short* const keys = (const unsigned short*)b" << f.key << ";\n"
           << "  " << T << "* const vals = b" << f.val << ";\n"
-          << runs_walk(f, GT,
+          << runs_walk(f, GT, f.windows ? cdiv(cdiv(gb.N, f.TILE), f.P1) / Wg : f.NTT / Wg,
                        "        u16x8 kv[2];\n"
                        "#pragma unroll\n"
                        "        for (int u = 0; u < 2; u++) kv[u] = *(const u16x8*)(keys + pos_[u]);\n",
@@ -3127,8 +3333,9 @@ struct Lowering {
         << "}\n";
       }
       src << k.str();
-      ks.push_back(add_kernel(kname + "_slices", {lead, f.key, gb.h, f.val}, (int)(gb.P * Wg), (int)GT,
-                              "gather_slices"));
+      std::vector<int> sargs = {lead, f.key, gb.h, f.val};
+      if (f.windows) sargs.push_back(f.wtab);
+      ks.push_back(add_kernel(kname + "_slices", sargs, (int)(gb.P * Wg), (int)GT, "gather_slices"));
     }
     auto unpartition = [&](const std::string &sfx, const PassOut &o, int from, int to, bool flag) {
       std::vector<int> args = {o.meta, o.slot, from, to};
@@ -3140,6 +3347,11 @@ struct Lowering {
         k << ", const int* __restrict__ b" << o.nbuf;
         args.push_back(o.nbuf);
       }
+      if (o.windows) {
+        k << ", const int* __restrict__ b" << o.wstart << ", const int* __restrict__ b" << o.wtab;
+        args.push_back(o.wstart);
+        args.push_back(o.wtab);
+      }
       if (flag) {
         k << ", int* __restrict__ err";
         args.push_back(err_buf());
@@ -3147,6 +3359,47 @@ struct Lowering {
       const int64_t KM = o.kmax();
       const int64_t E = o.TILE / GT, VB = cdiv(o.TILE, 8 * GT);  // slots, 8-element groups per thread
       const std::string zero = zero_of(n.dt);
+      if (o.windows) {
+        // a window's region, read whole into LDS; each element of the
+        // window (contiguous in the coarse order, at any alignment) takes
+        // the value at its slot. Every element of a window has a slot.
+        const int64_t VR = cdiv(o.RS, 8 * GT);
+        k << ") {\n"
+          << "  typedef " << v4 << " v4;\n"
+          << "  __shared__ __align__(16) " << T << " st[" << o.RS << "];\n"
+          << "  const int ft = blockIdx.x;\n"
+          << window_at(o, "ft")
+          << "  const unsigned short* const sl = (const unsigned short*)b" << o.slot << ";\n"
+          << "  unsigned sv[" << E << "];\n"
+          << "#pragma unroll\n"
+          << "  for (int u = 0; u < " << E << "; u++) {\n"
+          << "    const int i = (int)threadIdx.x + u * " << GT << ";\n"
+          << "    sv[u] = i < wn_ ? sl[wb_ + i] : 0u;\n"
+          << "  }\n"
+          << "  const int tot = ((const int2*)b" << o.meta << ")[(size_t)" << 64 * o.NTT << " + ft].x;\n"
+          << "  const " << T << "* const rg = b" << from << " + (size_t)ft * " << o.RS << ";\n"
+          << "  v4 ra[" << VR << "], rc[" << VR << "];\n"
+          << "#pragma unroll\n"
+          << "  for (int u = 0; u < " << VR << "; u++) {\n"
+          << "    const int s = 8 * ((int)threadIdx.x + " << GT << " * u);\n"
+          << "    if (s < tot) { ra[u] = *(const v4*)(rg + s); rc[u] = *(const v4*)(rg + s + 4); }\n"
+          << "  }\n"
+          << "#pragma unroll\n"
+          << "  for (int u = 0; u < " << VR << "; u++) {\n"
+          << "    const int s = 8 * ((int)threadIdx.x + " << GT << " * u);\n"
+          << "    if (s < tot) { *(v4*)(st + s) = ra[u]; *(v4*)(st + s + 4) = rc[u]; }\n"
+          << "  }\n"
+          << "  __syncthreads();\n"
+          << "#pragma unroll\n"
+          << "  for (int u = 0; u < " << E << "; u++) {\n"
+          << "    const int i = (int)threadIdx.x + u * " << GT << ";\n"
+          << "    if (i < wn_) b" << to << "[wb_ + i] = st[sv[u]];\n"
+          << "  }\n"
+          << "}\n";
+        src << k.str();
+        ks.push_back(add_kernel(kname + "_unpartition" + sfx, args, (int)o.NTT, (int)GT, "gather_unpartition"));
+        return;
+      }
       if (o.local) {
         // the tile's region, read whole into LDS, then every element takes
         // the value at its slot
@@ -3287,7 +3540,7 @@ struct Lowering {
       unpartition("", f, f.val, out, true);
     }
     for (const PassOut *o : {&gb.fin, &gb.coarse})
-      for (int b : {o->start, o->key, o->val, o->slot, o->meta, o->nbuf})
+      for (int b : {o->start, o->key, o->val, o->slot, o->meta, o->nbuf, o->wtab})
         if (b >= 0) free_after[b] = r;
     return ks;
   }

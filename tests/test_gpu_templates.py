@@ -245,7 +245,12 @@ def test_gather_back_through_the_partition(device, n, bins, dtype, two, monkeypa
     the plain gather (scatter_gather_back=0), integers bit for bit."""
     g = C.scatter_gather(n, bins, dtype)
     t = templates(g)
-    assert t[-3 if two else -2:] == ["gather_slices"] + ["gather_unpartition"] * (2 if two else 1)
+    # the slice step is its own kernel, or (one workgroup a slice) part of
+    # the accumulate
+    back = t[t.index("scatter_accumulate") + 1:]
+    assert back in (["gather_unpartition"] * (2 if two else 1),
+                    ["scatter_reduce", "gather_slices"] + ["gather_unpartition"] * (2 if two else 1),
+                    ["gather_slices"] + ["gather_unpartition"] * (2 if two else 1)), t
     assert ("scatter_coarse" in t) == two
     if two:
         idx = C.permutation(31, bins)[:n].astype(np.int32)
@@ -303,6 +308,25 @@ def test_scatter_atomic_path(device, dtype, monkeypatch):
     n, bins = 100003, 50000
     check(scatter_graph(n, bins, dtype), [("idx", scatter_idx(5, n, bins)), ("src", data(dtype, (n,), 6))],
           ["scatter_zero", "scatter_atomic"])
+
+
+def test_scatter_two_level_empty_super_slices(device):
+    """Two levels with most super-slices empty and two crowded ones: the
+    slice pass's windows all fall in those two (one of them over many
+    windows), with a gather back."""
+    n, bins = (1 << 20) + 9, 1 << 24
+    r = np.random.default_rng(5)
+    idx = np.where(r.random(n) < 0.8, r.integers(0, 1 << 18, n), r.integers(bins - 1024, bins, n)).astype(np.int32)
+    g = C.scatter_gather(n, bins, F32)
+    assert "scatter_coarse" in templates(g)
+    inputs = [("idx", idx), ("src", data(F32, (n,), 9))]
+    check(g, inputs, ["gather_unpartition"])
+    c = H.compile(g)
+    try:
+        o = dict(H.run(c, inputs))
+    finally:
+        c.release()
+    np.testing.assert_array_equal(o["back"], o["h"][idx])
 
 
 @pytest.mark.parametrize("bins", [3000, 70000])
@@ -419,6 +443,18 @@ KNOB_CASES = [
     ("scatter_part_threads=256,scatter_acc_threads=256,gather_threads=256",
      lambda: C.scatter_gather(300001, 70000, F32),
      lambda: [("idx", scatter_idx(81, 300001, 70000)), ("src", data(F32, (300001,), 82))], "gather_unpartition"),
+    # the slice pass of two levels over counted chunks instead of windows
+    ("scatter_windows=0", lambda: C.scatter_gather((1 << 21) + 11, (1 << 24) + 1, F32),
+     lambda: [("idx", scatter_idx(87, (1 << 21) + 11, (1 << 24) + 1)), ("src", data(F32, ((1 << 21) + 11,), 88))],
+     "scatter_coarse"),
+    # the gather's slice step as its own kernel where one workgroup a slice
+    # could have done it (one level with counted chunks; two levels)
+    ("scatter_fuse_back=0", lambda: C.scatter_gather((1 << 21) + 7, 301 * 16384 - 5, F32),
+     lambda: [("idx", scatter_idx(89, (1 << 21) + 7, 301 * 16384 - 5)), ("src", data(F32, ((1 << 21) + 7,), 90))],
+     "gather_slices"),
+    ("scatter_fuse_back=0", lambda: C.scatter_gather((1 << 21) + 11, (1 << 24) + 1, I32),
+     lambda: [("idx", scatter_idx(91, (1 << 21) + 11, (1 << 24) + 1)), ("src", data(I32, ((1 << 21) + 11,), 92))],
+     "gather_slices"),
     # per-chunk offsets instead of tile-local runs, with gather back
     ("scatter_local_max=0", lambda: C.scatter_gather((1 << 20) + 37, 1 << 16, F32),
      lambda: [("idx", scatter_idx(85, (1 << 20) + 37, 1 << 16)), ("src", data(F32, ((1 << 20) + 37,), 86))],

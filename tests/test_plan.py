@@ -139,10 +139,13 @@ def test_config_plans():
     # slices, so the partition keeps each tile's pairs in the tile's region
     assert [t for _, t in kernels_of(C.scatter_gather())] == ["scatter_partition", "scatter_accumulate",
                                                                "scatter_reduce", "gather_slices", "gather_unpartition"]
-    # 2^26 bins: one workgroup per slice stores its table, no partials; two
-    # partition levels, undone level by level
+    # 2^26 bins: one workgroup per slice stores its table, no partials, and
+    # puts h[key] in the pairs itself (no slice kernel); two partition
+    # levels, the slice pass in windows of each super-slice's run, undone
+    # level by level
     perm = [t for _, t in kernels_of(C.scatter_gather(C.N3, C.N3))]
-    assert "scatter_reduce" not in perm and perm[-3:] == ["gather_slices", "gather_unpartition", "gather_unpartition"]
+    assert perm == ["scatter_count", "scatter_colscan", "scatter_bscan", "scatter_coarse", "scatter_windows",
+                    "scatter_partition", "scatter_accumulate", "gather_unpartition", "gather_unpartition"]
 
 
 def test_gather_back_only_over_the_same_index(monkeypatch):
@@ -228,3 +231,38 @@ def test_algorithmic_bytes_per_kernel():
     # the price reduces the gathered last column only, not the whole path matrix
     b = _bytes(C.mc_paths(4096, 64))
     assert b["reduce_split"] < 4 * 4096 + 64
+
+
+def _launch_uses_live_buffers(g):
+    """Every buffer a launched kernel takes is allocated before the launch
+    and freed only after the last launch that takes it."""
+    lines = [l.split() for l in H.plan(g).splitlines()]
+    names = {}
+    kargs = {}
+    for f in lines:
+        if f[0] == "buffer":
+            names[f[1]] = f[2]
+        elif f[0] == "kernel":
+            kargs[f[1]] = [names[a] for a in f[f.index("args") + 1:]]
+    live = set()
+    for f in lines:
+        if f[0] == "alloc":
+            live.add(f[1])
+        elif f[0] == "free":
+            live.discard(f[1])
+        elif f[0] == "launch":
+            dead = [b for b in kargs[f[1]] if b not in live and b != "err"]
+            assert not dead, (g.name, f[1], dead)
+
+
+@pytest.mark.parametrize("build", [
+    lambda: C.rows(), lambda: C.global_scan(), lambda: C.scatter_gather(), lambda: C.scatter_gather(C.N3, C.N3),
+    lambda: C.scatter_gather((1 << 20) + 3, 300 * 16384), lambda: C.scatter_gather(1 << 20, 1 << 16, F64),
+    lambda: C.mc_greeks(4096, 64), lambda: C.matmul_grad(256), lambda: sx.program(1 << 20, 2.0),
+])
+@pytest.mark.parametrize("tune", ["", "scatter_windows=0", "scatter_local_max=0"])
+def test_plan_launches_only_live_buffers(monkeypatch, build, tune):
+    """Scratch shared between roots (a gather back reads the scatter's
+    partition, window table included) stays allocated until its last use."""
+    monkeypatch.setenv("CCHIP_TUNE", tune)
+    _launch_uses_live_buffers(build())
