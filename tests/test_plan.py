@@ -6,6 +6,7 @@ spellings, and that generated modules compile for gfx950 with hiprtc.
 Mirrors test_fusion.ml, test_lower.ml, test_multikernel.ml, test_emit.ml,
 test_scatter.ml:50-70 and test_matmul.ml:105-139."""
 
+import numpy as np
 import pytest
 
 from cudacaml_amd import backend_hip as H
@@ -266,3 +267,17 @@ def test_plan_launches_only_live_buffers(monkeypatch, build, tune):
     partition, window table included) stays allocated until its last use."""
     monkeypatch.setenv("CCHIP_TUNE", tune)
     _launch_uses_live_buffers(build())
+
+
+def test_plan_liveness_over_random_scatter_shapes(monkeypatch):
+    """Scatter/gather-back plans over random sizes, bin counts, dtypes and
+    layout knobs (direct, tile-local, counted, two levels in windows or
+    counted, fused slice step or not) launch only live buffers."""
+    r = np.random.default_rng(11)
+    for case in range(60):
+        n = int(r.integers(1, 1 << 24))
+        bins = int(2 ** r.uniform(0, 26.5)) + int(r.integers(0, 3))
+        dt = [F32, F64, I32][case % 3]
+        tune = ["", "scatter_windows=0", "scatter_fuse_back=0", "scatter_local_max=0", "scatter_two_level=0"][case % 5]
+        monkeypatch.setenv("CCHIP_TUNE", tune)
+        _launch_uses_live_buffers(C.scatter_gather(n, bins, dt))
