@@ -2997,11 +2997,16 @@ struct Lowering {
     {  // accumulate
       int dst = part >= 0 ? part : out;
       // Threads per workgroup: the LDS table caps the workgroups per CU, so
-      // more threads keep more loads in flight. 1024 (config 3 123 -> 117
-      // us, config 3b 167 -> 154 us, against 256); scatter_acc_threads=256
-      // or 512 for the others.
-      const int64_t AT = tune("scatter_acc_threads", 1024) == 256 ? 256
-                         : tune("scatter_acc_threads", 1024) == 512 ? 512 : 1024;
+      // more threads keep more loads in flight. 1024 where a slice has
+      // several workgroups (config 3: 0.545 ms a step against 0.552 with
+      // 512), 512 where it has one, whose workgroups are short (config 3b:
+      // 1.071 against 1.104 ms); scatter_acc_threads=256, 512 or 1024
+      // forces one.
+      const int64_t at_default = W == 1 ? 512 : 1024;
+      const int64_t AT = tune("scatter_acc_threads", at_default) == 256    ? 256
+                         : tune("scatter_acc_threads", at_default) == 512  ? 512
+                         : tune("scatter_acc_threads", at_default) == 1024 ? 1024
+                                                                           : at_default;
       const int lead = fin.local ? fin.meta : start;  // where the slice's pairs are found
       // With one workgroup a slice its table is final in LDS at the end, so
       // a gather back's slice step (each pair's value replaced by h at its

@@ -439,7 +439,8 @@ KNOB_CASES = [
     ("scatter_prefetch=0", lambda: scatter_graph(300001, 70000, F32),
      lambda: [("idx", scatter_idx(68, 300001, 70000)), ("src", data(F32, (300001,), 69))], "scatter_partition"),
     # threads per workgroup of the partition, accumulate and gather-back
-    # kernels, away from their defaults (1024, 1024, 512), with gather back
+    # kernels, away from their defaults (1024; 1024, or 512 with one
+    # workgroup a slice; 512), with gather back
     ("scatter_part_threads=256,scatter_acc_threads=256,gather_threads=256",
      lambda: C.scatter_gather(300001, 70000, F32),
      lambda: [("idx", scatter_idx(81, 300001, 70000)), ("src", data(F32, (300001,), 82))], "gather_unpartition"),
@@ -459,7 +460,7 @@ KNOB_CASES = [
     ("scatter_local_max=0", lambda: C.scatter_gather((1 << 20) + 37, 1 << 16, F32),
      lambda: [("idx", scatter_idx(85, (1 << 20) + 37, 1 << 16)), ("src", data(F32, ((1 << 20) + 37,), 86))],
      "scatter_count"),
-    ("scatter_part_threads=512,scatter_acc_threads=512,gather_threads=1024",
+    ("scatter_part_threads=512,scatter_acc_threads=1024,gather_threads=1024",
      lambda: C.scatter_gather((1 << 20) + 1, 1 << 22, F64),
      lambda: [("idx", scatter_idx(83, (1 << 20) + 1, 1 << 22)), ("src", data(F64, ((1 << 20) + 1,), 84))],
      "gather_unpartition"),
