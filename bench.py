@@ -11,7 +11,10 @@ preallocated, no host traffic). ``value`` is algorithmic bytes per second
 over the K timed steps (each materialised input read once, each output
 written once, per kernel of the plan). Other configs (``--config saxpy``,
 ``chain``, ``scatter``, ``scatter_perm``, ``matmul``, ``matmul64``, ``matmul_grad``,
-``mc``, ``mc64``, ``mc_greeks``) print their own line in the same format.
+``mc``, ``mc64``, ``mc_greeks``) print their own line in the same format;
+``saxpy_hbm`` and ``chain_hbm`` run config 1's graphs over 2^28 elements,
+whose inputs cannot stay in the 256 MB MALL between steps (config 1's
+2^24 ones do), for the map template's HBM-only rate.
 ``poly`` and ``poly64`` are the reference benchmark's own workload
 (bench/bench.ml): the degree-64 Horner chain plus its sum over 2^24
 elements; their ``value`` is GFLOP/s with the input resident, and their
@@ -118,15 +121,19 @@ def build_workload(name, H, C):
         x = device_inputs(H, C.gen_uniform_pm1((1 << 28,)), 1)
         add(Graph.create("copy", [("r", Dsl.map(lambda e: e, Dsl.param("x", F32, (1 << 28,))))]), [("x", x)])
         return Workload(name, progs, "GB/s", "f32", "calibration: copy of f32[2^28]")
-    if name in ("saxpy", "chain"):
-        x = device_inputs(H, C.gen_uniform_pm1((C.N1,)), 1)
-        if name == "saxpy":
-            y = device_inputs(H, C.gen_uniform_pm1((C.N1,)), 2)
-            add(C.saxpy(), [("x", x), ("y", y)])
-            desc = "config1: saxpy r=2x+y, s=sum r over f32[2^24]"
+    if name in ("saxpy", "chain", "saxpy_hbm", "chain_hbm"):
+        # the _hbm variants: the same graphs over 2^28 elements, whose 1-2
+        # GiB inputs cannot stay in the 256 MB MALL between steps
+        n = (1 << 28) if name.endswith("_hbm") else C.N1
+        what = "2^28 (beyond the MALL)" if name.endswith("_hbm") else "2^24"
+        x = device_inputs(H, C.gen_uniform_pm1((n,)), 1)
+        if name.startswith("saxpy"):
+            y = device_inputs(H, C.gen_uniform_pm1((n,)), 2)
+            add(C.saxpy(n), [("x", x), ("y", y)])
+            desc = "config1: saxpy r=2x+y, s=sum r over f32[%s]" % what
         else:
-            add(C.chain(), [("x", x)])
-            desc = "config1b: 5-map chain over f32[2^24], one fused kernel"
+            add(C.chain(n), [("x", x)])
+            desc = "config1b: 5-map chain over f32[%s], one fused kernel" % what
         return Workload(name, progs, "GB/s", "f32", desc)
     if name in ("scatter", "scatter_perm"):
         src = device_inputs(H, C.gen_uniform_pm1((C.N3,)), 5)
@@ -286,6 +293,14 @@ def cpu_baseline(name, C, H, w):
         secs = timed(C.rows(), [("x", x)]) + timed(C.global_scan(), [("v", v)])
         nbytes = plan_total(C.rows()) + plan_total(C.global_scan())
         return nbytes / secs / 1e9, "GB/s", "the whole workload: rows graph on f32[8192,8192] + global scan on i32[2^28]", secs
+    if name in ("saxpy_hbm", "chain_hbm"):
+        # the oracle's rate does not depend on the length: time the 2^24
+        # graph on the leading 2^24 elements of the same inputs
+        n = C.N1
+        g = C.saxpy(n) if name.startswith("saxpy") else C.chain(n)
+        ins = [(k, v[:n]) for k, v in host_inputs(0)]
+        secs = timed(g, ins)
+        return plan_total(g) / secs / 1e9, "GB/s", "the graph on the first 2^24 of the 2^28 elements", secs
     if name in ("saxpy", "chain", "scatter", "scatter_perm"):
         g, ins = w.programs[0][0], host_inputs(0)
         secs = timed(g, ins)
