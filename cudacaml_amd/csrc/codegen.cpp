@@ -3153,6 +3153,57 @@ struct Lowering {
                       "scatter_reduce");
   }
 
+  // An i32 tensor that is exactly a*i + b in its flat element index i:
+  // integer +, - and * by a constant over iota, the map's element index and
+  // constants, through maps and reshapes. Wrapping i32 arithmetic agrees
+  // with the exact value modulo 2^32, so where the exact value lies in
+  // [0, 2^31) it is the value the reference computes.
+  struct Aff {
+    bool ok = false;
+    int64_t a = 0, b = 0;
+  };
+  static bool aff_small(int64_t v) { return v > -(int64_t(1) << 40) && v < (int64_t(1) << 40); }
+  Aff aff_x(int x, const std::vector<Aff> &args) const {
+    const XNode &e = g.xs[x];
+    if (e.dt != DT::I32) return {};
+    switch (e.kind) {
+      case XK::Const: return {true, 0, e.i};
+      case XK::Arg: return e.arg < (int)args.size() ? args[e.arg] : Aff{};
+      case XK::Index: return {true, 1, 0};
+      case XK::Bin: {
+        const Aff l = aff_x(e.a, args), r = aff_x(e.b, args);
+        if (!l.ok || !r.ok) return {};
+        Aff o;
+        o.ok = true;
+        if (e.op == B_ADD) {
+          o.a = l.a + r.a;
+          o.b = l.b + r.b;
+        } else if (e.op == B_SUB) {
+          o.a = l.a - r.a;
+          o.b = l.b - r.b;
+        } else if (e.op == B_MUL && (l.a == 0 || r.a == 0)) {
+          const Aff &c = l.a == 0 ? l : r, &v = l.a == 0 ? r : l;
+          if (__builtin_mul_overflow(c.b, v.a, &o.a) || __builtin_mul_overflow(c.b, v.b, &o.b)) return {};
+        } else {
+          return {};
+        }
+        return aff_small(o.a) && aff_small(o.b) ? o : Aff{};
+      }
+      default: return {};
+    }
+  }
+  Aff aff_t(int t) const {
+    const TNode &n = g.ts[t];
+    if (n.dt != DT::I32) return {};
+    switch (n.kind) {
+      case TK::Iota: return {true, 1, 0};
+      case TK::Reshape: return aff_t(n.a);
+      case TK::Map: return aff_x(n.body, {aff_t(n.a)});
+      case TK::Map2: return aff_x(n.body, {aff_t(n.a), aff_t(n.b)});
+      default: return {};
+    }
+  }
+
   std::vector<int> lower_scatter(int t) {
     const TNode &n = g.ts[t];
     std::string id = std::to_string(n.id);
@@ -3161,6 +3212,16 @@ struct Lowering {
     int out = buf_of[t];
     int64_t M = n.numel;
     int64_t N = g.ts[n.a].numel;
+    // An index a*i + b with a != 0 and every value in range hits each bin
+    // at most once (the adjoint of a strided gather, such as the last
+    // column of the path matrix): then each bin is 0 + its one source
+    // value or 0, written by one pass over the bins, with no atomics and no
+    // partition (scatter_affine=0 turns this off).
+    const Aff ia = aff_t(n.a);
+    if (ia.ok && ia.a != 0 && M > 0 && N > 0 && tune("scatter_affine", 1)) {
+      const __int128 e0 = ia.b, e1 = (__int128)ia.a * (N - 1) + ia.b;
+      if (std::min(e0, e1) >= 0 && std::max(e0, e1) < M) return lower_scatter_affine(t, ia.a, ia.b);
+    }
     if (M > 0 && N > 0 && tune("scatter_lds", 1)) {
       const int64_t ES = dt_size(n.dt);
       // Slices of 16384 bins where the table fits 64 KiB of LDS (8192 for
@@ -3224,6 +3285,52 @@ struct Lowering {
     int64_t nvec = std::max<int64_t>(1, N / 4);
     ks.push_back(add_kernel(kname, args, (int)std::min<int64_t>(cdiv(nvec, 256), 65536), 256, "scatter_atomic"));
     return ks;
+  }
+
+  // scatter_add with an injective affine index (see lower_scatter): one
+  // grid-stride pass over the bins, four a thread, each bin j taking
+  // 0 + src((j - b) / a) where a divides j - b and the quotient is a source
+  // index, else 0.
+  std::vector<int> lower_scatter_affine(int t, int64_t A, int64_t Bc) {
+    const TNode &n = g.ts[t];
+    const std::string id = std::to_string(n.id), kname = "k_" + id, T = dt_ctype(n.dt);
+    const int out = buf_of[t];
+    const int64_t M = n.numel, N = g.ts[n.a].numel;
+    ElemFn fs = gen.element_fn("fs_" + id, n.b, false, true);
+    src << fs.code;
+    Params p;
+    add_in(p, fs);
+    p.out.push_back(out);
+    std::vector<int> args;
+    std::string params = param_list(p, args);
+    const bool wide = M > INT32_MAX - 4 || Bc > INT32_MAX || Bc < INT32_MIN || A > INT32_MAX || A < INT32_MIN;
+    const std::string I = wide ? "long long" : "int";
+    const std::string z = zero_of(n.dt);
+    std::ostringstream k;
+    k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_affine(" << params << ") {\n"
+      << "  for (" << I << " j0 = 4 * ((" << I << ")blockIdx.x * 256 + threadIdx.x); j0 < " << M << "; j0 += 4 * ("
+      << I << ")gridDim.x * 256) {\n"
+      << "    " << T << " v[4];\n"
+      << "#pragma unroll\n"
+      << "    for (int u = 0; u < 4; u++) {\n"
+      << "      const " << I << " q = j0 + u - (" << Bc << ");\n"
+      << "      v[u] = " << z << ";\n"
+      << "      if (q % (" << A << ") == 0) {\n"
+      << "        const " << I << " i = q / (" << A << ");\n"
+      << "        if (i >= 0 && i < " << N << ") v[u] = " << z << " + " << fs.call_scalar("(int)i") << ";\n"
+      << "      }\n"
+      << "    }\n"
+      << "    if (j0 + 4 <= " << M << ") {\n"
+      << "      *(__attribute__((ext_vector_type(4))) " << T << "*)(b" << out << " + j0) = (__attribute__((ext_vector_type(4))) "
+      << T << "){v[0], v[1], v[2], v[3]};\n"
+      << "    } else {\n"
+      << "      for (int u = 0; j0 + u < " << M << "; u++) b" << out << "[j0 + u] = v[u];\n"
+      << "    }\n"
+      << "  }\n"
+      << "}\n";
+    src << k.str();
+    return {add_kernel(kname + "_affine", args, (int)std::min<int64_t>(cdiv(cdiv(M, 4), 256), 65536), 256,
+                       "scatter_affine")};
   }
 
   // ---- Gather back through a scatter's partition ----------------------------

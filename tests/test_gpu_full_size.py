@@ -233,12 +233,13 @@ def check_pathwise(o, zsum, steps, tol):
 
 def test_config5_greeks_f64_full_size_pathwise(device):
     """The benchmark's f64 graph at 2^22 paths x 64 steps (its gather
-    adjoint takes the zero-fill + hardware-atomic scatter into 2^28 bins)
-    against the pathwise estimator on the same Philox draws, within 1e-9
-    relative (summation order is the only difference)."""
+    adjoint, a scatter into 2^28 bins through the strided index p*64 + 63,
+    is one pass over the bins) against the pathwise estimator on the same
+    Philox draws, within 1e-9 relative (summation order is the only
+    difference)."""
     n, steps = C.PATHS5, C.STEPS5
     g = C.mc_greeks(n, steps, F64)
-    assert {"scatter_zero", "scatter_atomic", "scan_rowseq", "reduce_rowseq"} <= set(roles(g))
+    assert {"scatter_affine", "scan_rowseq", "reduce_rowseq"} <= set(roles(g))
     o = run_dev(g, bs.inputs(F64, seed=7))
     zg = Graph.create("z", [("z", rng.normal(F64, D.scalar("seed", I32), (n, steps)))])
     z = run_dev(zg, [("seed", np.array(7, np.int32))])["z"]
@@ -310,18 +311,23 @@ def test_config5_greeks_f32_full_size(device):
     zf = gen(C.gen_normals((n, steps), F32), 7)
     assert np.isfinite(zf).all()
     g = bs.call_paths_greeks(n, steps, F32, draws=D.param("z", F32, (n, steps)))
-    assert {"scatter_zero", "scatter_atomic", "scan_rowseq", "reduce_rowseq"} <= set(roles(g))
+    assert {"scatter_affine", "scan_rowseq", "reduce_rowseq"} <= set(roles(g))
     o = run_dev(g, [x for x in bs.inputs(F32) if x[0] != "seed"] + [("z", zf)])
     zsum = zf.sum(axis=1, dtype=np.float64)
     del zf
     check_pathwise(o, zsum, steps, 1e-4)
 
 
-def test_gather_adjoint_default_atomic_scatter(device):
-    """The default path of a scatter_add whose table exceeds the LDS slice
-    limit (4096 slices of 16384 f32 bins): the adjoint of picking the last
-    column of an f32[2^20 + 8; 64] by a gather, as the path pricer does,
-    through scatter_zero + scatter_atomic, against the oracle."""
+@pytest.mark.parametrize("tune,tpl", [("", {"scatter_affine"}),
+                                      ("scatter_affine=0", {"scatter_zero", "scatter_atomic"})])
+def test_gather_adjoint_of_the_last_column(device, monkeypatch, tune, tpl):
+    """The adjoint of picking the last column of an f32[2^20 + 8; 64] by a
+    gather, as the path pricer does: a scatter_add into 2^26 bins through
+    the index p*64 + 63, one pass over the bins by default (the index is
+    affine and in range, so each bin takes at most one value), or (with
+    scatter_affine=0) the path for tables beyond the LDS slice limit,
+    scatter_zero + scatter_atomic; against the oracle."""
+    monkeypatch.setenv("CCHIP_TUNE", tune)
     rows, steps = (1 << 20) + 8, 64
     x = D.param("x", F32, (rows, steps))
     idx = D.map(lambda p: D.add(D.mul(p, D.const(I32, steps)), D.const(I32, steps - 1)), D.iota((rows,)))
@@ -329,7 +335,7 @@ def test_gather_adjoint_default_atomic_scatter(device):
     payoff = D.map(lambda s: D.mul(s, D.max(D.sub(s, D.const(F32, 0.25)), D.const(F32, 0.0))), st)
     loss = D.reduce(D.add, D.const(F32, 0.0), payoff)
     g = G.grad(Graph.create("pick", [("loss", loss)]), "loss", ["x"])
-    assert {"scatter_zero", "scatter_atomic"} <= set(roles(g))
+    assert tpl <= set(roles(g))
     xv = np.random.default_rng(3).uniform(-1, 1, (rows, steps)).astype(np.float32)
     exp = oracle.run(g, [("x", xv)])
     got = run_dev(g, [("x", xv)])

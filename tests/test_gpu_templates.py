@@ -310,6 +310,46 @@ def test_scatter_atomic_path(device, dtype, monkeypatch):
           ["scatter_zero", "scatter_atomic"])
 
 
+@pytest.mark.parametrize("dtype", [F32, F64, I32])
+def test_scatter_affine_index(device, dtype):
+    """scatter_add through an index a*i + b built from iota (a strided,
+    reversed, offset index; also through a reshape): one pass over the bins,
+    bit-exact against the oracle, including each hit bin's 0 + x (a -0.0
+    source lands as +0.0) and NaN/inf sources; an affine index that leaves
+    the range takes the general path and raises."""
+    n = 300007
+    for a, b, m in [(3, 1, 3 * n + 5), (-2, 2 * n + 7, 2 * n + 9), (1, 0, n), (64, 63, 64 * n)]:
+        idx = D.map(lambda p: D.add(D.mul(p, D.const(I32, a)), D.const(I32, b)), D.iota((n,)))
+        src = D.param("src", dtype, (n,))
+        g = Graph.create("aff", [("h", D.scatter_add(idx, src, (m,)))])
+        assert templates(g) == ["scatter_affine"], (a, b, templates(g))
+        x = data(dtype, (n,), 21)
+        if dtype is not I32:
+            x[:8] = [-0.0, np.nan, np.inf, -np.inf, 0.0, -1.5, 2.5, -0.0]
+        exp = oracle.run(g, [("src", x)])
+        c = H.compile(g)
+        try:
+            got = H.run(c, [("src", x)])
+        finally:
+            c.release()
+        np.testing.assert_array_equal(got[0][1].view(np.uint8), exp[0][1].view(np.uint8))
+    # through a reshape of a 2-d iota
+    idx = D.reshape((7007,), D.map(lambda p: D.sub(D.mul(p, D.const(I32, 2)), D.const(I32, -5)), D.iota((7, 1001))))
+    g = Graph.create("aff2", [("h", D.scatter_add(idx, D.param("src", dtype, (7007,)), (2 * 7007 + 5,)))])
+    assert templates(g) == ["scatter_affine"]
+    check(g, [("src", data(dtype, (7007,), 22))], ["scatter_affine"])
+    # out of range: the general path, which raises
+    idx = D.map(lambda p: D.mul(p, D.const(I32, 2)), D.iota((1000,)))
+    g = Graph.create("aff3", [("h", D.scatter_add(idx, D.param("src", dtype, (1000,)), (1500,)))])
+    assert "scatter_affine" not in templates(g)
+    c = H.compile(g)
+    try:
+        with pytest.raises(ValueError, match="scatter_add index out of bounds"):
+            H.run(c, [("src", data(dtype, (1000,), 23))])
+    finally:
+        c.release()
+
+
 def test_scatter_two_level_empty_super_slices(device):
     """Two levels with most super-slices empty and two crowded ones: the
     slice pass's windows all fall in those two (one of them over many
