@@ -3320,10 +3320,14 @@ struct Lowering {
       << "        if (i >= 0 && i < " << N << ") v[u] = " << z << " + " << fs.call_scalar("(int)i") << ";\n"
       << "      }\n"
       << "    }\n"
-      << "    if (j0 + 4 <= " << M << ") {\n"
-      << "      *(__attribute__((ext_vector_type(4))) " << T << "*)(b" << out << " + j0) = (__attribute__((ext_vector_type(4))) "
-      << T << "){v[0], v[1], v[2], v[3]};\n"
-      << "    } else {\n"
+      << "    if (j0 + 4 <= " << M << ") {\n";
+    // streamed past the caches where the table is larger than the MALL
+    if (streams(M * dt_size(n.dt)))
+      k << "      cc_st4_nt(b" << out << " + j0, cc_v4<" << T << ">{v[0], v[1], v[2], v[3]});\n";
+    else
+      k << "      *(__attribute__((ext_vector_type(4))) " << T << "*)(b" << out
+        << " + j0) = (__attribute__((ext_vector_type(4))) " << T << "){v[0], v[1], v[2], v[3]};\n";
+    k << "    } else {\n"
       << "      for (int u = 0; j0 + u < " << M << "; u++) b" << out << "[j0 + u] = v[u];\n"
       << "    }\n"
       << "  }\n"
