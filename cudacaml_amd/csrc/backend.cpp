@@ -534,6 +534,7 @@ int cchip_backend_compile(const char *graph, int device, int streams, cchip_prog
             e.bufs[b] = e.arena + e.off[b];
             continue;
           }
+          if (p->ir.bufs[b].elided) continue;  // no kernel reads or writes it
           e.bufs[b] = rt_alloc((size_t)p->ir.bufs[b].bytes());
           // Scratch (per-row counters, look-back status) and the error word
           // start at zero; the kernels leave them at zero again.

@@ -135,9 +135,12 @@ struct ElemFn {
   }
 };
 
+int64_t tune(const char *key, int64_t dflt);
+
 class Gen {
  public:
-  Gen(const Graph &g, const Plan &p, const std::vector<int> &buf_of) : g_(g), p_(p), buf_of_(buf_of) {
+  Gen(const Graph &g, const Plan &p, const std::vector<int> &buf_of)
+      : g_(g), p_(p), buf_of_(buf_of), remat_(tune("remat_broadcast", 1) != 0) {
     for (const XNode &n : g_.xs) {
       int xa = -1, xb = -1;
       if (n.kind == XK::Bin && n.dt == DT::I64 && n.op == B_MUL && zext32(n.a, &xa) && zext32(n.b, &xb)) {
@@ -201,6 +204,7 @@ class Gen {
   const Graph &g_;
   const Plan &p_;
   const std::vector<int> &buf_of_;
+  bool remat_;
   std::ostringstream body_;
   int ntmp_ = 0;
   bool allow_ident_ = true;
@@ -261,7 +265,12 @@ class Gen {
     auto it = tmemo_.find(key);
     if (it != tmemo_.end()) return it->second;
     Val r;
-    if (p_.materialized[t]) {
+    const TNode &tn = g_.ts[t];
+    if (p_.materialized[t] && tn.kind == TK::Broadcast && p_.materialized[tn.a] && remat_) {
+      // a broadcast of a value already in memory: its one element read in
+      // place of the broadcast's own buffer (4 or 8 bytes an element saved)
+      r = inline_node(t, idx);
+    } else if (p_.materialized[t]) {
       int b = buf_of_[t];
       DT d = g_.ts[t].dt;
       if (allow_ident_ && idx.s == "i") {
@@ -4057,6 +4066,44 @@ struct Lowering {
     return {add_kernel(kname, args, (int)cdiv(N, 16), 256, "matmul_tiled", (int)cdiv(M, 16))};
   }
 
+  // Broadcast roots whose buffer no other root's kernel reads (their
+  // consumers read the broadcast's source instead; see Gen::elem) and that
+  // the graph does not output: their kernels are dropped and their buffers
+  // never allocated. The fusion plan itself is unchanged.
+  void elide_unread_broadcasts(std::vector<std::vector<int>> &launches) {
+    if (!tune("remat_broadcast", 1)) return;
+    std::vector<char> dead_kernel(prog.kernels.size(), 0);
+    bool any = false;
+    for (size_t ri = 0; ri < plan.roots.size(); ri++) {
+      const int r = plan.roots[ri];
+      if (g.ts[r].kind != TK::Broadcast) continue;
+      const int b = buf_of[r];
+      bool needed = false;
+      for (auto &o : g.outputs) needed |= o.second == r;
+      for (size_t rj = 0; rj < launches.size() && !needed; rj++) {
+        if (rj == ri) continue;
+        for (int k : launches[rj])
+          for (int a : prog.kernels[k].args) needed |= a == b;
+      }
+      if (needed) continue;
+      prog.bufs[b].elided = true;
+      for (int k : launches[ri]) dead_kernel[k] = 1;
+      launches[ri].clear();
+      any = true;
+    }
+    if (!any) return;
+    std::vector<int> remap(prog.kernels.size(), -1);
+    std::vector<KernelSpec> kept;
+    for (size_t k = 0; k < prog.kernels.size(); k++)
+      if (!dead_kernel[k]) {
+        remap[k] = (int)kept.size();
+        kept.push_back(prog.kernels[k]);
+      }
+    prog.kernels = kept;
+    for (auto &l : launches)
+      for (int &k : l) k = remap[k];
+  }
+
   void run() {
     prog.name = g.name;
     buf_of.assign(g.ts.size(), -1);
@@ -4112,11 +4159,13 @@ struct Lowering {
       scratch_of.push_back(sc);
     }
     prog.source = src.str();
+    elide_unread_broadcasts(launches);
     for (size_t i = 0; i < g.ts.size(); i++)
       if (g.ts[i].kind == TK::Param) prog.params.push_back({g.ts[i].pname, g.ts[i].dt, g.ts[i].shape, buf_of[i]});
     for (auto &o : g.outputs) prog.outputs.push_back({o.first, g.ts[o.second].dt, g.ts[o.second].shape, buf_of[o.second]});
     // Host plan.
-    for (int b = 0; b < ncomputed; b++) prog.plan.push_back({OpK::Alloc, b, -1, ""});
+    for (int b = 0; b < ncomputed; b++)
+      if (!prog.bufs[b].elided) prog.plan.push_back({OpK::Alloc, b, -1, ""});
     if (prog.err_buf >= 0) prog.plan.push_back({OpK::Alloc, prog.err_buf, -1, ""});
     for (auto &p : prog.params) prog.plan.push_back({OpK::Upload, p.buf, -1, p.name});
     for (size_t r = 0; r < launches.size(); r++) {
@@ -4128,7 +4177,8 @@ struct Lowering {
         if (fa.second == plan.roots[r]) prog.plan.push_back({OpK::Free, fa.first, -1, ""});
     }
     for (auto &o : prog.outputs) prog.plan.push_back({OpK::Download, o.buf, -1, o.name});
-    for (int b = 0; b < ncomputed; b++) prog.plan.push_back({OpK::Free, b, -1, ""});
+    for (int b = 0; b < ncomputed; b++)
+      if (!prog.bufs[b].elided) prog.plan.push_back({OpK::Free, b, -1, ""});
     if (prog.err_buf >= 0) prog.plan.push_back({OpK::Free, prog.err_buf, -1, ""});
   }
 };
@@ -4149,8 +4199,8 @@ std::string plan_to_string(const ProgramIR &p) {
   for (size_t i = 0; i < p.bufs.size(); i++) {
     const BufSpec &b = p.bufs[i];
     static const char *roles[] = {"param", "computed", "scratch", "err"};
-    os << "buffer " << i << " " << b.name << " " << dt_name(b.dt) << " " << b.numel << " " << roles[(int)b.role]
-       << "\n";
+    os << "buffer " << i << " " << b.name << " " << dt_name(b.dt) << " " << b.numel << " "
+       << (b.elided ? "elided" : roles[(int)b.role]) << "\n";
   }
   for (auto &k : p.kernels) {
     os << "kernel " << k.name << " " << k.role << " grid " << k.grid << " " << k.grid_y << " block " << k.block

@@ -130,6 +130,10 @@ struct BufSpec {
   DT dt = DT::F32;
   int64_t numel = 0;
   BufRole role = BufRole::Computed;
+  // A materialised tensor that no kernel reads and the graph does not
+  // output (a broadcast its consumers recompute): never allocated, its
+  // kernel not launched.
+  bool elided = false;
   int64_t bytes() const { return numel * dt_size(dt); }
 };
 

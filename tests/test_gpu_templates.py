@@ -311,6 +311,27 @@ def test_scatter_atomic_path(device, dtype, monkeypatch):
 
 
 @pytest.mark.parametrize("dtype", [F32, F64, I32])
+def test_broadcast_read_from_its_source(device, dtype):
+    """Broadcasts the fusion plan materialises, read by their consumers
+    from the one-element source (the broadcast's own kernel dropped), with
+    a broadcast output and a matrix-core operand that keep theirs; against
+    the oracle."""
+    s = D.scalar("s", dtype)
+    x = D.param("x", dtype, (300, 257))
+    b = D.broadcast((300, 257), s)
+    g = Graph.create("bc", [("u", D.map2(D.add, b, x)), ("v", D.map2(D.mul, b, x)),
+                            ("r", D.reduce_rows(D.add, D.const(dtype, 0), D.map2(D.sub, x, b))),
+                            ("p", D.scan_rows(D.max, D.const(dtype, -100), D.map2(D.add, b, x)))])
+    assert "elided" in H.plan(g)
+    sv = np.array(3, np.int32) if dtype is I32 else np.array(0.375, dtype.np)
+    check(g, [("s", sv), ("x", data(dtype, (300, 257), 24))], [])
+    if dtype is not I32:
+        b2, x2 = D.broadcast((256, 256), s), D.param("x", dtype, (256, 256))
+        g3 = Graph.create("bc3", [("c", D.matmul(b2, x2)), ("v", D.map2(D.mul, b2, x2)), ("b", b2)])
+        check(g3, [("s", sv), ("x", data(dtype, (256, 256), 25))], [])
+
+
+@pytest.mark.parametrize("dtype", [F32, F64, I32])
 def test_scatter_affine_index(device, dtype):
     """scatter_add through an index a*i + b built from iota (a strided,
     reversed, offset index; also through a reshape): one pass over the bins,

@@ -281,3 +281,29 @@ def test_plan_liveness_over_random_scatter_shapes(monkeypatch):
         tune = ["", "scatter_windows=0", "scatter_fuse_back=0", "scatter_local_max=0", "scatter_two_level=0"][case % 5]
         monkeypatch.setenv("CCHIP_TUNE", tune)
         _launch_uses_live_buffers(C.scatter_gather(n, bins, dt))
+
+
+def test_broadcast_read_in_place_by_its_consumers(monkeypatch):
+    """A broadcast of a one-element tensor that the fusion plan
+    materialises (it has two consumers) is read from its source by those
+    consumers; with no other reader and not an output, its kernel is
+    dropped and its buffer never allocated. An output broadcast, or one a
+    matmul reads straight from memory, keeps its kernel; remat_broadcast=0
+    keeps every one."""
+    s = D.scalar("s", F32)
+    x = D.param("x", F32, (64, 64))
+    b = D.broadcast((64, 64), s)
+    g = Graph.create("bc", [("u", D.map2(D.add, b, x)), ("v", D.map2(D.mul, b, x))])
+    bufs, ks, ops = parse(H.plan(g))
+    assert [r for _, _, _, r in bufs].count("elided") == 1 and len(ks) == 2
+    assert not any(o[0] in ("alloc", "free") and o[1] == [n for n, _, _, r in bufs if r == "elided"][0] for o in ops)
+    _launch_uses_live_buffers(g)
+    g2 = Graph.create("bc2", [("u", D.map2(D.add, b, x)), ("v", D.map2(D.mul, b, x)), ("b", b)])
+    assert "elided" not in [r for _, _, _, r in parse(H.plan(g2))[0]] and len(kernels_of(g2)) == 3
+    b2, x2 = D.broadcast((256, 256), s), D.param("x", F32, (256, 256))
+    g3 = Graph.create("bc3", [("c", D.matmul(b2, x2)), ("v", D.map2(D.mul, b2, x2))])
+    assert "matmul_mfma_f32_a0b0" in [t for _, t in kernels_of(g3)]
+    assert "elided" not in [r for _, _, _, r in parse(H.plan(g3))[0]]
+    _launch_uses_live_buffers(g3)
+    monkeypatch.setenv("CCHIP_TUNE", "remat_broadcast=0")
+    assert "elided" not in [r for _, _, _, r in parse(H.plan(g))[0]] and len(kernels_of(g)) == 3
