@@ -153,6 +153,41 @@ class Gen {
   // f(i) = the value of tensor `t` at flat index i. If `inline_root`, t is
   // computed (inlined) even though it is materialised: it is the kernel's
   // own output (lower.ml:120-126).
+  // A tensor whose elements all equal one value computed from one-element
+  // tensors alone: a broadcast, or a map over such tensors whose body does
+  // not use the element index.
+  bool uniform(int t) {
+    if (uni_.empty()) uni_.assign(g_.ts.size(), -1);
+    if (uni_[t] >= 0) return uni_[t] != 0;
+    const TNode &n = g_.ts[t];
+    bool u = false;
+    switch (n.kind) {
+      case TK::Broadcast: u = true; break;
+      case TK::Reshape: u = uniform(n.a); break;
+      case TK::Map: u = uniform(n.a) && !uses_index(n.body); break;
+      case TK::Map2: u = uniform(n.a) && uniform(n.b) && !uses_index(n.body); break;
+      default: break;
+    }
+    uni_[t] = u ? 1 : 0;
+    return u;
+  }
+  bool uses_index(int x) const {
+    std::vector<int> stack = {x};
+    std::vector<char> seen(g_.xs.size(), 0);
+    while (!stack.empty()) {
+      const int y = stack.back();
+      stack.pop_back();
+      if (y < 0 || seen[y]) continue;
+      seen[y] = 1;
+      const XNode &e = g_.xs[y];
+      if (e.kind == XK::Index) return true;
+      stack.push_back(e.a);
+      stack.push_back(e.b);
+      stack.push_back(e.c);
+    }
+    return false;
+  }
+
   ElemFn element_fn(const std::string &name, int t, bool inline_root, bool allow_ident) {
     reset(allow_ident);
     Val idx{"i", VC::I32};
@@ -205,6 +240,7 @@ class Gen {
   const Plan &p_;
   const std::vector<int> &buf_of_;
   bool remat_;
+  std::vector<signed char> uni_;
   std::ostringstream body_;
   int ntmp_ = 0;
   bool allow_ident_ = true;
@@ -265,10 +301,10 @@ class Gen {
     auto it = tmemo_.find(key);
     if (it != tmemo_.end()) return it->second;
     Val r;
-    const TNode &tn = g_.ts[t];
-    if (p_.materialized[t] && tn.kind == TK::Broadcast && p_.materialized[tn.a] && remat_) {
-      // a broadcast of a value already in memory: its one element read in
-      // place of the broadcast's own buffer (4 or 8 bytes an element saved)
+    if (p_.materialized[t] && remat_ && uniform(t)) {
+      // every element is the same value, computed from one-element tensors:
+      // computed here (loop-invariant) in place of reading the tensor's
+      // buffer, 4 or 8 bytes an element
       r = inline_node(t, idx);
     } else if (p_.materialized[t]) {
       int b = buf_of_[t];
@@ -4066,17 +4102,18 @@ struct Lowering {
     return {add_kernel(kname, args, (int)cdiv(N, 16), 256, "matmul_tiled", (int)cdiv(M, 16))};
   }
 
-  // Broadcast roots whose buffer no other root's kernel reads (their
-  // consumers read the broadcast's source instead; see Gen::elem) and that
-  // the graph does not output: their kernels are dropped and their buffers
-  // never allocated. The fusion plan itself is unchanged.
+  // Uniform roots (broadcasts, and maps of them that do not use the
+  // element index) whose buffer no other root's kernel reads (their
+  // consumers compute the value instead; see Gen::elem) and that the graph
+  // does not output: their kernels are dropped and their buffers never
+  // allocated. The fusion plan itself is unchanged.
   void elide_unread_broadcasts(std::vector<std::vector<int>> &launches) {
     if (!tune("remat_broadcast", 1)) return;
     std::vector<char> dead_kernel(prog.kernels.size(), 0);
     bool any = false;
     for (size_t ri = 0; ri < plan.roots.size(); ri++) {
       const int r = plan.roots[ri];
-      if (g.ts[r].kind != TK::Broadcast) continue;
+      if (!gen.uniform(r)) continue;
       const int b = buf_of[r];
       bool needed = false;
       for (auto &o : g.outputs) needed |= o.second == r;

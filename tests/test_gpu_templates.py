@@ -325,6 +325,11 @@ def test_broadcast_read_from_its_source(device, dtype):
     assert "elided" in H.plan(g)
     sv = np.array(3, np.int32) if dtype is I32 else np.array(0.375, dtype.np)
     check(g, [("s", sv), ("x", data(dtype, (300, 257), 24))], [])
+    # a map of the broadcast, materialised and computed by its consumers
+    e = D.map(lambda v: D.mul(D.add(v, D.const(dtype, 1)), v), b)
+    g2 = Graph.create("bc2", [("u", D.map2(D.add, e, x)), ("v", D.map2(D.sub, x, e))])
+    assert H.plan(g2).count("elided") == 1
+    check(g2, [("s", sv), ("x", data(dtype, (300, 257), 26))], [])
     if dtype is not I32:
         b2, x2 = D.broadcast((256, 256), s), D.param("x", dtype, (256, 256))
         g3 = Graph.create("bc3", [("c", D.matmul(b2, x2)), ("v", D.map2(D.mul, b2, x2)), ("b", b2)])

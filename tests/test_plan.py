@@ -286,10 +286,11 @@ def test_plan_liveness_over_random_scatter_shapes(monkeypatch):
 def test_broadcast_read_in_place_by_its_consumers(monkeypatch):
     """A broadcast of a one-element tensor that the fusion plan
     materialises (it has two consumers) is read from its source by those
-    consumers; with no other reader and not an output, its kernel is
-    dropped and its buffer never allocated. An output broadcast, or one a
-    matmul reads straight from memory, keeps its kernel; remat_broadcast=0
-    keeps every one."""
+    consumers, and so is a map of broadcasts that does not use the element
+    index; with no other reader and not an output, such a tensor's kernel
+    is dropped and its buffer never allocated. An output broadcast, or one
+    a matmul reads straight from memory, keeps its kernel;
+    remat_broadcast=0 keeps every one."""
     s = D.scalar("s", F32)
     x = D.param("x", F32, (64, 64))
     b = D.broadcast((64, 64), s)
@@ -305,5 +306,15 @@ def test_broadcast_read_in_place_by_its_consumers(monkeypatch):
     assert "matmul_mfma_f32_a0b0" in [t for _, t in kernels_of(g3)]
     assert "elided" not in [r for _, _, _, r in parse(H.plan(g3))[0]]
     _launch_uses_live_buffers(g3)
+    # a map of broadcasts is one value too (elided); one that uses the
+    # element index is not
+    e = D.map(lambda v: D.exp(D.mul(v, D.const(F32, 0.5))), b)
+    g4 = Graph.create("bc4", [("u", D.map2(D.add, e, x)), ("v", D.map2(D.mul, e, x))])
+    assert [r for _, _, _, r in parse(H.plan(g4))[0]].count("elided") == 1 and len(kernels_of(g4)) == 2
+    _launch_uses_live_buffers(g4)
+    ei = D.map(lambda v: D.add(v, D.cast(F32, D.index())), b)
+    g5 = Graph.create("bc5", [("u", D.map2(D.add, ei, x)), ("v", D.map2(D.mul, ei, x))])
+    assert "elided" not in [r for _, _, _, r in parse(H.plan(g5))[0]] and len(kernels_of(g5)) == 3
+    _launch_uses_live_buffers(g5)
     monkeypatch.setenv("CCHIP_TUNE", "remat_broadcast=0")
     assert "elided" not in [r for _, _, _, r in parse(H.plan(g))[0]] and len(kernels_of(g)) == 3
