@@ -2193,6 +2193,13 @@ struct Lowering {
   // and flag error 2, as the atomic path does. Within a slice the order of
   // the additions depends on LDS arrival order, so float sums are not
   // bit-reproducible (the atomic path's are not either).
+  // The largest power of two below n (1 for n <= 2): the first step of a
+  // binary search over n sorted entries.
+  static int64_t top_pow2(int64_t n) {
+    int64_t t = 1;
+    while (t * 2 < n) t *= 2;
+    return t;
+  }
   // Emitted code: the windows of super-slice `Q` of a windowed pass are
   // tiles [ta_, tz_).
   static std::string windows_of(const PassOut &o, const std::string &Q) {
@@ -2212,7 +2219,7 @@ struct Lowering {
       << "  if (" << ft << " >= wt_[" << o.P1 << "]) return;\n"
       << "  int Q_ = 0;\n"
       << "#pragma unroll\n"
-      << "  for (int st = 32; st >= 1; st >>= 1)\n"
+      << "  for (int st = " << top_pow2(o.P1) << "; st >= 1; st >>= 1)\n"
       << "    if (Q_ + st < " << o.P1 << " && wt_[Q_ + st] <= " << ft << ") Q_ += st;\n"
       << "  const int* const s1_ = b" << o.wstart << ";\n"
       << "  const int wb_ = s1_[Q_] + (" << ft << " - wt_[Q_]) * " << o.TILE << ";\n"
@@ -2872,17 +2879,30 @@ struct Lowering {
         std::ostringstream k;
         k << "extern \"C\" __global__ __launch_bounds__(64) void " << kname << "_windows(const int* __restrict__ b"
           << c1.start << ", int* __restrict__ b" << o.wtab << ") {\n"
-          << "  const int Q = threadIdx.x;\n"
-          << "  const int nt = Q < " << P1 << " ? (b" << c1.start << "[Q + 1] - b" << c1.start << "[Q] + " << TILE - 1
-          << ") / " << TILE << " : 0;\n"
-          << "  int in = nt;\n"
+          // lane l takes super-slices [l PQ, l PQ + PQ)
+          << "  const int l = threadIdx.x;\n"
+          << "  int nt[" << cdiv(P1, 64) << "], sum = 0;\n"
+          << "#pragma unroll\n"
+          << "  for (int c = 0; c < " << cdiv(P1, 64) << "; c++) {\n"
+          << "    const int Q = l * " << cdiv(P1, 64) << " + c;\n"
+          << "    nt[c] = Q < " << P1 << " ? (b" << c1.start << "[Q + 1] - b" << c1.start << "[Q] + " << TILE - 1 << ") / "
+          << TILE << " : 0;\n"
+          << "    sum += nt[c];\n"
+          << "  }\n"
+          << "  int in = sum;\n"
           << "#pragma unroll\n"
           << "  for (int d = 1; d < 64; d <<= 1) {\n"
           << "    const int o_ = __shfl_up(in, d);\n"
-          << "    if (Q >= d) in += o_;\n"
+          << "    if (l >= d) in += o_;\n"
           << "  }\n"
-          << "  if (Q < " << P1 << ") b" << o.wtab << "[Q] = in - nt;\n"
-          << "  if (Q == 63) b" << o.wtab << "[" << P1 << "] = in;\n"
+          << "  int run = in - sum;\n"
+          << "#pragma unroll\n"
+          << "  for (int c = 0; c < " << cdiv(P1, 64) << "; c++) {\n"
+          << "    const int Q = l * " << cdiv(P1, 64) << " + c;\n"
+          << "    if (Q < " << P1 << ") b" << o.wtab << "[Q] = run;\n"
+          << "    run += nt[c];\n"
+          << "  }\n"
+          << "  if (l == 63) b" << o.wtab << "[" << P1 << "] = in;\n"
           << "}\n";
         src << k.str();
         ks.push_back(add_kernel(kname + "_windows", {c1.start, o.wtab}, 1, 64, "scatter_windows"));
@@ -3279,8 +3299,11 @@ struct Lowering {
       while (S < want && S * 2 * ES <= lds) S *= 2;
       while (cdiv(M, S) > 4096 && S * ES < lds) S *= 2;
       int64_t P = cdiv(M, S);
+      // Two levels with the slice pass in windows take up to 8192 slices
+      // (128 super-slices); the counted forms up to 4096.
+      const bool windows = P > tune("scatter_stage_p", 512) && tune("scatter_two_level", 1) && tune("scatter_windows", 1);
       if (P == 1) return lower_scatter_lds(t, M, N, M, 1);
-      if (P <= 4096) return lower_scatter_lds(t, M, N, S, P);
+      if (P <= 4096 || (windows && P <= 8192)) return lower_scatter_lds(t, M, N, S, P);
     }
     std::vector<int> ks;
     if (M > 0) {

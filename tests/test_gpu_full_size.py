@@ -319,14 +319,16 @@ def test_config5_greeks_f32_full_size(device):
 
 
 @pytest.mark.parametrize("tune,tpl", [("", {"scatter_affine"}),
-                                      ("scatter_affine=0", {"scatter_zero", "scatter_atomic"})])
+                                      ("scatter_affine=0", {"scatter_coarse", "scatter_windows"}),
+                                      ("scatter_affine=0,scatter_lds=0", {"scatter_zero", "scatter_atomic"})])
 def test_gather_adjoint_of_the_last_column(device, monkeypatch, tune, tpl):
     """The adjoint of picking the last column of an f32[2^20 + 8; 64] by a
-    gather, as the path pricer does: a scatter_add into 2^26 bins through
-    the index p*64 + 63, one pass over the bins by default (the index is
-    affine and in range, so each bin takes at most one value), or (with
-    scatter_affine=0) the path for tables beyond the LDS slice limit,
-    scatter_zero + scatter_atomic; against the oracle."""
+    gather, as the path pricer does: a scatter_add into 2^26 + 512 bins
+    through the index p*64 + 63, one pass over the bins by default (the
+    index is affine and in range, so each bin takes at most one value);
+    with scatter_affine=0, the two-level LDS path over 4097 slices; with
+    scatter_lds=0 as well, scatter_zero + scatter_atomic; against the
+    oracle."""
     monkeypatch.setenv("CCHIP_TUNE", tune)
     rows, steps = (1 << 20) + 8, 64
     x = D.param("x", F32, (rows, steps))

@@ -233,6 +233,9 @@ GATHER_BACK_CASES = [
     ((1 << 24) + 5, 1 << 20, F32, False),
     # 301 slices: one level, per-chunk offsets (no tile-local runs)
     ((1 << 21) + 7, 301 * 16384 - 5, F32, False),
+    # 5001 slices in 79 super-slices (more than 64: two windows-table
+    # entries a lane)
+    ((1 << 20) + 5, 5000 * 16384 + 3, F32, True),
 ]
 
 

@@ -85,6 +85,8 @@ def test_scatter_template_choice(monkeypatch):
     assert ks(1 << 22, 256 * 16384) == ["scatter_partition", "scatter_accumulate", "scatter_reduce"]
     assert ks(1 << 22, 256 * 16384 + 1)[:4] == ["scatter_count", "scatter_colscan", "scatter_bscan", "scatter_partition"]
     assert ks(1 << 22, 1 << 28) == ["scatter_zero", "scatter_atomic"]
+    # two levels in windows up to 8192 slices (128 super-slices)
+    assert "scatter_windows" in ks(1 << 20, 8192 * 16384) and ks(1 << 20, 8192 * 16384 + 1)[-1] == "scatter_atomic"
     monkeypatch.setenv("CCHIP_TUNE", "scatter_local_max=0")
     assert ks(100000, 16385)[:4] == ["scatter_count", "scatter_colscan", "scatter_bscan", "scatter_partition"]
     monkeypatch.setenv("CCHIP_TUNE", "scatter_lds=0")
