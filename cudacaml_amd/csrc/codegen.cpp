@@ -3083,10 +3083,14 @@ struct Lowering {
         << lead << ", const int* __restrict__ b" << key << ", " << (fuse_back ? "" : "const ") << T << "* __restrict__ b"
         << val << ", " << T << "* __restrict__ b" << dst;
       if (fin.windows) k << ", const int* __restrict__ b" << fin.wtab;
+      // the table cleared and stored 4 bins at a time (S is a multiple of 4;
+      // a table cut short by the end of the bins stores its tail one by one)
+      const std::string tv4 = "__attribute__((ext_vector_type(4))) " + T;
       k << ") {\n"
-        << "  __shared__ " << T << " h[" << S << "];\n"
+        << "  __shared__ __align__(16) " << T << " h[" << S << "];\n"
         << "  const int q = blockIdx.x / " << W << ", w = blockIdx.x % " << W << ";\n"
-        << "  for (int b = threadIdx.x; b < " << S << "; b += " << AT << ") h[b] = " << zero_of(n.dt) << ";\n"
+        << "  for (int b = 4 * (int)threadIdx.x; b < " << S << "; b += " << 4 * AT << ") *(" << tv4 << "*)(h + b) = ("
+        << tv4 << ")" << zero_of(n.dt) << ";\n"
         << "  __syncthreads();\n";
       if (fin.local) {
         // the slice's runs in W shares of the tiles; a group's elements past
@@ -3184,12 +3188,16 @@ struct Lowering {
           << "  }\n";
       }
       if (part >= 0)
-        k << "  for (int b = threadIdx.x; b < " << S << "; b += " << AT << ") b" << dst << "[(size_t)w * " << P * S
-          << " + (size_t)q * " << S << " + b] = h[b];\n";
+        k << "  for (int b = 4 * (int)threadIdx.x; b < " << S << "; b += " << 4 * AT << ") *(" << tv4 << "*)(b" << dst
+          << " + (size_t)w * " << P * S << " + (size_t)q * " << S << " + b) = *(const " << tv4 << "*)(h + b);\n";
       else
         k << "  const int nb = " << B << " - q * " << S << " < " << S << " ? " << B << " - q * " << S << " : " << S
           << ";\n"
-          << "  for (int b = threadIdx.x; b < nb; b += " << AT << ") b" << dst << "[(size_t)q * " << S << " + b] = h[b];\n";
+          << "  for (int b = 4 * (int)threadIdx.x; b < nb; b += " << 4 * AT << ") {\n"
+          << "    if (b + 4 <= nb) *(" << tv4 << "*)(b" << dst << " + (size_t)q * " << S << " + b) = *(const " << tv4
+          << "*)(h + b);\n"
+          << "    else for (int e = b; e < nb; e++) b" << dst << "[(size_t)q * " << S << " + e] = h[e];\n"
+          << "  }\n";
       k << "}\n";
       src << k.str();
       std::vector<int> aargs = {lead, key, val, dst};
