@@ -3904,10 +3904,20 @@ struct Lowering {
     int64_t NACC = f64 ? 4 : 16;
     std::string mfma = f64 ? "__builtin_amdgcn_mfma_f64_16x16x4f64" : "__builtin_amdgcn_mfma_f32_32x32x2f32";
     int64_t tiles_m = M / BM, tiles_n = N / BM, ntiles = tiles_m * tiles_n;
+    // f64: one LDS buffer, refilled between two barriers (the fragments are
+    // in registers by the first), and a four-waves-a-SIMD register budget,
+    // which also keeps the accumulators in ordinary vector registers: at
+    // 2048^3, 47 -> 52 TFLOP/s against the double-buffered kernel
+    // (mm_f64_single=0, mm_f64_waves=0 restore it). f32 measured no gain
+    // from either.
+    const bool single = f64 && tune("mm_f64_single", 1) != 0;
+    const int64_t waves = f64 ? std::max<int64_t>(0, std::min<int64_t>(8, tune("mm_f64_waves", 4))) : 0;
     k << "typedef " << T << " " << accT << " __attribute__((ext_vector_type(" << NACC << ")));\n"
-      << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
-      << "  __shared__ __attribute__((aligned(16))) " << T << " As[2][" << ALDS << "];\n"
-      << "  __shared__ __attribute__((aligned(16))) " << T << " Bs[2][" << BLDS << "];\n"
+      << "extern \"C\" __global__ __launch_bounds__(256) ";
+    if (waves > 0) k << "__attribute__((amdgpu_waves_per_eu(" << waves << ", " << waves << "))) ";
+    k << "void " << kname << "(" << params << ") {\n"
+      << "  __shared__ __attribute__((aligned(16))) " << T << " As[" << (single ? 1 : 2) << "][" << ALDS << "];\n"
+      << "  __shared__ __attribute__((aligned(16))) " << T << " Bs[" << (single ? 1 : 2) << "][" << BLDS << "];\n"
       << "  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;\n"
       << "  const int wm = (wid >> 1) * " << WT << ", wn = (wid & 1) * " << WT << ";\n"
       // blocks are dispatched round-robin over the 8 XCDs; give each XCD a
@@ -3939,7 +3949,7 @@ struct Lowering {
       << gload(A, true, "ra") << gload(B, false, "rb") << lstore(A, "As[0]", "ra") << lstore(B, "Bs[0]", "rb")
       << "  __syncthreads();\n"
       << "  for (int it = 0; it < " << K / BK << "; it++) {\n"
-      << "    const int buf = it & 1;\n"
+      << "    const int buf = " << (single ? "0" : "it & 1") << ";\n"
       << "    kt = (it + 1) * " << BK << ";\n"
       << "    if (it + 1 < " << K / BK << ") {\n"
       << gload(A, true, "ra") << gload(B, false, "rb") << "    }\n"
@@ -3950,16 +3960,22 @@ struct Lowering {
       << "      __attribute__((aligned(16))) " << T << " fa[" << RT << "][" << S << "], fb[" << RT << "][" << S << "];\n"
       << "      const " << T << "* const al = As[buf];\n"
       << "      const " << T << "* const bl = Bs[buf];\n"
-      << fragload(A, "al", "fa", "wm") << fragload(B, "bl", "fb", "wn") << "#pragma unroll\n"
+      << fragload(A, "al", "fa", "wm") << fragload(B, "bl", "fb", "wn");
+    if (single)  // every wave holds its fragments: the buffer takes the next tile
+      k << "      __syncthreads();\n"
+        << "      if (it + 1 < " << K / BK << ") {\n"
+        << lstore(A, "As[0]", "ra") << lstore(B, "Bs[0]", "rb") << "      }\n";
+    k << "#pragma unroll\n"
       << "      for (int s2 = 0; s2 < " << S << "; s2++)\n"
       << "#pragma unroll\n"
       << "        for (int i = 0; i < " << RT << "; i++)\n"
       << "#pragma unroll\n"
       << "          for (int j = 0; j < " << RT << "; j++) acc[i][j] = " << mfma
       << "(fa[i][s2], fb[j][s2], acc[i][j], 0, 0, 0);\n"
-      << "    }\n"
-      << "    if (it + 1 < " << K / BK << ") {\n"
-      << lstore(A, "As[buf ^ 1]", "ra") << lstore(B, "Bs[buf ^ 1]", "rb") << "    }\n";
+      << "    }\n";
+    if (!single)
+      k << "    if (it + 1 < " << K / BK << ") {\n"
+        << lstore(A, "As[buf ^ 1]", "ra") << lstore(B, "Bs[buf ^ 1]", "rb") << "    }\n";
     if (KCT > 0)
       k << "    if ((it + 1) % " << KCT << " == 0) {\n"
         << "#pragma unroll\n"

@@ -476,6 +476,11 @@ KNOB_CASES = [
      lambda: [("a", data(F32, (128, 512), 43)), ("b", data(F32, (512, 256), 44))], "matmul_mfma_f32_a0b0"),
     ("mm_f64_bm=128,mm_f64_bk=32", lambda: C.matmul(256, F64, k=128, m=256),
      lambda: [("a", data(F64, (256, 128), 45)), ("b", data(F64, (128, 256), 46))], "matmul_mfma_f64_a0b0"),
+    # the f64 kernel double-buffered without the register budget
+    ("mm_f64_single=0,mm_f64_waves=0", lambda: C.matmul(192, F64, k=320, m=256),
+     lambda: [("a", data(F64, (256, 320), 93)), ("b", data(F64, (320, 192), 94))], "matmul_mfma_f64_a0b0"),
+    ("mm_f64_waves=6", lambda: C.matmul_grad(128, F64),
+     lambda: [("a", data(F64, (128, 128), 95)), ("b", data(F64, (128, 128), 96))], "matmul_mfma_f64_a1b0"),
     ("mm_kpad=3,mm_mpad=2", lambda: C.matmul_grad(256, F32),
      lambda: [("a", data(F32, (256, 256), 47)), ("b", data(F32, (256, 256), 48))], "matmul_mfma_f32_a1b0"),
     ("mm_mfma=0", lambda: C.matmul(128, F32, k=64, m=128),
