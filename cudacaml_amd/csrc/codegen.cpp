@@ -2669,9 +2669,9 @@ struct Lowering {
           k << "  int jn[" << E << "];\n"
             << "  " << T << " xn[" << E << "];\n"
             << "  if (lo < hi) {\n" << tile_load("lo", "jn", "xn") << "  }\n";
-        k << "  for (int t0 = lo; t0 < hi; t0 += " << TILE << ") {\n"
-          << "    const int tt = blockIdx.x * " << o.TPC << " + (t0 - lo) / " << TILE << ";\n"
-          << "    for (int q = threadIdx.x; q < " << PB << "; q += " << NT << ") tc[q] = 0;\n"
+        k << "  for (int t0 = lo; t0 < hi; t0 += " << TILE << ") {\n";
+        if (local) k << "    const int tt = blockIdx.x * " << o.TPC << " + (t0 - lo) / " << TILE << ";\n";
+        k << "    for (int q = threadIdx.x; q < " << PB << "; q += " << NT << ") tc[q] = 0;\n"
           << "    int jj[" << E << "], rk[" << E << "];\n"
           << "    " << T << " xv[" << E << "];\n";
         if (pf)
