@@ -569,6 +569,13 @@ KNOB_CASES = [
     ("map_unroll=2", lambda: P.chain(5003).graph(), lambda: P.chain(5003).inputs(), "map"),
     ("map_unroll=3", lambda: RB.poly_graph(10001, F64), lambda: [("x", RB.x_input(10001, F64))], "map"),
     ("map_unroll=1", lambda: RB.poly_graph(70001, F64), lambda: [("x", RB.x_input(70001, F64))], "map"),
+    # a capped grid: lanes loop over several workgroup-wide runs
+    ("map_blocks=3", lambda: P.chain(300007).graph(), lambda: P.chain(300007).inputs(), "map"),
+    ("map_blocks=5,map_unroll=2", lambda: RB.poly_graph(100003, F64), lambda: [("x", RB.x_input(100003, F64))], "map"),
+    ("map_blocks=7", lambda: Graph.create("aff", [("h", D.scatter_add(
+        D.map(lambda p: D.add(D.mul(p, D.const(I32, 3)), D.const(I32, 1)), D.iota((100003,))),
+        D.param("src", F32, (100003,)), (300014,)))]),
+     lambda: [("src", data(F32, (100003,), 81))], "scatter_affine"),
 ]
 
 
