@@ -512,6 +512,13 @@ KNOB_CASES = [
      lambda: [("x", data(I32, (3, 100001), 65))], "scan_lookback"),
     ("scatter_prefetch=0", lambda: scatter_graph(300001, 70000, F32),
      lambda: [("idx", scatter_idx(68, 300001, 70000)), ("src", data(F32, (300001,), 69))], "scatter_partition"),
+    # fewer, longer partition chunks: three and five tiles a workgroup, the
+    # last one ragged, with gather back
+    ("scatter_chunks=16", lambda: C.scatter_gather(300001, 70000, F32),
+     lambda: [("idx", scatter_idx(91, 300001, 70000)), ("src", data(F32, (300001,), 92))], "gather_unpartition"),
+    ("scatter_chunks=256", lambda: C.scatter_gather((1 << 23) + 5, 1 << 20, F32),
+     lambda: [("idx", scatter_idx(93, (1 << 23) + 5, 1 << 20)), ("src", data(F32, ((1 << 23) + 5,), 94))],
+     "gather_unpartition"),
     # threads per workgroup of the partition, accumulate and gather-back
     # kernels, away from their defaults (1024; 1024, or 512 with one
     # workgroup a slice; 512), with gather back
