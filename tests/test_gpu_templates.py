@@ -508,6 +508,9 @@ KNOB_CASES = [
     ("rr_depth=2,rr_bytes=16384", lambda: C.rows(2048, 5003),
      lambda: [("x", data(F32, (2048, 5003), 63))], "reduce_rowseq"),
     ("rs_chunk=4,rr_chunk=128", lambda: C.rows(1024, 3000), lambda: [("x", data(F32, (1024, 3000), 64))], "scan_rowseq"),
+    # tiles of a non-power-of-two width (384 and 1536 columns)
+    ("rs_bytes=6144,rr_bytes=24576", lambda: C.rows(1024, 3000),
+     lambda: [("x", data(F32, (1024, 3000), 96))], "scan_rowseq"),
     ("lb_buf=0", lambda: Graph.create("s", [("p", D.scan_rows(D.add, D.const(I32, 2), D.param("x", I32, (3, 100001))))]),
      lambda: [("x", data(I32, (3, 100001), 65))], "scan_lookback"),
     ("scatter_prefetch=0", lambda: scatter_graph(300001, 70000, F32),
