@@ -1416,21 +1416,38 @@ struct Lowering {
     // Tiles in flight in registers while one is folded: D register buffers
     // rotate, buffer d receiving tile kt + 1 + D when tile kt has been folded.
     const int64_t D = std::max<int64_t>(1, std::min<int64_t>(2, scan ? tune("rs_depth", 1) : tune("rr_depth", 1)));
+    // Split roles, for rows of four tiles or more: wave 0 folds tile kt
+    // from one LDS buffer while four loader waves move tile kt + 1 from
+    // registers into the other, load tile kt + 3 (two tiles in flight) and,
+    // in scans, store tile kt - 1. Done in turn by one workgroup, the fold
+    // and the wait for the next tile add up (the 8192^2 add reduction: 26.7
+    // us folding and 13 us waiting and moving per workgroup). Measured on
+    // 8192^2 f32: the row scan 101.5 -> 93.5-95.6 us split; the add and
+    // max reductions 55 / 49 -> 58 / 54 us, so reductions keep the turns.
+    const bool split = tune(scan ? "rs_split" : "rr_split", scan ? 1 : 0) != 0 && NT >= 4 &&
+                       2 * R * S * dt_size(n.dt) <= 150 * 1024;
+    const int NTH = split ? 320 : 256;
     std::ostringstream k;
-    k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
-      << "  __shared__ " << V4 << " sm4[" << R * S / 4 << "];\n"
-      << "  " << T << "* const sm = (" << T << "*)sm4;\n";
-    for (int64_t d = 0; d < D; d++) k << "  " << T << " rg" << d << "[" << E * 4 << "];\n";
+    k << "extern \"C\" __global__ __launch_bounds__(" << NTH << ") void " << kname << "(" << params << ") {\n";
+    if (split)
+      k << "  __shared__ " << V4 << " sm4a[" << R * S / 4 << "], sm4b[" << R * S / 4 << "];\n"
+        << "  " << T << "* const sma = (" << T << "*)sm4a;\n"
+        << "  " << T << "* const smb = (" << T << "*)sm4b;\n"
+        << "  const int lt = (int)threadIdx.x - 64;  // loader index (threads 64..319)\n";
+    else
+      k << "  __shared__ " << V4 << " sm4[" << R * S / 4 << "];\n"
+        << "  " << T << "* const sm = (" << T << "*)sm4;\n";
+    for (int64_t d = 0; d < (split ? 2 : D); d++) k << "  " << T << " rg" << d << "[" << E * 4 << "];\n";
     k << "  for (int g0 = blockIdx.x * " << R << "; g0 < " << rows << "; g0 += gridDim.x * " << R << ") {\n";
     // Tile c0 into registers: group u of thread t covers flat tile elements
     // q..q+3 with q = 4 (t + 256 u), at row q / W, column q % W.
-    auto load = [&](const std::string &c0, const std::string &rg) {
+    auto load = [&](const std::string &c0, const std::string &rg, const std::string &tid = "threadIdx.x") {
       std::ostringstream l;
       l << "    {\n"
         << "      const int c0 = " << c0 << ";\n"
         << "#pragma unroll\n"
         << "      for (int u = 0; u < " << E << "; u++) {\n"
-        << "        const int q = 4 * (threadIdx.x + 256 * u);\n"
+        << "        const int q = 4 * (" << tid << " + 256 * u);\n"
         << "        const int rr = q / " << W << ", j = q - rr * " << W << ";\n"
         << "        const int row = min(g0 + rr, " << rows - 1 << ");\n"
         << "        if (q < " << elems << ") {\n";
@@ -1451,27 +1468,26 @@ struct Lowering {
         << "    }\n";
       return l.str();
     };
-    auto to_lds = [&](const std::string &rg) {
+    auto to_lds = [&](const std::string &rg, const std::string &tid = "threadIdx.x", const std::string &buf = "sm4") {
       std::ostringstream l;
       l << "#pragma unroll\n"
         << "    for (int u = 0; u < " << E << "; u++) {\n"
-        << "      const int q = 4 * (threadIdx.x + 256 * u);\n"
+        << "      const int q = 4 * (" << tid << " + 256 * u);\n"
         << "      const int rr = q / " << W << ", j = q - rr * " << W << ";\n"
         << "      if (q < " << elems << ") {\n"
         << "        " << V4 << " w;\n";
       for (int c = 0; c < 4; c++) l << "        w." << comp[c] << " = " << rg << "[4 * u + " << c << "];\n";
-      l << "        sm4[(rr * " << S << " + j) / 4] = w;\n"
+      l << "        " << buf << "[(rr * " << S << " + j) / 4] = w;\n"
         << "      }\n"
         << "    }\n";
       return l.str();
     };
-    // One tile: fold it (lane r folds row r of the tile), store it (scans),
-    // move the next tile from registers into LDS, refill the registers.
-    auto body = [&](const std::string &rg) {
+    // Lane r folds row r of tile kt, held in LDS at `smp` (scans write the
+    // prefixes back in place).
+    auto fold_tile = [&](const std::string &smp) {
       std::ostringstream b;
-      b << "      const int c0 = kt * " << W << ";\n"
-        << "      if (threadIdx.x < " << R << " && g0 + threadIdx.x < " << rows << ") {\n"
-        << "        " << T << "* const s = sm + threadIdx.x * " << S << ";\n"
+      b << "      if (threadIdx.x < " << R << " && g0 + threadIdx.x < " << rows << ") {\n"
+        << "        " << T << "* const s = " << smp << " + threadIdx.x * " << S << ";\n"
         << "        if (kt + 1 < " << NT << " || " << REM << " == " << W << ") {\n"
         << "          for (int j0 = 0; j0 < " << W << "; j0 += " << CH << ") {\n"
         << "            " << T << " tv[" << CH << "];\n"
@@ -1494,37 +1510,84 @@ struct Lowering {
         << "          for (int j = 0; j < " << REM << "; j++) { acc = " << cmb << "(acc, s[j]);"
         << (scan ? " s[j] = acc;" : "") << " }\n"
         << "        }\n"
-        << "      }\n"
-        << "      __syncthreads();\n";
-      if (scan) {
-        b << "#pragma unroll\n"
-          << "      for (int u = 0; u < " << E << "; u++) {\n"
-          << "        const int q = 4 * (threadIdx.x + 256 * u);\n"
-          << "        const int rr = q / " << W << ", j = q - rr * " << W << ";\n"
-          << "        const int row = g0 + rr;\n"
-          << "        if (q < " << elems << " && row < " << rows << ") {\n"
-          << "          const int i = row * " << len << " + c0 + j;\n"
-          << "          const " << V4 << " o = sm4[(rr * " << S << " + j) / 4];\n";
-        if (vec) {
-          if (nt_stores)
-            b << "          if (c0 + j < " << len << ") cc_st4_nt(b" << out << " + i, o);\n";
-          else
-            b << "          if (c0 + j < " << len << ") *(" << V4 << "*)(b" << out << " + i) = o;\n";
-        } else {
-          for (int c = 0; c < 4; c++)
-            b << "          if (c0 + j + " << c << " < " << len << ") b" << out << "[i + " << c << "] = o." << comp[c]
-              << ";\n";
-        }
-        b << "        }\n"
-          << "      }\n"
-          << "      __syncthreads();\n";
+        << "      }\n";
+      return b.str();
+    };
+    // A scan's store of tile `ktx` from the LDS buffer `buf`, thread `tid`
+    // taking the same groups it moved into LDS.
+    auto store_tile = [&](const std::string &ktx, const std::string &tid, const std::string &buf) {
+      std::ostringstream b;
+      b << "#pragma unroll\n"
+        << "      for (int u = 0; u < " << E << "; u++) {\n"
+        << "        const int c0 = (" << ktx << ") * " << W << ";\n"
+        << "        const int q = 4 * (" << tid << " + 256 * u);\n"
+        << "        const int rr = q / " << W << ", j = q - rr * " << W << ";\n"
+        << "        const int row = g0 + rr;\n"
+        << "        if (q < " << elems << " && row < " << rows << ") {\n"
+        << "          const int i = row * " << len << " + c0 + j;\n"
+        << "          const " << V4 << " o = " << buf << "[(rr * " << S << " + j) / 4];\n";
+      if (vec) {
+        if (nt_stores)
+          b << "          if (c0 + j < " << len << ") cc_st4_nt(b" << out << " + i, o);\n";
+        else
+          b << "          if (c0 + j < " << len << ") *(" << V4 << "*)(b" << out << " + i) = o;\n";
+      } else {
+        for (int c = 0; c < 4; c++)
+          b << "          if (c0 + j + " << c << " < " << len << ") b" << out << "[i + " << c << "] = o." << comp[c]
+            << ";\n";
       }
+      b << "        }\n"
+        << "      }\n";
+      return b.str();
+    };
+    // One tile: fold it, store it (scans), move the next tile from
+    // registers into LDS, refill the registers.
+    auto body = [&](const std::string &rg) {
+      std::ostringstream b;
+      b << fold_tile("sm") << "      __syncthreads();\n";
+      if (scan) b << store_tile("kt", "threadIdx.x", "sm4") << "      __syncthreads();\n";
       b << "      if (kt + 1 < " << NT << ") {\n" << to_lds(rg) << "      }\n"
         << "      if (kt + " << 1 + D << " < " << NT << ") {\n"
         << load("(kt + " + std::to_string(1 + D) + ") * " + std::to_string(W), rg) << "      }\n"
         << "      __syncthreads();\n";
       return b.str();
     };
+    if (split) {
+      // Tile kt sits in buffer kt & 1; registers rg(kt & 1) hold tile
+      // kt + 1 while tile kt is folded.
+      auto step = [&](int d) {
+        const std::string mine = d ? "smb" : "sma", other4 = d ? "sm4a" : "sm4b", rg = "rg" + std::to_string(d);
+        std::ostringstream b;
+        b << fold_tile(mine) << "      if (threadIdx.x >= 64) {\n";
+        if (scan) b << "      if (kt >= 1) {\n" << store_tile("kt - 1", "lt", other4) << "      }\n";
+        b << "      if (kt + 1 < " << NT << ") {\n" << to_lds(rg, "lt", other4) << "      }\n"
+          << "      if (kt + 3 < " << NT << ") {\n"
+          << load("(kt + 3) * " + std::to_string(W), rg, "lt") << "      }\n"
+          << "      }\n"
+          << "      __syncthreads();\n";
+        return b.str();
+      };
+      k << "    if (threadIdx.x >= 64) {\n"
+        << load("0", "rg0", "lt") << to_lds("rg0", "lt", "sm4a") << load(std::to_string(W), "rg0", "lt")
+        << load(std::to_string(2 * W), "rg1", "lt") << "    }\n"
+        << "    __syncthreads();\n"
+        << "    " << T << " acc = " << ini << "();\n"
+        << "    for (int kt0 = 0; kt0 < " << NT << "; kt0 += 2) {\n"
+        << "      {\n      const int kt = kt0;\n" << step(0) << "      }\n"
+        << "      if (kt0 + 1 < " << NT << ") {\n      const int kt = kt0 + 1;\n" << step(1) << "      }\n"
+        << "    }\n";
+      if (scan)
+        k << "    if (threadIdx.x >= 64) {\n" << store_tile(std::to_string(NT - 1), "lt", (NT - 1) % 2 ? "sm4b" : "sm4a")
+          << "    }\n"
+          << "    __syncthreads();\n";
+      else
+        k << "    if (threadIdx.x < " << R << " && g0 + threadIdx.x < " << rows << ") b" << out
+          << "[g0 + threadIdx.x] = acc;\n";
+      k << "  }\n}\n";
+      src << k.str();
+      int grid = (int)std::min<int64_t>(cdiv(rows, R), 1 << 20);
+      return {add_kernel(kname, args, grid, NTH, scan ? "scan_rowseq" : "reduce_rowseq")};
+    }
     k << load("0", "rg0") << to_lds("rg0");
     for (int64_t d = 0; d < D; d++)
       k << "    if (" << NT << " > " << d + 1 << ") {\n"

@@ -67,6 +67,11 @@ SCAN_CASES = [
     (1024, 333, I32, "scan_rowseq"),
     (2048, 64, F32, "scan_rowseq"),
     (1500, 2050, I64, "scan_rowseq"),
+    # four tiles a row or more: one wave folds while four load and store
+    # (ragged last tiles; a last workgroup with rows past the end)
+    (1024, 20003, F32, "scan_rowseq"),
+    (1030, 9000, I32, "scan_rowseq"),
+    (2048, 9001, F64, "scan_rowseq"),
 ]
 
 
@@ -87,6 +92,8 @@ REDUCE_CASES = [
     (200, 8192, F32, "reduce_split"),
     (1024, 333, I32, "reduce_rowseq"),
     (4096, 5000, F64, "reduce_rowseq"),
+    (1024, 20003, F32, "reduce_rowseq"),
+    (1030, 30000, I32, "reduce_rowseq"),
 ]
 
 
@@ -508,6 +515,13 @@ KNOB_CASES = [
     ("rr_depth=2,rr_bytes=16384", lambda: C.rows(2048, 5003),
      lambda: [("x", data(F32, (2048, 5003), 63))], "reduce_rowseq"),
     ("rs_chunk=4,rr_chunk=128", lambda: C.rows(1024, 3000), lambda: [("x", data(F32, (1024, 3000), 64))], "scan_rowseq"),
+    # one workgroup folding and loading in turn for the scan, split roles for
+    # the reductions (the defaults the other way round), and split f64 ones
+    ("rs_split=0,rr_split=1", lambda: C.rows(1024, 20003), lambda: [("x", data(F32, (1024, 20003), 98))], "scan_rowseq"),
+    ("rr_split=1", lambda: (lambda x: Graph.create("r", [("s", D.reduce_rows(D.add, D.const(F64, 1.5), x)),
+                                                        ("m", D.reduce_rows(D.max, D.const(F64, 0.25), x))]))(
+        D.param("x", F64, (4096, 5000))),
+     lambda: [("x", data(F64, (4096, 5000), 99))], "reduce_rowseq"),
     # tiles of a non-power-of-two width (384 and 1536 columns)
     ("rs_bytes=6144,rr_bytes=24576", lambda: C.rows(1024, 3000),
      lambda: [("x", data(F32, (1024, 3000), 96))], "scan_rowseq"),
