@@ -9,7 +9,11 @@ an i32 vector of 2^28 elements. One step is one run of both compiled
 programs over inputs already resident in HBM (run_resident_into, outputs
 preallocated, no host traffic). ``value`` is algorithmic bytes per second
 over the K timed steps (each materialised input read once, each output
-written once, per kernel of the plan). Other configs (``--config saxpy``,
+written once, per root of the fusion plan). Where the lowering folds a
+whole-tensor reduction inside the map that writes its input (config 1's
+s = sum r), that read of r is still counted though no kernel moves it, so
+config 1's ``value`` is the plan's bytes per second, not HBM traffic (the
+dominant kernel's ``roofline`` is per kernel and unaffected). Other configs (``--config saxpy``,
 ``chain``, ``scatter``, ``scatter_perm``, ``matmul``, ``matmul64``, ``matmul_grad``,
 ``mc``, ``mc64``, ``mc_greeks``) print their own line in the same format;
 ``saxpy_hbm`` and ``chain_hbm`` run config 1's graphs over 2^28 elements,
@@ -130,7 +134,8 @@ def build_workload(name, H, C):
         if name.startswith("saxpy"):
             y = device_inputs(H, C.gen_uniform_pm1((n,)), 2)
             add(C.saxpy(n), [("x", x), ("y", y)])
-            desc = "config1: saxpy r=2x+y, s=sum r over f32[%s]" % what
+            desc = ("config1: saxpy r=2x+y, s=sum r over f32[%s]; s is folded inside r's map kernel, so the "
+                    "plan's read of r by the reduction (counted in value) is not moved" % what)
         else:
             add(C.chain(n), [("x", x)])
             desc = "config1b: 5-map chain over f32[%s], one fused kernel" % what

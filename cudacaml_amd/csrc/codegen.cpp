@@ -1015,6 +1015,15 @@ struct Lowering {
   std::map<int, GatherBack> gather_back;
   // scratch buffers freed after a later root than the one that made them
   std::map<int, int> free_after;
+  // Whole-tensor reductions of the previous root's map output, folded inside
+  // that map's kernel: map root -> reduce root, and reduce root -> the
+  // partials (one value a map wave), their has-element flags and count.
+  struct FusedPartials {
+    int part = -1, flags = -1;
+    int64_t count = 0;
+  };
+  std::map<int, int> fused_red_of_map;
+  std::map<int, FusedPartials> fused_part_of_red;
 
   explicit Lowering(const Graph &gr) : g(gr), plan(fusion_plan(gr)), gen(gr, plan, buf_of) {
     gen.bufdt_ = [this](int b) { return prog.bufs[b].dt; };
@@ -1313,6 +1322,32 @@ struct Lowering {
     int64_t UN = tune("map_unroll", -1);
     if (UN < 0) UN = std::count(f.code.begin(), f.code.end(), '\n') >= 48 ? 4 / G : 1;
     UN = std::max<int64_t>(1, std::min<int64_t>(4, UN));
+    // A whole-tensor reduction of this output folds it here: each lane
+    // folds the elements it stores, each wave combines its lanes and stores
+    // one partial and whether it held any element (the last workgroup's
+    // waves may hold none), and the reduction's root folds the partials.
+    // Its input is then never read back (config 1: s = sum(r) over 2^24).
+    // No workgroup barrier: waves leave as they finish.
+    const auto fr = fused_red_of_map.find(t);
+    const bool fuse = fr != fused_red_of_map.end();
+    std::string rc, ri;
+    int part = -1, pflag = -1;
+    if (fuse) {
+      const TNode &rn = g.ts[fr->second];
+      rc = "c_" + std::to_string(rn.id);
+      ri = "z_" + std::to_string(rn.id);
+      src << gen.combine_fn(rc, rn.body, rn.dt) << gen.const_fn(ri, rn.init, rn.dt);
+      const int64_t np = 4 * std::min<int64_t>(cdiv(std::max<int64_t>(1, N / G), 256 * UN), tune("map_blocks", 1 << 22));
+      part = add_buf("t" + std::to_string(rn.id) + "_partials", rn.dt, np, BufRole::Scratch);
+      pflag = add_buf("t" + std::to_string(rn.id) + "_partial_has", DT::I32, np, BufRole::Scratch);
+      free_after[part] = fr->second;
+      free_after[pflag] = fr->second;
+      fused_part_of_red[fr->second] = {part, pflag, np};
+      p.out.push_back(part);
+      p.out.push_back(pflag);
+      args.clear();
+      params = param_list(p, args);
+    }
     static const char *comp[] = {"x", "y", "z", "w"};
     // Each workgroup takes a contiguous run of 256 * UN groups, lane l its
     // groups l, l + 256, ..., and the grid covers the whole tensor, so each
@@ -1325,6 +1360,7 @@ struct Lowering {
     k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
       << "  const int stride = gridDim.x * " << 256 * UN << ";\n"
       << "  const int nvec = " << N / G << ";\n";
+    if (fuse) k << "  " << T << " acc = " << ri << "();\n  bool has = false;\n";
     if (UN == 1) {
       k << "  for (int v = blockIdx.x * 256 + threadIdx.x; v < nvec; v += stride) {\n"
         << "    const int i = v * " << G << ";\n"
@@ -1334,6 +1370,8 @@ struct Lowering {
         k << "    cc_st" << G << "_nt(b" << out << " + i, r);\n";
       else
         k << "    *(" << VG << "<" << T << ">*)(b" << out << " + i) = r;\n";
+      if (fuse)
+        for (int u = 0; u < G; u++) k << "    " << fold_in(rc, T, std::string("r.") + comp[u]) << "\n";
     } else {
       k << "  for (int v0 = blockIdx.x * " << 256 * UN << " + threadIdx.x; v0 < nvec; v0 += stride) {\n"
         << "    " << VG << "<" << T << "> r[" << UN << "];\n";
@@ -1352,12 +1390,28 @@ struct Lowering {
         else
           k << "*(" << VG << "<" << T << ">*)(b" << out << " + " << iq << ") = r[" << q << "];\n";
       }
+      // a clamped group is its owner's: folded once, by the owner
+      if (fuse)
+        for (int64_t q = 0; q < UN; q++)
+          for (int u = 0; u < G; u++)
+            k << "    " << fold_in_if(rc, T, "r[" + std::to_string(q) + "]." + comp[u], "v0 + " + std::to_string(q * 256) + " < nvec")
+              << "\n";
     }
-    k
-      << "  }\n"
-      << "  for (int i = nvec * " << G << " + blockIdx.x * 256 + threadIdx.x; i < " << N << "; i += gridDim.x * 256)\n"
-      << "    b" << out << "[i] = " << f.call_scalar("i") << ";\n"
-      << "}\n";
+    k << "  }\n"
+      << "  for (int i = nvec * " << G << " + blockIdx.x * 256 + threadIdx.x; i < " << N << "; i += gridDim.x * 256)";
+    if (fuse)
+      k << " {\n    const " << T << " v_ = " << f.call_scalar("i") << ";\n    b" << out << "[i] = v_;\n    "
+        << fold_in(rc, T, "v_") << "\n  }\n";
+    else
+      k << "\n    b" << out << "[i] = " << f.call_scalar("i") << ";\n";
+    if (fuse)
+      k << "  for (int off = 32; off > 0; off >>= 1) " << xor_combine(rc, T, "off") << "\n"
+        << "  if ((threadIdx.x & 63) == 0) {\n"
+        << "    const int w = blockIdx.x * 4 + (threadIdx.x >> 6);\n"
+        << "    b" << part << "[w] = acc;\n"
+        << "    b" << pflag << "[w] = has;\n"
+        << "  }\n";
+    k << "}\n";
     src << k.str();
     int64_t nvec = std::max<int64_t>(1, N / G);
     int grid = (int)std::min<int64_t>(cdiv(nvec, 256 * UN), tune("map_blocks", 1 << 22));
@@ -1621,6 +1675,70 @@ struct Lowering {
     int64_t len = row_length(s.shape);
     int64_t rows = n.numel;
     std::string cmb = "c_" + id, ini = "z_" + id;
+    const auto fp = fused_part_of_red.find(t);
+    if (fp != fused_part_of_red.end()) {
+      // The map that wrote the input left one partial a wave (its kernel
+      // emitted the combine): fold them, 1024 a workgroup in a first kernel
+      // where there are more, then the rest and init once.
+      std::vector<int> ks;
+      const int in = fp->second.part, flags = fp->second.flags;
+      const int64_t np = fp->second.count;
+      // the flags matter in the first fold only: a run of 1024 partials
+      // starts at a workgroup's first wave, which is never empty
+      // Each workgroup folds runs of 1024 partials, four a lane loaded
+      // together (indices clamped into the run, so no load waits behind a
+      // branch), then its lanes.
+      auto fold_kernel = [&](const std::string &name, int from, int to, int64_t count, int64_t per, bool final) {
+        const bool flagged = from == in;
+        Params p;
+        p.in.push_back(from);
+        if (flagged) p.in.push_back(flags);
+        p.out.push_back(to);
+        std::vector<int> args;
+        std::string params = param_list(p, args);
+        const std::string P = "b" + std::to_string(from), F = "b" + std::to_string(flags);
+        std::ostringstream k;
+        k << "extern \"C\" __global__ __launch_bounds__(256) void " << name << "(" << params << ") {\n"
+          << "  __shared__ " << T << " wpart[4];\n"
+          << "  __shared__ bool whas[4];\n"
+          << "  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;\n"
+          << "  const int lo = blockIdx.x * " << per << ", hi = min(lo + " << per << ", " << count << ");\n"
+          << "  " << T << " acc = " << ini << "();\n"
+          << "  bool has = false;\n"
+          << "  for (int c0 = lo; c0 < hi; c0 += 1024) {\n"
+          << "    " << T << " v[4];\n"
+          << "    bool ok[4];\n"
+          << "#pragma unroll\n"
+          << "    for (int u = 0; u < 4; u++) {\n"
+          << "      const int q = c0 + (int)threadIdx.x + 256 * u, qc = min(q, hi - 1);\n"
+          << "      v[u] = " << P << "[qc];\n"
+          << "      ok[u] = q < hi" << (flagged ? " && " + F + "[qc] != 0" : "") << ";\n"
+          << "    }\n"
+          << "#pragma unroll\n"
+          << "    for (int u = 0; u < 4; u++) " << fold_in_if(cmb, T, "v[u]", "ok[u]") << "\n"
+          << "  }\n"
+          << "  for (int off = 32; off > 0; off >>= 1) " << xor_combine(cmb, T, "off") << "\n"
+          << "  if (lane == 0) { wpart[wid] = acc; whas[wid] = has; }\n"
+          << "  __syncthreads();\n"
+          << "  if (threadIdx.x == 0) {\n"
+          << "    " << T << " t = " << ini << "();\n    bool th = false;\n"
+          << "    for (int w = 0; w < 4; w++) if (whas[w]) { t = th ? " << cmb << "(t, wpart[w]) : wpart[w]; th = true; }\n"
+          << "    b" << to << "[blockIdx.x] = " << (final ? cmb + "(" + ini + "(), t)" : "t") << ";\n"
+          << "  }\n"
+          << "}\n";
+        src << k.str();
+        ks.push_back(add_kernel(name, args, (int)cdiv(count, per), 256, "reduce_split_fold"));
+      };
+      if (np > 1024) {
+        const int64_t n1 = cdiv(np, 1024);
+        int mid = add_buf("t" + id + "_partials2", n.dt, n1, BufRole::Scratch);
+        fold_kernel(kname + "_fold", in, mid, np, 1024, false);
+        fold_kernel(kname, mid, out, n1, n1, true);
+      } else {
+        fold_kernel(kname, in, out, np, np, true);
+      }
+      return ks;
+    }
     src << gen.combine_fn(cmb, n.body, n.dt) << gen.const_fn(ini, n.init, n.dt);
     if (rows == 0) return {};
     if (len == 0) {
@@ -4290,6 +4408,25 @@ struct Lowering {
         if (n.kind != TK::Gather) continue;
         const int S = n.b;
         if (g.ts[S].kind == TK::Scatter && g.ts[S].a == n.a && !gbp_root_of.count(S)) gbp_root_of[S] = r;
+      }
+    // A reduction of a whole map output to one value, right after the map's
+    // own root, is folded inside the map kernel when the map is light
+    // (fuse_reduce=0: its own split reduction, reading the output back).
+    // Measured step times, fused against not: saxpy 2^24 0.043 / 0.049 ms,
+    // 2^28 0.52 / 0.67 ms, config 5's Greeks 4.00 / 4.04 ms; the degree-64
+    // Horner map (VALU-bound, 48 lines or more, as for map_unroll) 0.129 /
+    // 0.124 ms, since its waves then end on the fold's dependent tail.
+    if (tune("fuse_reduce", 1))
+      for (size_t ri = 1; ri < plan.roots.size(); ri++) {
+        const int r = plan.roots[ri], m = plan.roots[ri - 1];
+        const TNode &n = g.ts[r], &mn = g.ts[m];
+        if (n.kind != TK::Reduce || n.numel != 1 || n.a != m) continue;
+        if (mn.kind != TK::Map && mn.kind != TK::Map2) continue;
+        if (mn.dt != n.dt || n.dt == DT::BOOL || mn.numel < (1 << 16) || gen.uniform(m)) continue;
+        if (row_length(mn.shape) != mn.numel) continue;
+        const std::string code = gen.element_fn("fz_", m, true, true).code;
+        if (std::count(code.begin(), code.end(), '\n') >= 48) continue;
+        fused_red_of_map[m] = r;
       }
     std::vector<std::vector<int>> launches;
     std::vector<std::vector<int>> scratch_of;

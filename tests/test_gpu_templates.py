@@ -125,6 +125,30 @@ def test_scan_init_applied_once(device, rows, n, dtype, tpl):
     check(g, [("x", data(dtype, (rows, n), 15))], [tpl])
 
 
+FOLDED_CASES = [((1 << 16) + 3, F32, "add"), ((1 << 22) + 5, F32, "add"), ((1 << 20) + 2, F64, "add"),
+                (300 * 1024 + 5, F32, "add"), (1 << 18, F32, "add"), (102421, F32, "max"),
+                ((1 << 22) + 1, I32, "add"), ((1 << 20) + 7, F32, "max"), (1 << 23, I32, "max"),
+                ((1 << 21) + 1, F64, "max")]
+
+
+@pytest.mark.parametrize("n,dtype,comb", FOLDED_CASES, ids=lambda v: str(v))
+def test_reduce_folded_into_its_map(device, n, dtype, comb):
+    """A whole-tensor reduce of the previous root's map output folds inside
+    the map kernel: one partial a wave (flagged where the wave held no
+    element), then one fold kernel, or two where there are more than 1024
+    partials (past 2^18 4-byte elements). Ragged tails,
+    init not the identity (folded once), integers exact."""
+    x, y = D.param("x", dtype, (n,)), D.param("y", dtype, (n,))
+    r = D.map2(lambda a, b: D.add(D.mul(a, D.const(dtype, 2)), b), x, y)
+    op = D.add if comb == "add" else D.max
+    g = Graph.create("mr", [("r", r), ("s", D.reduce(op, D.const(dtype, 3), r))])
+    t = templates(g)
+    assert t[0] == "map" and "reduce_split" not in t, t
+    groups = n // (2 if dtype is F64 else 4)  # 16-byte groups, one a lane, 256 lanes a workgroup
+    assert t.count("reduce_split_fold") == (2 if 4 * -(-groups // 256) > 1024 else 1), t  # one partial a wave
+    check(g, [("x", data(dtype, (n,), 31)), ("y", data(dtype, (n,), 32))], ["map", "reduce_split_fold"])
+
+
 def test_reduce_empty_rows(device):
     x = D.param("x", F32, (5, 0))
     g = Graph.create("e", [("s", D.reduce_rows(D.add, D.const(F32, 2.5), x))])

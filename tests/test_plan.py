@@ -40,7 +40,18 @@ def test_chain_is_one_kernel():
     assert [t for _, t in kernels_of(P.chain(4096).graph())] == ["map"]
 
 
-def test_saxpy_is_map_then_reduce():
+def test_saxpy_is_map_then_reduce(monkeypatch):
+    """s = sum(r) of the map's own output folds inside the map kernel (one
+    partial a workgroup, then the fold); fuse_reduce=0 keeps the split
+    reduction that reads r back."""
+    ks = kernels_of(sx.program(1 << 18, 2.0))
+    assert [t for _, t in ks] == ["map", "reduce_split_fold"]
+    bufs, kk, _ = parse(H.plan(sx.program(1 << 18, 2.0)))
+    part = [b for b in bufs if b[0].endswith("_partials")]
+    assert len(part) == 1 and part[0][3] == "scratch" and part[0][2] == 4 * 256  # one a wave
+    # 2^20: more partials than one workgroup folds at once, so two fold kernels
+    assert [t for _, t in kernels_of(sx.program(1 << 20, 2.0))] == ["map", "reduce_split_fold", "reduce_split_fold"]
+    monkeypatch.setenv("CCHIP_TUNE", "fuse_reduce=0")
     ks = kernels_of(sx.program(1 << 20, 2.0))
     assert [t for _, t in ks] == ["map", "reduce_split", "reduce_split_fold"]
 
@@ -217,13 +228,19 @@ def _bytes(g):
             (l.split() for l in H.plan(g).splitlines() if l.startswith("kernel"))}
 
 
-def test_algorithmic_bytes_per_kernel():
+def test_algorithmic_bytes_per_kernel(monkeypatch):
     """Each root's algorithmic bytes sit on its main kernel: identity reads
     count the elements read, a gather one element per output, a broadcast
-    source one; helper kernels carry none."""
+    source one; helper kernels carry none. A reduction folded inside its
+    input's map keeps its root's bytes (its input read once), on its last
+    fold."""
     n = 1 << 20
     b = _bytes(sx.program(n, 2.0))
+    assert b["map"] == 3 * 4 * n and b["reduce_split_fold"] == 4 * n + 4
+    monkeypatch.setenv("CCHIP_TUNE", "fuse_reduce=0")
+    b = _bytes(sx.program(n, 2.0))
     assert b["map"] == 3 * 4 * n and b["reduce_split"] == 4 * n + 4
+    monkeypatch.delenv("CCHIP_TUNE")
     b = _bytes(C.global_scan(n))
     assert b["scan_lookback"] == 8 * n and b["scan_init"] == 0
     b = _bytes(C.scatter_gather(n, 1 << 15))
