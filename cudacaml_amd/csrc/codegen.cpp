@@ -4413,9 +4413,9 @@ struct Lowering {
     // own root, is folded inside the map kernel when the map is light
     // (fuse_reduce=0: its own split reduction, reading the output back).
     // Measured step times, fused against not: saxpy 2^24 0.043 / 0.049 ms,
-    // 2^28 0.52 / 0.67 ms, config 5's Greeks 4.00 / 4.04 ms; the degree-64
-    // Horner map (VALU-bound, 48 lines or more, as for map_unroll) 0.129 /
-    // 0.124 ms, since its waves then end on the fold's dependent tail.
+    // 2^28 0.52 / 0.67 ms; the degree-64 Horner map (VALU-bound, 48 lines or
+    // more, as for map_unroll) 0.129 / 0.124 ms, since its waves then end
+    // on the fold's dependent tail.
     if (tune("fuse_reduce", 1))
       for (size_t ri = 1; ri < plan.roots.size(); ri++) {
         const int r = plan.roots[ri], m = plan.roots[ri - 1];
