@@ -3513,13 +3513,21 @@ struct Lowering {
     }
     std::vector<int> ks;
     if (M > 0) {
+      // 16-byte stores, one group a lane over a grid as wide as the table
+      // (the map template's shape), the ragged tail by the first lanes
+      const int ZG = dt_size(n.dt) == 8 ? 2 : 4;
+      const int64_t zvec = M / ZG;
       std::ostringstream z;
       z << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "_zero(" << T << "* __restrict__ b"
         << out << ") {\n"
-        << "  for (int i = blockIdx.x * 256 + threadIdx.x; i < " << M << "; i += gridDim.x * 256) b" << out
-        << "[i] = " << zero_of(n.dt) << ";\n}\n";
+        << "  typedef " << T << " zv __attribute__((ext_vector_type(" << ZG << ")));\n"
+        << "  for (long long v = (long long)blockIdx.x * 256 + threadIdx.x; v < " << zvec
+        << "; v += (long long)gridDim.x * 256) ((zv*)b" << out << ")[v] = (zv)(" << zero_of(n.dt) << ");\n"
+        << "  if (blockIdx.x == 0 && (long long)threadIdx.x < " << M - zvec * ZG << ") b" << out << "[" << zvec * ZG
+        << " + threadIdx.x] = " << zero_of(n.dt) << ";\n}\n";
       src << z.str();
-      ks.push_back(add_kernel(kname + "_zero", {out}, (int)std::min<int64_t>(cdiv(M, 256), 16384), 256, "scatter_zero"));
+      ks.push_back(add_kernel(kname + "_zero", {out}, (int)std::min<int64_t>(std::max<int64_t>(1, cdiv(zvec, 256)), 1 << 22),
+                              256, "scatter_zero"));
     }
     if (N == 0) return ks;
     ElemFn fi = gen.element_fn("fi_" + id, n.a, false, true);
@@ -3557,7 +3565,7 @@ struct Lowering {
       << "  }\n}\n";
     src << k.str();
     int64_t nvec = std::max<int64_t>(1, N / 4);
-    ks.push_back(add_kernel(kname, args, (int)std::min<int64_t>(cdiv(nvec, 256), 65536), 256, "scatter_atomic"));
+    ks.push_back(add_kernel(kname, args, (int)std::min<int64_t>(cdiv(nvec, 256), 1 << 22), 256, "scatter_atomic"));
     return ks;
   }
 
