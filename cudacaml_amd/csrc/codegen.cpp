@@ -1272,7 +1272,7 @@ struct Lowering {
     prog.kernels[main].algo_bytes = bytes;
   }
 
-  // ---- element-wise root (K1 -> vectorised grid-stride map) --------------
+  // ---- element-wise root (K1 -> vectorised map, one 16-byte group a lane) ---
   std::vector<int> lower_map(int t) {
     const TNode &n = g.ts[t];
     std::string kname = "k_" + std::to_string(n.id);
@@ -3570,7 +3570,8 @@ struct Lowering {
   }
 
   // scatter_add with an injective affine index (see lower_scatter): one
-  // grid-stride pass over the bins, four a thread, each bin j taking
+  // pass over the bins, four a thread on a grid as wide as the table, each
+  // bin j taking
   // 0 + src((j - b) / a) where a divides j - b and the quotient is a source
   // index, else 0.
   std::vector<int> lower_scatter_affine(int t, int64_t A, int64_t Bc) {
