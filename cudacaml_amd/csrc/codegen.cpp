@@ -4130,7 +4130,16 @@ struct Lowering {
       // blocks are dispatched round-robin over the 8 XCDs; give each XCD a
       // contiguous run of tiles so its L2 sees shared A row panels.
       << "  int tile = blockIdx.x;\n";
-    if (ntiles % 8 == 0) k << "  tile = (tile % 8) * " << ntiles / 8 << " + tile / 8;\n";
+    if (ntiles % 8 == 0) {
+      const int64_t TX = ntiles / 8, RX = TX % tiles_n == 0 ? TX / tiles_n : 0;
+      k << "  tile = (tile % 8) * " << TX << " + tile / 8;\n";
+      // Within an XCD's RX whole tile rows, walk column by column, so the
+      // tiles resident together span RX row panels of A and few column
+      // panels of B instead of one row panel and every column panel.
+      if (RX > 1 && tune("mm_xcd_cols", 1))
+        k << "  { const int x = tile / " << TX << ", l = tile - x * " << TX << "; tile = x * " << TX << " + (l % " << RX
+          << ") * " << tiles_n << " + l / " << RX << "; }\n";
+    }
     k << "  const int bm = (tile / " << tiles_n << ") * " << BM << ", bn = (tile % " << tiles_n << ") * " << BM << ";\n"
       << "  " << accT << " acc[" << RT << "][" << RT << "];\n"
       << "#pragma unroll\n"

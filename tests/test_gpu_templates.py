@@ -514,6 +514,12 @@ KNOB_CASES = [
      lambda: [("a", data(F64, (128, 128), 95)), ("b", data(F64, (128, 128), 96))], "matmul_mfma_f64_a1b0"),
     ("mm_kpad=3,mm_mpad=2", lambda: C.matmul_grad(256, F32),
      lambda: [("a", data(F32, (256, 256), 47)), ("b", data(F32, (256, 256), 48))], "matmul_mfma_f32_a1b0"),
+    # tile order inside each XCD's run of tile rows: column by column (the
+    # default; a non-square grid of 16 x 8 tiles) and row by row
+    ("mm_xcd_cols=1", lambda: C.matmul(1024, F32, k=64, m=2048),
+     lambda: [("a", data(F32, (2048, 64), 51)), ("b", data(F32, (64, 1024), 52))], "matmul_mfma_f32_a0b0"),
+    ("mm_xcd_cols=0", lambda: C.matmul(1024, F64, k=64, m=1024),
+     lambda: [("a", data(F64, (1024, 64), 53)), ("b", data(F64, (64, 1024), 54))], "matmul_mfma_f64_a0b0"),
     ("mm_mfma=0", lambda: C.matmul(128, F32, k=64, m=128),
      lambda: [("a", data(F32, (128, 64), 49)), ("b", data(F32, (64, 128), 50))], "matmul_tiled"),
     ("map_nt=2", lambda: P.chain(5000).graph(), lambda: P.chain(5000).inputs(), "map"),
