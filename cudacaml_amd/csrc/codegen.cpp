@@ -1699,6 +1699,19 @@ struct Lowering {
   }
 
   // ---- Reduce root (K2-K4 -> wave / block / split-row reductions) --------
+  // Whether the combine (x0, x1) -> body is op(x0, x1) or op(x1, x0) for
+  // an op whose result does not depend on the grouping or order of its
+  // operands.
+  bool any_order(int body, DT dt) const {
+    const XNode &x = g.xs[body];
+    if (x.kind != XK::Bin || x.a < 0 || x.b < 0) return false;
+    const XNode &l = g.xs[x.a], &r = g.xs[x.b];
+    if (l.kind != XK::Arg || r.kind != XK::Arg || l.arg == r.arg) return false;
+    if (x.op == B_MIN || x.op == B_MAX) return true;
+    const bool integer = dt == DT::I32 || dt == DT::I64;
+    return integer && (x.op == B_ADD || x.op == B_MUL || x.op == B_AND || x.op == B_OR || x.op == B_XOR);
+  }
+
   std::vector<int> lower_reduce(int t) {
     const TNode &n = g.ts[t];
     const TNode &s = g.ts[n.a];
@@ -1788,7 +1801,11 @@ struct Lowering {
     }
     ElemFn f = gen.element_fn("f_" + id, n.a, false, true);
     src << f.code;
-    if (rows >= 1024) return lower_rows_seq(t, false, f, cmb, ini, rows, len);
+    // A combine that gives the same bits in any grouping (max and min,
+    // which propagate NaN and order -0 below +0; wrapping integer add, mul
+    // and bit operations) folds rows as a tree (rr_tree=0: in order).
+    if (rows >= 1024 && !(tune("rr_tree", 1) && any_order(n.body, n.dt)))
+      return lower_rows_seq(t, false, f, cmb, ini, rows, len);
     bool vec = len % 4 == 0;
     if (len <= 2048) {
       // One wave (or a power-of-two segment of one) per row.

@@ -90,10 +90,12 @@ REDUCE_CASES = [
     (1, 1 << 22, I32, "reduce_split"),
     (3, 999999, I64, "reduce_split"),
     (200, 8192, F32, "reduce_split"),
-    (1024, 333, I32, "reduce_rowseq"),
+    (1024, 333, F32, "reduce_rowseq"),
     (4096, 5000, F64, "reduce_rowseq"),
     (1024, 20003, F32, "reduce_rowseq"),
-    (1030, 30000, I32, "reduce_rowseq"),
+    # integer add and max give the same bits in any order: tree templates
+    (1024, 333, I32, "reduce_wave"),
+    (1030, 30000, I32, "reduce_block"),
 ]
 
 
@@ -545,6 +547,12 @@ KNOB_CASES = [
     ("rr_depth=2,rr_bytes=16384", lambda: C.rows(2048, 5003),
      lambda: [("x", data(F32, (2048, 5003), 63))], "reduce_rowseq"),
     ("rs_chunk=4,rr_chunk=128", lambda: C.rows(1024, 3000), lambda: [("x", data(F32, (1024, 3000), 64))], "scan_rowseq"),
+    # integer row reductions folded in order, as floats are (rows of four
+    # tiles or more, split roles, and a last workgroup past the rows)
+    ("rr_tree=0", lambda: Graph.create("r", [("s", D.reduce_rows(D.add, D.const(I32, 5), D.param("x", I32, (1030, 30000))))]),
+     lambda: [("x", data(I32, (1030, 30000), 61))], "reduce_rowseq"),
+    ("rr_tree=0,rr_split=1", lambda: Graph.create("r", [("m", D.reduce_rows(D.max, D.const(I32, 3), D.param("x", I32, (1030, 30000))))]),
+     lambda: [("x", data(I32, (1030, 30000), 62))], "reduce_rowseq"),
     # one workgroup folding and loading in turn for the scan, split roles for
     # the reductions (the defaults the other way round), and split f64 ones
     ("rs_split=0,rr_split=1", lambda: C.rows(1024, 20003), lambda: [("x", data(F32, (1024, 20003), 98))], "scan_rowseq"),

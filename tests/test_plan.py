@@ -147,7 +147,8 @@ def test_scan_template_choice(rows, n, tpls):
 
 
 def test_config_plans():
-    assert [t for _, t in kernels_of(C.rows())] == ["reduce_rowseq", "reduce_rowseq", "scan_rowseq"]
+    # the max reduction gives the same bits in any order: a workgroup a row
+    assert [t for _, t in kernels_of(C.rows())] == ["reduce_rowseq", "reduce_block", "scan_rowseq"]
     # the gather back reads the scatter's partition: the table slice by
     # slice from LDS, then each tile's values back in element order; 128
     # slices, so the partition keeps each tile's pairs in the tile's region
