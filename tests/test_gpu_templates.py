@@ -151,6 +151,54 @@ def test_reduce_folded_into_its_map(device, n, dtype, comb):
     check(g, [("x", data(dtype, (n,), 31)), ("y", data(dtype, (n,), 32))], ["map", "reduce_split_fold"])
 
 
+@pytest.mark.parametrize("order", ["sum_first", "map_first"])
+def test_reduce_folded_with_fan_out(device, order):
+    """A map output materialised only by its fan-out (two consumers, not an
+    output): the sum folds inside the map kernel when it is the next root,
+    and reads the output back when the other consumer's root comes
+    between."""
+    n = (1 << 20) + 3
+    x, y = D.param("x", F32, (n,)), D.param("y", F32, (n,))
+    r = D.map2(lambda a, b: D.add(D.mul(a, D.const(F32, 2)), b), x, y)
+    s = D.reduce(D.add, D.const(F32, 0.5), r)
+    q = D.map(lambda e: D.mul(e, e), r)
+    outs = [("s", s), ("q", q)] if order == "sum_first" else [("q", q), ("s", s)]
+    g = Graph.create("fan", outs)
+    t = templates(g)
+    assert ("reduce_split" in t) == (order == "map_first"), t
+    check(g, [("x", data(F32, (n,), 33)), ("y", data(F32, (n,), 34))], ["map", "reduce_split_fold"])
+
+
+def test_rows_max_min_tree_edges(device):
+    """max and min of rows fold as a tree: IEEE maximum and minimum
+    propagate NaN and order -0 below +0, so every row matches the
+    interpreter's fold in order bit for bit (rows of zeros of both signs,
+    infinities, NaNs); init applied once."""
+    rows, n = 1024, 5000
+    v = data(F32, (rows, n), 35)
+    r = np.random.default_rng(5)
+    v[r.integers(0, rows, 40), r.integers(0, n, 40)] = np.nan
+    v[v > 0.999] = np.inf
+    v[v < -0.999] = -np.inf
+    v[100:110] = 0.0
+    v[100:110, ::3] = -0.0
+    v[200:210] = -0.0
+    x = D.param("x", F32, (rows, n))
+    g = Graph.create("mm", [("mx", D.reduce_rows(D.max, D.const(F32, -0.0), x)),
+                            ("mn", D.reduce_rows(D.min, D.const(F32, 0.0), x))])
+    assert templates(g) == ["reduce_block", "reduce_block"]
+    exp = oracle.run(g, [("x", v)])
+    c = H.compile(g)
+    try:
+        got = H.run(c, [("x", v)])
+    finally:
+        c.release()
+    for (name, e), (_, d) in zip(exp, got):
+        assert np.array_equal(np.isnan(e), np.isnan(d)), name
+        ok = ~np.isnan(e)
+        np.testing.assert_array_equal(e[ok].view(np.uint32), d[ok].view(np.uint32), err_msg=name)
+
+
 def test_reduce_empty_rows(device):
     x = D.param("x", F32, (5, 0))
     g = Graph.create("e", [("s", D.reduce_rows(D.add, D.const(F32, 2.5), x))])
