@@ -13,7 +13,9 @@ written once, per root of the fusion plan). Where the lowering folds a
 whole-tensor reduction inside the map that writes its input (config 1's
 s = sum r), that read of r is still counted though no kernel moves it, so
 config 1's ``value`` is the plan's bytes per second, not HBM traffic (the
-dominant kernel's ``roofline`` is per kernel and unaffected). Other configs (``--config saxpy``,
+dominant kernel's ``roofline`` is per kernel and unaffected); ``config``
+gives both ``algorithmic_bytes_per_step`` and ``moved_bytes_per_step``.
+Other configs (``--config saxpy``,
 ``chain``, ``scatter``, ``scatter_perm``, ``matmul``, ``matmul64``, ``matmul_grad``,
 ``mc``, ``mc64``, ``mc_greeks``) print their own line in the same format;
 ``saxpy_hbm`` and ``chain_hbm`` run config 1's graphs over 2^28 elements,
@@ -57,6 +59,25 @@ FP64_MFMA_TFLOPS = 78.6
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def folded_reads(H, graph):
+    """Bytes of the plan's algorithmic total that no kernel moves: a
+    whole-tensor reduction folded inside the map that writes its input
+    keeps its root's bytes (the input read once, one value written) on its
+    last fold kernel, but reads nothing back. Such a fold is the only
+    reduce_split_fold that carries bytes (a split reduction's fold carries
+    none); its input read is those bytes less the one output value."""
+    sizes, kern = {}, []
+    for line in H.plan(graph).splitlines():
+        f = line.split()
+        if f[0] == "buffer":
+            sizes[f[1]] = int(f[4]) * (8 if f[3] in ("f64", "i64") else 4)
+        elif f[0] == "kernel" and f[2] == "reduce_split_fold":
+            b = int(f[f.index("bytes") + 1])
+            if b > 0:
+                kern.append((b, f[-1]))
+    return sum(b - sizes.get(o, 0) for b, o in kern)
 
 
 def plan_bytes(H, graph):
@@ -736,7 +757,8 @@ def main():
         "vs_baseline": vs_baseline,
         "dtype": w.dtype,
         "data": "synthetic (Philox-4x32-10 inputs generated on the device)",
-        "config": {"workload": w.describe, "parallelism": "single GPU", "algorithmic_bytes_per_step": total_bytes},
+        "config": {"workload": w.describe, "parallelism": "single GPU", "algorithmic_bytes_per_step": total_bytes,
+                   "moved_bytes_per_step": total_bytes - sum(folded_reads(H, g) for g, _, _, _ in w.programs)},
         "roofline": roof,
         "cpu_baseline": cpu,
         "whole_run": whole,
