@@ -1,0 +1,88 @@
+"""Seeded random graphs for the two reduction paths that fold in a new
+order: a whole-tensor reduction folded inside the map that writes its input
+(the map's output is also a graph output, and the reduction is the next
+root), and row reductions whose combine gives the same bits in any order
+(max, min; integer add, mul and bit operations), folded as a tree. Random
+dtypes, light element-wise expressions (tests/fuzz_graphs.py), ragged
+sizes above the fold's 2^16 threshold and non-identity inits, against the
+oracle under the per-output policy: integers and max/min bit-exact, float
+sums within the accumulation band."""
+
+import numpy as np
+import pytest
+
+import fuzz_graphs as FG
+import oracle
+from cudacaml_amd import backend_hip as H
+from cudacaml_amd import differential as Diff
+from cudacaml_amd import dsl as D
+from cudacaml_amd.ir import F32, F64, I32, Graph
+
+pytestmark = pytest.mark.gpu
+
+N_CASES = 16
+
+
+def templates(g):
+    return [l.split()[2] for l in H.plan(g).splitlines() if l.startswith("kernel")]
+
+
+def folded_case(seed):
+    r = np.random.default_rng(5000 + seed)
+    dt = [F32, F64, I32][seed % 3]
+    n = int(2 ** r.uniform(16.1, 21.5)) + int(r.integers(0, 4))
+    x, y = D.param("x", dt, (n,)), D.param("y", dt, (n,))
+    expr = FG._int_expr if dt is I32 else FG._float_expr
+    m = D.map2(lambda a, b: expr(r, [a, b], 2), x, y)
+    ops = ["add", "max", "min"] + (["mul", "xor"] if dt is I32 else [])
+    op = ops[int(r.integers(len(ops)))]
+    comb = {"add": D.add, "max": D.max, "min": D.min, "mul": D.mul, "xor": D.bit_xor}[op]
+    init = D.const(dt, int(r.integers(-3, 4)) if dt is I32 else float(r.choice([0.0, 1.5, -2.0])))
+    g = Graph.create("fold%d" % seed, [("m", m), ("s", D.reduce(comb, init, m))])
+    inputs = [("x", FG._input(r, dt, (n,))), ("y", FG._input(r, dt, (n,)))]
+    return g, inputs, (dt.name, n, op)
+
+
+def tree_case(seed):
+    r = np.random.default_rng(6000 + seed)
+    dt = [F32, F64, I32][seed % 3]
+    rows, cols = int(r.choice([1024, 1100, 2048, 3001])), int(r.choice([1, 63, 333, 2049, 5000]))
+    x = D.param("x", dt, (rows, cols))
+    ops = ["max", "min"] + (["add", "mul", "and"] if dt is I32 else [])
+    op = ops[int(r.integers(len(ops)))]
+    comb = {"add": D.add, "max": D.max, "min": D.min, "mul": D.mul, "and": D.bit_and}[op]
+    init = D.const(dt, int(r.integers(-3, 4)) if dt is I32 else float(r.choice([0.0, 0.75, -1.0])))
+    g = Graph.create("tree%d" % seed, [("s", D.reduce_rows(comb, init, x))])
+    return g, [("x", FG._input(r, dt, (rows, cols)))], (dt.name, rows, cols, op)
+
+
+def _run(g, inputs):
+    exp = oracle.run(g, inputs)
+    c = H.compile(g)
+    try:
+        got = H.run(c, inputs)
+    finally:
+        c.release()
+    return exp, got
+
+
+@pytest.mark.parametrize("seed", range(N_CASES))
+def test_folded_reduction_fuzz(device, seed):
+    g, inputs, what = folded_case(seed)
+    print("case", seed, *what, flush=True)
+    t = templates(g)
+    assert "reduce_split" not in t and "reduce_split_fold" in t, (what, t)
+    exp, got = _run(g, inputs)
+    bad = [v for v in Diff.policy_check(g, exp, got) if not v.ok]
+    assert not bad, (what, bad)
+
+
+@pytest.mark.parametrize("seed", range(N_CASES))
+def test_tree_row_reduction_fuzz(device, seed):
+    g, inputs, what = tree_case(seed)
+    print("case", seed, *what, flush=True)
+    assert "reduce_rowseq" not in templates(g), what
+    exp, got = _run(g, inputs)
+    for (name, e), (_, d) in zip(exp, got):
+        # any grouping gives the same bits (no NaN among these inputs)
+        np.testing.assert_array_equal(e.view(np.uint8), d.view(np.uint8), err_msg=str(what))
