@@ -111,6 +111,48 @@ def test_noalloc_calls_in_a_row_match_run_resident_into(device, on):
         cb.release()
 
 
+def test_noalloc_folded_sum_calls_in_a_row(device):
+    """A map whose output the next root sums: the sum is folded inside the
+    map kernel, so its wave partials and flags are scratch live across two
+    roots. Two calls in a row, the second smaller (two fold kernels, then
+    one), each bit for bit against run_resident_into and numpy (integers:
+    exact in any order)."""
+    def prog(n):
+        x, y = D.param("x", I32, (n,)), D.param("y", I32, (n,))
+        r = D.map2(lambda a, b: D.add(D.mul(a, D.const(I32, 3)), b), x, y)
+        return Graph.create("nafold", [("r", r), ("s", D.reduce(D.add, D.const(I32, 7), r))])
+
+    stream = Stream.create()
+    for n, seed in (((1 << 21) + 3, 5), ((1 << 17) + 1, 6)):
+        g = prog(n)
+        roles = [l.split()[2] for l in H.plan(g).splitlines() if l.startswith("kernel")]
+        assert roles == ["map"] + ["reduce_split_fold"] * (2 if n > 1 << 20 else 1), roles
+        r = np.random.default_rng(seed)
+        ins = [("x", r.integers(-1000, 1000, n, dtype=np.int32)), ("y", r.integers(-1000, 1000, n, dtype=np.int32))]
+        c = H.compile(g)
+        res = [(nm, H.upload(v)) for nm, v in ins]
+        want_o, got_o = outputs_of(c), outputs_of(c)
+        try:
+            H.run_resident_into(c, res, want_o, sync=True)
+            live = Buffer.live_count()
+            H.run_resident_noalloc(c, res, got_o, stream.ptr)
+            stream.synchronize()
+            assert Buffer.live_count() == live
+            want = {nm: H.download(o) for nm, o in want_o}
+            got = {nm: H.download(o) for nm, o in got_o}
+            for nm in want:
+                np.testing.assert_array_equal(got[nm], want[nm], err_msg=nm)
+            exp_r = ins[0][1].astype(np.int64) * 3 + ins[1][1]
+            np.testing.assert_array_equal(got["r"], exp_r.astype(np.int32))
+            exp_s = np.array(7 + int(exp_r.sum()), dtype=np.int64).astype(np.int32)  # wrapping int32 sum
+            assert int(got["s"]) == int(exp_s)
+        finally:
+            free_all(res)
+            free_all(want_o)
+            free_all(got_o)
+            c.release()
+
+
 def test_noalloc_rejects_programs_beyond_the_static_scratch(device):
     n, bins = 1 << 23, 1 << 20
     g = program(n, bins)
