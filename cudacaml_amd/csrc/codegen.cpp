@@ -916,7 +916,9 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // Launch-shape knobs for sweeps: CCHIP_TUNE="key=value,key=value". Every
 // key has a default that is the shipped configuration; a knob only changes
-// tile sizes and grid shapes, never what is computed.
+// tile sizes and grid shapes, never what is computed, except that the
+// grouping knobs of float reductions (rr_tree, fuse_reduce) change their
+// last bits within the reduction tolerance.
 int64_t tune(const char *key, int64_t dflt) {
   const char *env = getenv("CCHIP_TUNE");
   if (!env) return dflt;
@@ -1700,16 +1702,17 @@ struct Lowering {
 
   // ---- Reduce root (K2-K4 -> wave / block / split-row reductions) --------
   // Whether the combine (x0, x1) -> body is op(x0, x1) or op(x1, x0) for
-  // an op whose result does not depend on the grouping or order of its
-  // operands.
-  bool any_order(int body, DT dt) const {
+  // an op that may be folded in any grouping: with floats too, one whose
+  // result depends on the grouping only through rounding (add, mul).
+  bool any_order(int body, DT dt, bool floats) const {
     const XNode &x = g.xs[body];
     if (x.kind != XK::Bin || x.a < 0 || x.b < 0) return false;
     const XNode &l = g.xs[x.a], &r = g.xs[x.b];
     if (l.kind != XK::Arg || r.kind != XK::Arg || l.arg == r.arg) return false;
     if (x.op == B_MIN || x.op == B_MAX) return true;
     const bool integer = dt == DT::I32 || dt == DT::I64;
-    return integer && (x.op == B_ADD || x.op == B_MUL || x.op == B_AND || x.op == B_OR || x.op == B_XOR);
+    if (!integer) return floats && (x.op == B_ADD || x.op == B_MUL);
+    return x.op == B_ADD || x.op == B_MUL || x.op == B_AND || x.op == B_OR || x.op == B_XOR;
   }
 
   std::vector<int> lower_reduce(int t) {
@@ -1801,11 +1804,19 @@ struct Lowering {
     }
     ElemFn f = gen.element_fn("f_" + id, n.a, false, true);
     src << f.code;
-    // A combine that gives the same bits in any grouping (max and min,
-    // which propagate NaN and order -0 below +0; wrapping integer add, mul
-    // and bit operations) folds rows as a tree (rr_tree=0: in order).
-    if (rows >= 1024 && !(tune("rr_tree", 1) && any_order(n.body, n.dt)))
-      return lower_rows_seq(t, false, f, cmb, ini, rows, len);
+    // 1024 rows or more fold one lane a row, in order, unless the rows are
+    // long (rr_tree_len) and the combine allows any grouping: max and min
+    // (which propagate NaN and order -0 below +0), wrapping integer add,
+    // mul and bit operations, all bit-exact in any grouping; and float add
+    // and mul, whose tree differs from the in-order fold by rounding only.
+    // Those fold as a tree, a workgroup or a wave a row. A GiB of f32 or
+    // i32 rows, µs in order against as a tree: 8192 long 205-221 / 155,
+    // 2048 long 188-191 / 178, 1000 long 172-176 / 174, 256 long 184-190 /
+    // 198, 64 long 181 / 425. rr_tree=1 folds float rows in order
+    // (bit-identical to the interpreter), rr_tree=0 every row.
+    const int64_t tree = tune("rr_tree", 2);
+    const bool as_tree = tree >= 1 && len >= tune("rr_tree_len", 1024) && any_order(n.body, n.dt, tree >= 2);
+    if (rows >= 1024 && !as_tree) return lower_rows_seq(t, false, f, cmb, ini, rows, len);
     bool vec = len % 4 == 0;
     if (len <= 2048) {
       // One wave (or a power-of-two segment of one) per row.

@@ -1,12 +1,13 @@
 """Seeded random graphs for the two reduction paths that fold in a new
 order: a whole-tensor reduction folded inside the map that writes its input
 (the map's output is also a graph output, and the reduction is the next
-root), and row reductions whose combine gives the same bits in any order
-(max, min; integer add, mul and bit operations), folded as a tree. Random
+root), and row reductions of rows of 1024 elements or more whose combine
+allows any grouping (max, min; integer add, mul and bit operations; float
+add), folded as a tree. Random
 dtypes, light element-wise expressions (tests/fuzz_graphs.py), ragged
 sizes above the fold's 2^16 threshold and non-identity inits, against the
 oracle under the per-output policy: integers and max/min bit-exact, float
-sums within the accumulation band."""
+sums within the accumulation band (row sums also against float64)."""
 
 import numpy as np
 import pytest
@@ -46,14 +47,14 @@ def folded_case(seed):
 def tree_case(seed):
     r = np.random.default_rng(6000 + seed)
     dt = [F32, F64, I32][seed % 3]
-    rows, cols = int(r.choice([1024, 1100, 2048, 3001])), int(r.choice([1, 63, 333, 2049, 5000]))
+    rows, cols = int(r.choice([1024, 1100, 2048, 3001])), int(r.choice([1024, 1031, 2048, 2049, 5000]))
     x = D.param("x", dt, (rows, cols))
-    ops = ["max", "min"] + (["add", "mul", "and"] if dt is I32 else [])
+    ops = ["max", "min", "add"] + (["mul", "and"] if dt is I32 else [])
     op = ops[int(r.integers(len(ops)))]
     comb = {"add": D.add, "max": D.max, "min": D.min, "mul": D.mul, "and": D.bit_and}[op]
-    init = D.const(dt, int(r.integers(-3, 4)) if dt is I32 else float(r.choice([0.0, 0.75, -1.0])))
-    g = Graph.create("tree%d" % seed, [("s", D.reduce_rows(comb, init, x))])
-    return g, [("x", FG._input(r, dt, (rows, cols)))], (dt.name, rows, cols, op)
+    iv = int(r.integers(-3, 4)) if dt is I32 else float(r.choice([0.0, 0.75, -1.0]))
+    g = Graph.create("tree%d" % seed, [("s", D.reduce_rows(comb, D.const(dt, iv), x))])
+    return g, [("x", FG._input(r, dt, (rows, cols)))], (dt.name, rows, cols, op, iv)
 
 
 def _run(g, inputs):
@@ -83,6 +84,13 @@ def test_tree_row_reduction_fuzz(device, seed):
     print("case", seed, *what, flush=True)
     assert "reduce_rowseq" not in templates(g), what
     exp, got = _run(g, inputs)
+    if what[0] != "i32" and what[3] == "add":
+        bad = [v for v in Diff.policy_check(g, exp, got) if not v.ok]
+        assert not bad, (what, bad)
+        e64 = inputs[0][1].astype(np.float64).sum(axis=1) + what[4]
+        d = np.asarray(got[0][1], dtype=np.float64)
+        assert np.all(np.abs(d - e64) <= 1e-4 * (1 + np.abs(e64))), what
+        return
     for (name, e), (_, d) in zip(exp, got):
         # any grouping gives the same bits (no NaN among these inputs)
         np.testing.assert_array_equal(e.view(np.uint8), d.view(np.uint8), err_msg=str(what))

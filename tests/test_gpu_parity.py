@@ -129,14 +129,35 @@ def test_s13_bs_greeks_f64(device):
     diff(g, bs.inputs(F64, seed=7), tolerance=1e-6)
 
 
-def test_config_rows_bit_exact(device):
-    """With >= 1024 rows each row is folded by one lane in the interpreter's
-    order: reduce_rows add/max and scan_rows add are bit-identical."""
+def test_config_rows_bit_exact(device, monkeypatch):
+    """With rr_tree=1 each float row of a 1024-row add reduction is folded
+    by one lane in the interpreter's order: reduce_rows add/max and
+    scan_rows add are bit-identical."""
+    monkeypatch.setenv("CCHIP_TUNE", "rr_tree=1")
     g = C.rows(1024, 8192)
     x = C.uniform_pm1(3, (1024, 8192))
     exp, got = both(g, [("x", x)])
     for (n, e), (_, v) in zip(exp, got):
         np.testing.assert_array_equal(e, v, err_msg=n)
+
+
+def test_config_rows_tree_add(device):
+    """By default the add of 8192-long rows folds as a tree: within the
+    reduction band of the float64 row sums, and no further from them than
+    the oracle's in-order fold (whose own drift, 6.5e-5 of the band here,
+    grows with the row count); the max (the same bits in any grouping) and
+    the row scan (in order) bit for bit."""
+    g = C.rows(1024, 8192)
+    x = C.uniform_pm1(3, (1024, 8192))
+    exp, got = both(g, [("x", x)])
+    exp, got = dict(exp), dict(got)
+    e64 = x.astype(np.float64).sum(axis=1)
+    err = lambda s: np.max(np.abs(np.asarray(s, dtype=np.float64) - e64) / (1 + np.abs(e64)))
+    assert err(got["sum"]) <= 1e-4
+    assert err(got["sum"]) <= err(exp["sum"])
+    assert not np.array_equal(got["sum"], exp["sum"])  # another grouping
+    np.testing.assert_array_equal(got["max"], exp["max"])
+    np.testing.assert_array_equal(got["scan"], exp["scan"])
 
 
 def test_config_global_scan_bit_exact(device):

@@ -131,7 +131,8 @@ def test_uniform_graph_uploads_only_the_seed():
     assert [o for o in ops if o[0] == "upload"] == [("upload", "seed", "p_seed")]
 
 
-@pytest.mark.parametrize("rows,n,tpl", [(8192, 8192, "reduce_rowseq"), (1, 1 << 24, "reduce_split"),
+@pytest.mark.parametrize("rows,n,tpl", [(8192, 8192, "reduce_block"), (8192, 1023, "reduce_rowseq"),
+                                        (8192, 1024, "reduce_wave"), (1, 1 << 24, "reduce_split"),
                                         (600, 4096, "reduce_block"), (64, 64, "reduce_wave")])
 def test_reduce_template_choice(rows, n, tpl):
     x = D.param("x", F32, (rows, n))
@@ -147,8 +148,9 @@ def test_scan_template_choice(rows, n, tpls):
 
 
 def test_config_plans():
-    # the max reduction gives the same bits in any order: a workgroup a row
-    assert [t for _, t in kernels_of(C.rows())] == ["reduce_rowseq", "reduce_block", "scan_rowseq"]
+    # rows of 8192 fold as trees, a workgroup a row (the add within the
+    # rounding of another grouping, the max bit-exact); the scan in order
+    assert [t for _, t in kernels_of(C.rows())] == ["reduce_block", "reduce_block", "scan_rowseq"]
     # the gather back reads the scatter's partition: the table slice by
     # slice from LDS, then each tile's values back in element order; 128
     # slices, so the partition keeps each tile's pairs in the tile's region
