@@ -2023,7 +2023,18 @@ struct Lowering {
     if (rows == 0) return {};
     ElemFn f = gen.element_fn("f_" + id, n.a, false, true);
     src << f.code;
-    if (rows >= 1024) return lower_rows_seq(t, true, f, cmb, ini, rows, len);
+    // 1024 rows or more scan one lane a row, in order, unless the rows are
+    // long (rs_tree_len) and the combine allows any grouping (bit-exact for
+    // max, min and integer ops; float add and mul within rounding): those
+    // take the tile templates below, a workgroup a row, or a look-back
+    // chain of tiles where a row is longer than one tile. 2^28 f32 or i32
+    // elements, µs in order against as tiles: 8192 long 475-480 / 375-381,
+    // 4096 long 427-429 / 340-344, 2048 long 411-430 / 363-373, 1000 long
+    // 501-504 / 538-569, 256 long 401-405 / 1453-1572. rs_tree=0 scans
+    // every row in order (bit-identical to the interpreter).
+    if (rows >= 1024 &&
+        !(tune("rs_tree", 1) && len >= tune("rs_tree_len", 2048) && any_order(n.body, n.dt, true)))
+      return lower_rows_seq(t, true, f, cmb, ini, rows, len);
     bool wide = dt_size(n.dt) == 8;
     if (len <= 64) {
       int64_t S = pow2ceil(len);

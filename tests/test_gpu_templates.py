@@ -64,6 +64,8 @@ SCAN_CASES = [
     (3, 53248, I32, "scan_lookback"),
     (2, 16385, I64, "scan_lookback"),
     (3, 32768, F64, "scan_lookback"),
+    # 1024 rows or more, one lane a row in order (run with rs_tree=0, so at
+    # every length)
     (1024, 333, I32, "scan_rowseq"),
     (2048, 64, F32, "scan_rowseq"),
     (1500, 2050, I64, "scan_rowseq"),
@@ -72,14 +74,49 @@ SCAN_CASES = [
     (1024, 20003, F32, "scan_rowseq"),
     (1030, 9000, I32, "scan_rowseq"),
     (2048, 9001, F64, "scan_rowseq"),
+    # 1024 rows or more of 2048 elements or more (the default): a workgroup
+    # a row, or a look-back chain of tiles a row
+    (1500, 2050, I64, "scan_tile"),
+    (1030, 9000, I32, "scan_tile"),
+    (2048, 9001, F64, "scan_tile"),
+    (1024, 20003, F32, "scan_tile"),
+    (1024, 40000, I32, "scan_lookback"),
+    (1024, 30000, F32, "scan_lookback"),
 ]
 
 
+def check_scans(monkeypatch, g, inputs, tpl, init):
+    """check() for an add scan "p" (and a max scan "q"). The scan_rowseq
+    cases run with rs_tree=0, so the in-order template is the one under
+    test at every length. A float add scan through a tile template is
+    checked against the float64 prefix sums plus init, within the policy's
+    band: over long rows the interpreter's own in-order f32 prefix drifts
+    beyond the band where a prefix is near zero. Everything else against
+    the oracle."""
+    if tpl == "scan_rowseq":
+        monkeypatch.setenv("CCHIP_TUNE", "rs_tree=0")
+    assert tpl in templates(g), (tpl, templates(g))
+    exp = oracle.run(g, inputs)
+    c = H.compile(g)
+    try:
+        got = H.run(c, inputs)
+    finally:
+        c.release()
+    x = inputs[0][1]
+    fl = x.dtype.kind == "f" and tpl != "scan_rowseq"
+    bad = [v for v in Diff.policy_check(g, exp, got) if not v.ok and not (fl and v.name == "p")]
+    assert not bad, bad
+    if fl:
+        p = np.asarray(dict(got)["p"], dtype=np.float64)
+        e = np.cumsum(x.astype(np.float64), axis=1) + init
+        assert np.max(np.abs(p - e) / (1 + np.abs(e))) <= (1e-4 if x.dtype == np.float32 else 1e-12)
+
+
 @pytest.mark.parametrize("rows,n,dtype,tpl", SCAN_CASES, ids=lambda v: str(v))
-def test_scan_variants(device, rows, n, dtype, tpl):
+def test_scan_variants(device, monkeypatch, rows, n, dtype, tpl):
     x = D.param("x", dtype, (rows, n))
     g = Graph.create("scan", [("p", D.scan_rows(D.add, D.const(dtype, 0), x))])
-    check(g, [("x", data(dtype, (rows, n), 11))], [tpl])
+    check_scans(monkeypatch, g, [("x", data(dtype, (rows, n), 11))], tpl, 0)
 
 
 REDUCE_CASES = [
@@ -148,11 +185,11 @@ def test_reduce_init_applied_once(device, rows, n, dtype, tpl):
 
 
 @pytest.mark.parametrize("rows,n,dtype,tpl", SCAN_CASES, ids=lambda v: str(v))
-def test_scan_init_applied_once(device, rows, n, dtype, tpl):
+def test_scan_init_applied_once(device, monkeypatch, rows, n, dtype, tpl):
     x = D.param("x", dtype, (rows, n))
     g = Graph.create("scan", [("p", D.scan_rows(D.add, D.const(dtype, 7), x)),
                               ("q", D.scan_rows(D.max, D.const(dtype, 2), x))])
-    check(g, [("x", data(dtype, (rows, n), 15))], [tpl])
+    check_scans(monkeypatch, g, [("x", data(dtype, (rows, n), 15))], tpl, 7)
 
 
 FOLDED_CASES = [((1 << 16) + 3, F32, "add"), ((1 << 22) + 5, F32, "add"), ((1 << 20) + 2, F64, "add"),
@@ -234,9 +271,9 @@ def test_reduce_empty_rows(device):
 
 
 def test_scan_rows_exact_order_f32(device, monkeypatch):
-    """Row-sequential scans, and with rr_tree=1 row sums, fold in the
+    """With rs_tree=0 row scans, and with rr_tree=1 row sums, fold in the
     interpreter's order: bit-exact f32."""
-    monkeypatch.setenv("CCHIP_TUNE", "rr_tree=1")
+    monkeypatch.setenv("CCHIP_TUNE", "rr_tree=1,rs_tree=0")
     x = D.param("x", F32, (2048, 3000))
     g = Graph.create("s", [("p", D.scan_rows(D.add, D.const(F32, 0.0), x)),
                            ("s", D.reduce_rows(D.add, D.const(F32, 0.0), x))])
@@ -606,7 +643,7 @@ KNOB_CASES = [
     ("scatter_slice_bins=8192", lambda: scatter_graph(300001, 70000, F32),
      lambda: [("idx", scatter_idx(51, 300001, 70000)), ("src", data(F32, (300001,), 52))], "scatter_partition"),
     ("rs_groups=512", lambda: C.rows(8192, 1000), lambda: [("x", data(F32, (8192, 1000), 77))], "scan_rowseq"),
-    ("rs_bytes=8192,rs_groups=64", lambda: C.rows(1024, 3000),
+    ("rs_tree=0,rs_bytes=8192,rs_groups=64", lambda: C.rows(1024, 3000),
      lambda: [("x", data(F32, (1024, 3000), 53))], "scan_rowseq"),
     ("mm_splitk_groups=7", lambda: C.matmul(3, F64, k=65536, m=3),
      lambda: [("a", data(F64, (3, 65536), 54)), ("b", data(F64, (65536, 3), 55))], "matmul_splitk"),
@@ -615,16 +652,16 @@ KNOB_CASES = [
      lambda: [("x", data(I32, (2, 300004), 57))], "scan_lookback"),
     ("scan_nt=1", lambda: Graph.create("s", [("p", D.scan_rows(D.add, D.const(I64, 0), D.param("x", I64, (1, 200000))))]),
      lambda: [("x", data(I64, (1, 200000), 58))], "scan_lookback"),
-    ("rs_nt=0", lambda: C.rows(1024, 3000), lambda: [("x", data(F32, (1024, 3000), 59))], "scan_rowseq"),
+    ("rs_tree=0,rs_nt=0", lambda: C.rows(1024, 3000), lambda: [("x", data(F32, (1024, 3000), 59))], "scan_rowseq"),
     ("rs_nt=2", lambda: C.rows(2048, 1000), lambda: [("x", data(F32, (2048, 1000), 60))], "reduce_rowseq"),
     ("rr_tree=1,rr_bytes=16384,rr_groups=64", lambda: C.rows(1500, 2001),
      lambda: [("x", data(F32, (1500, 2001), 61))], "reduce_rowseq"),
     # two tiles in flight: an odd tile count with a ragged last tile
-    ("rs_depth=2,rs_bytes=4096,rr_depth=2,rr_bytes=16384", lambda: C.rows(1024, 3000),
+    ("rs_tree=0,rs_depth=2,rs_bytes=4096,rr_depth=2,rr_bytes=16384", lambda: C.rows(1024, 3000),
      lambda: [("x", data(F32, (1024, 3000), 62))], "scan_rowseq"),
-    ("rr_tree=1,rr_depth=2,rr_bytes=16384", lambda: C.rows(2048, 5003),
+    ("rs_tree=0,rr_tree=1,rr_depth=2,rr_bytes=16384", lambda: C.rows(2048, 5003),
      lambda: [("x", data(F32, (2048, 5003), 63))], "reduce_rowseq"),
-    ("rs_chunk=4,rr_chunk=128", lambda: C.rows(1024, 3000), lambda: [("x", data(F32, (1024, 3000), 64))], "scan_rowseq"),
+    ("rs_tree=0,rs_chunk=4,rr_chunk=128", lambda: C.rows(1024, 3000), lambda: [("x", data(F32, (1024, 3000), 64))], "scan_rowseq"),
     # long rows folded in order: floats bit-identical to the interpreter,
     # integers too (rows of four tiles or more, split roles, and a last
     # workgroup past the rows); rows just below and at the tree's length
@@ -640,13 +677,13 @@ KNOB_CASES = [
      lambda: [("x", data(I32, (1030, 30000), 62))], "reduce_rowseq"),
     # one workgroup folding and loading in turn for the scan, split roles for
     # the reductions (the defaults the other way round), and split f64 ones
-    ("rs_split=0,rr_split=1", lambda: C.rows(1024, 20003), lambda: [("x", data(F32, (1024, 20003), 98))], "scan_rowseq"),
+    ("rs_tree=0,rs_split=0,rr_split=1", lambda: C.rows(1024, 20003), lambda: [("x", data(F32, (1024, 20003), 98))], "scan_rowseq"),
     ("rr_tree=1,rr_split=1", lambda: (lambda x: Graph.create("r", [("s", D.reduce_rows(D.add, D.const(F64, 1.5), x)),
                                                         ("m", D.reduce_rows(D.max, D.const(F64, 0.25), x))]))(
         D.param("x", F64, (4096, 5000))),
      lambda: [("x", data(F64, (4096, 5000), 99))], "reduce_rowseq"),
     # tiles of a non-power-of-two width (384 and 1536 columns)
-    ("rs_bytes=6144,rr_bytes=24576", lambda: C.rows(1024, 3000),
+    ("rs_tree=0,rs_bytes=6144,rr_bytes=24576", lambda: C.rows(1024, 3000),
      lambda: [("x", data(F32, (1024, 3000), 96))], "scan_rowseq"),
     ("lb_buf=0", lambda: Graph.create("s", [("p", D.scan_rows(D.add, D.const(I32, 2), D.param("x", I32, (3, 100001))))]),
      lambda: [("x", data(I32, (3, 100001), 65))], "scan_lookback"),

@@ -140,7 +140,8 @@ def test_reduce_template_choice(rows, n, tpl):
     assert got == ([tpl, "reduce_split_fold"] if tpl == "reduce_split" else [tpl])
 
 
-@pytest.mark.parametrize("rows,n,tpls", [(8192, 8192, ["scan_rowseq"]), (1, 1 << 28, ["scan_init", "scan_lookback"]),
+@pytest.mark.parametrize("rows,n,tpls", [(8192, 8192, ["scan_tile"]), (8192, 2047, ["scan_rowseq"]),
+                                         (1024, 40000, ["scan_init", "scan_lookback"]), (1, 1 << 28, ["scan_init", "scan_lookback"]),
                                          (100, 5000, ["scan_tile"]), (100, 50, ["scan_wave"])])
 def test_scan_template_choice(rows, n, tpls):
     x = D.param("x", I32, (rows, n))
@@ -148,9 +149,9 @@ def test_scan_template_choice(rows, n, tpls):
 
 
 def test_config_plans():
-    # rows of 8192 fold as trees, a workgroup a row (the add within the
-    # rounding of another grouping, the max bit-exact); the scan in order
-    assert [t for _, t in kernels_of(C.rows())] == ["reduce_block", "reduce_block", "scan_rowseq"]
+    # rows of 8192 fold as trees, a workgroup a row (the adds within the
+    # rounding of another grouping, the max bit-exact)
+    assert [t for _, t in kernels_of(C.rows())] == ["reduce_block", "reduce_block", "scan_tile"]
     # the gather back reads the scatter's partition: the table slice by
     # slice from LDS, then each tile's values back in element order; 128
     # slices, so the partition keeps each tile's pairs in the tile's region
