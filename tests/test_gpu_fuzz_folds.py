@@ -97,3 +97,40 @@ def test_tree_row_reduction_fuzz(device, seed):
     for (name, e), (_, d) in zip(exp, got):
         # any grouping gives the same bits (no NaN among these inputs)
         np.testing.assert_array_equal(e.view(np.uint8), d.view(np.uint8), err_msg=str(what))
+
+
+def scan_case(seed):
+    r = np.random.default_rng(7000 + seed)
+    dt = [F32, F64, I32][seed % 3]
+    rows, cols = int(r.choice([1024, 1100])), int(r.choice([2048, 2049, 5000, 9001, 30000]))
+    x = D.param("x", dt, (rows, cols))
+    ops = ["max", "min", "add", "mul"] + (["xor"] if dt is I32 else [])
+    op = ops[int(r.integers(len(ops)))]
+    comb = {"add": D.add, "max": D.max, "min": D.min, "mul": D.mul, "xor": D.bit_xor}[op]
+    iv = int(r.integers(-3, 4)) if dt is I32 else float(r.choice([0.0, 0.75, -1.0]))
+    g = Graph.create("tscan%d" % seed, [("p", D.scan_rows(comb, D.const(dt, iv), x))])
+    return g, [("x", FG._input(r, dt, (rows, cols)))], (dt.name, rows, cols, op, iv)
+
+
+@pytest.mark.parametrize("seed", range(N_CASES))
+def test_tile_row_scan_fuzz(device, seed):
+    """Scans of 1024 rows or more of 2048 elements or more, whose combine
+    allows any grouping, run as tile scans (a workgroup a row, or a
+    look-back chain of tiles): integers, max and min bit-exact against the
+    oracle; float add and mul within the policy's band, add also against
+    the float64 prefix sums."""
+    g, inputs, what = scan_case(seed)
+    print("case", seed, *what, flush=True)
+    t = templates(g)
+    assert "scan_rowseq" not in t and ("scan_tile" in t or "scan_lookback" in t), (what, t)
+    exp, got = _run(g, inputs)
+    if what[0] != "i32" and what[3] in ("add", "mul"):
+        bad = [v for v in Diff.policy_check(g, exp, got) if not v.ok]
+        assert not bad, (what, bad)
+        if what[3] == "add":
+            e64 = np.cumsum(inputs[0][1].astype(np.float64), axis=1) + what[4]
+            d = np.asarray(got[0][1], dtype=np.float64)
+            assert np.all(np.abs(d - e64) <= 1e-4 * (1 + np.abs(e64))), what
+        return
+    for (name, e), (_, d) in zip(exp, got):
+        np.testing.assert_array_equal(e.view(np.uint8), d.view(np.uint8), err_msg=str(what))
