@@ -669,6 +669,11 @@ KNOB_CASES = [
      lambda: [("x", data(F32, (1024, 20003), 60))], "reduce_rowseq"),
     ("rr_tree_len=2048", lambda: Graph.create("r", [("s", D.reduce_rows(D.max, D.const(I32, 3), D.param("x", I32, (1500, 2047))))]),
      lambda: [("x", data(I32, (1500, 2047), 63))], "reduce_rowseq"),
+    # the tile scans' row length, both ways
+    ("rs_tree_len=4096", lambda: Graph.create("s", [("p", D.scan_rows(D.max, D.const(I32, -7), D.param("x", I32, (1100, 3000))))]),
+     lambda: [("x", data(I32, (1100, 3000), 65))], "scan_rowseq"),
+    ("rs_tree_len=512", lambda: Graph.create("s", [("p", D.scan_rows(D.add, D.const(I32, 2), D.param("x", I32, (1030, 1000))))]),
+     lambda: [("x", data(I32, (1030, 1000), 66))], "scan_tile"),
     ("rr_tree_len=64", lambda: Graph.create("r", [("s", D.reduce_rows(D.add, D.const(F32, 1.0), D.param("x", F32, (2000, 64))))]),
      lambda: [("x", data(F32, (2000, 64), 64))], "reduce_wave"),
     ("rr_tree=0", lambda: Graph.create("r", [("s", D.reduce_rows(D.add, D.const(I32, 5), D.param("x", I32, (1030, 30000))))]),
