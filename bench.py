@@ -7,14 +7,16 @@ on, config 2 (row ops): reduce_rows(add), reduce_rows(max) and
 scan_rows(add) over an f32 [8192; 8192] matrix, plus an inclusive scan of
 an i32 vector of 2^28 elements. One step is one run of both compiled
 programs over inputs already resident in HBM (run_resident_into, outputs
-preallocated, no host traffic). ``value`` is algorithmic bytes per second
-over the K timed steps (each materialised input read once, each output
-written once, per root of the fusion plan). Where the lowering folds a
-whole-tensor reduction inside the map that writes its input (config 1's
-s = sum r), that read of r is still counted though no kernel moves it, so
-config 1's ``value`` is the plan's bytes per second, not HBM traffic (the
-dominant kernel's ``roofline`` is per kernel and unaffected); ``config``
-gives both ``algorithmic_bytes_per_step`` and ``moved_bytes_per_step``.
+preallocated, no host traffic). ``value`` is HBM bytes per second over
+the K timed steps: the bytes the step's kernels read and write of
+materialised tensors, each tensor a kernel reads counted once
+(``config.moved_bytes_per_step``; scratch excluded). It is checked
+against the 8 TB/s peak before the line is printed. The fusion plan's own
+algorithmic total (each root's inputs read once and output written once,
+counting reads the lowering removed: the read of r by config 1's s = sum r,
+folded inside r's map; the second and third reads of x by config 2's
+sibling row roots, fused into one kernel) is
+``config.plan_bytes_per_step``, and its rate ``config.plan_gbs``.
 Other configs (``--config saxpy``,
 ``chain``, ``scatter``, ``scatter_perm``, ``matmul``, ``matmul64``, ``matmul_grad``,
 ``mc``, ``mc64``, ``mc_greeks``) print their own line in the same format;
@@ -26,7 +28,8 @@ whose inputs cannot stay in the 256 MB MALL between steps (config 1's
 elements; their ``value`` is GFLOP/s with the input resident, and their
 ``whole_run`` carries the reference's RESULT fields (saxpy and poly whole
 runs, best of 5, and the host-device copy rates) beside its published
-A100 figures.
+A100 figures; ``--pinned`` runs them from page-locked host memory, as the
+reference's own flag does.
 ``bs``, ``bs_greeks`` (and their f64 ``bs64``, ``bs_greeks64``) are the
 reference's S20 timing row: the one-step Black-Scholes price and its
 Greeks adjoint at 2^22 paths; their ``whole_run`` is timed as S20 times it
@@ -61,35 +64,21 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def folded_reads(H, graph):
-    """Bytes of the plan's algorithmic total that no kernel moves: a
-    whole-tensor reduction folded inside the map that writes its input
-    keeps its root's bytes (the input read once, one value written) on its
-    last fold kernel, but reads nothing back. Such a fold is the only
-    reduce_split_fold that carries bytes (a split reduction's fold carries
-    none); its input read is those bytes less the one output value."""
-    sizes, kern = {}, []
-    for line in H.plan(graph).splitlines():
-        f = line.split()
-        if f[0] == "buffer":
-            sizes[f[1]] = int(f[4]) * (8 if f[3] in ("f64", "i64") else 4)
-        elif f[0] == "kernel" and f[2] == "reduce_split_fold":
-            b = int(f[f.index("bytes") + 1])
-            if b > 0:
-                kern.append((b, f[-1]))
-    return sum(b - sizes.get(o, 0) for b, o in kern)
-
-
 def plan_bytes(H, graph):
-    """Algorithmic bytes of every kernel of the plan, as the code generator
-    attributes them: each element a root reads counted once (a gather one
-    element per output, a broadcast source one), its output written once,
-    on the root's main kernel; helper kernels carry 0."""
+    """Per kernel of the plan, as the code generator attributes them:
+    (template, root bytes, moved bytes). Root bytes are the fusion plan's
+    algorithmic bytes of the root the kernel computes: each element the
+    root reads counted once (a gather one element per output, a broadcast
+    source one), its output written once. Moved bytes are what the kernel
+    itself reads and writes of materialised tensors, each tensor read once:
+    the root bytes, less reads the lowering removed (a reduction folded
+    inside the map that writes its input reads nothing back; row roots over
+    one input fused into one kernel read it once). Helper kernels carry 0."""
     out = {}
     for line in H.plan(graph).splitlines():
         f = line.split()
         if f[0] == "kernel":
-            out[f[1]] = (f[2], int(f[f.index("bytes") + 1]))
+            out[f[1]] = (f[2], int(f[f.index("bytes") + 1]), int(f[f.index("moved") + 1]))
     return out
 
 
@@ -155,8 +144,8 @@ def build_workload(name, H, C):
         if name.startswith("saxpy"):
             y = device_inputs(H, C.gen_uniform_pm1((n,)), 2)
             add(C.saxpy(n), [("x", x), ("y", y)])
-            desc = ("config1: saxpy r=2x+y, s=sum r over f32[%s]; s is folded inside r's map kernel, so the "
-                    "plan's read of r by the reduction (counted in value) is not moved" % what)
+            desc = ("config1: saxpy r=2x+y, s=sum r over f32[%s]; s is folded inside r's map kernel, so "
+                    "r is never read back" % what)
         else:
             add(C.chain(n), [("x", x)])
             desc = "config1b: 5-map chain over f32[%s], one fused kernel" % what
@@ -188,9 +177,12 @@ def build_workload(name, H, C):
         g = C.mc_greeks() if name == "mc_greeks" else C.mc_paths(C.PATHS5, C.STEPS5, dt)
         ins = [(k, H.upload(v)) for k, v in bs.inputs(dt, seed=7)]
         add(g, ins)
-        return Workload(name, progs, "paths/s", dt.name,
-                        "config5: BS MC %s 2^22 paths x 64 steps %s" % ("greeks" if name == "mc_greeks" else "price",
-                                                                        dt.name))
+        desc = "config5: BS MC %s 2^22 paths x 64 steps %s" % ("greeks" if name == "mc_greeks" else "price", dt.name)
+        if dt is F32:
+            desc += ("; at seed 7 about 12 of the 2^28 f32 draws are +-inf under the reference's own f32 generator "
+                     "(rng.ml:61-71: u rounds to 1.0 in f32), so the price is +inf and the Greeks NaN, "
+                     "as the interpreter gives them")
+        return Workload(name, progs, "paths/s", dt.name, desc)
     if name in ("poly", "poly64"):
         from cudacaml_amd.examples import refbench as RB
 
@@ -219,16 +211,24 @@ BS_CONFIGS = ("bs", "bs64", "bs_greeks", "bs_greeks64")
 BS_PUBLISHED_MS = {"bs": 0.2, "bs_greeks": 0.7}
 
 
-def refbench_whole_runs(H, dt, reps=5):
+# The reference's published host-transfer rates on the A100: a 64 MiB
+# round trip, pinned against pageable (README.md:198-201, S18).
+PUBLISHED_A100_COPY_GBS = {"pinned": 12.3, "pageable": 4.8}
+
+
+def refbench_whole_runs(H, dt, reps=5, pinned=False):
     """The reference benchmark's RESULT fields (bench/bench.ml:227-300),
     measured as it measures them: best of ``reps`` whole runs (upload,
-    launches, download; pageable host memory) of saxpy and poly after one
-    warm run, and the 2^24-element host-to-device and device-to-host copy
-    rates."""
+    launches, download) of saxpy and poly after one warm run, and the
+    2^24-element host-to-device and device-to-host copy rates. With
+    ``pinned`` (the reference's --pinned, bench/bench.ml:126-145) the
+    inputs and the copy sink are page-locked host memory (Pinned.alloc),
+    so the copies DMA straight from and into them; the run's outputs are
+    fresh host values either way, as Backend.run returns them."""
     import numpy as np
 
     from cudacaml_amd.examples import refbench as RB
-    from cudacaml_amd.runtime import Buffer
+    from cudacaml_amd.runtime import Buffer, Pinned
 
     def best(f):
         t = math.inf
@@ -240,8 +240,12 @@ def refbench_whole_runs(H, dt, reps=5):
 
     n = RB.N
     x, y = RB.x_input(n, dt), RB.y_input(n, dt)
-    buf = Buffer.alloc(x.nbytes)
     sink = np.empty_like(x)
+    if pinned:
+        x, y = Pinned.of_value(x), Pinned.of_value(y)
+        sink = Pinned.alloc(dt, x.shape)
+        assert Pinned.is_pinned(x) and Pinned.is_pinned(y) and Pinned.is_pinned(sink)
+    buf = Buffer.alloc(x.nbytes)
     buf.upload(x)
     t_h2d = best(lambda: buf.upload(x))
     t_d2h = best(lambda: buf.download(sink))
@@ -257,7 +261,9 @@ def refbench_whole_runs(H, dt, reps=5):
     return {"saxpy_cuda_s": round(t_saxpy, 5), "poly_cuda_s": round(t_poly, 5),
             "poly_gflops": round(n * RB.poly_flops() / t_poly / 1e9, 2),
             "h2d_gbs": round(x.nbytes / t_h2d / 1e9, 2), "d2h_gbs": round(x.nbytes / t_d2h / 1e9, 2),
-            "hostmem": "pageable", "n": n, "reps": reps}
+            "hostmem": "pinned" if pinned else "pageable", "n": n, "reps": reps,
+            "published_a100_copy_gbs": {"value": PUBLISHED_A100_COPY_GBS["pinned" if pinned else "pageable"],
+                                        "what": "64 MiB host transfer on the A100, README.md:198-201"}}
 
 
 def step(H, w, sync=False):
@@ -304,7 +310,7 @@ def cpu_baseline(name, C, H, w):
         return [(n, H.download(r)) for n, r in w.programs[k][2]]
 
     def plan_total(g):
-        return sum(b for _, (_, b) in plan_bytes(H, g).items())
+        return sum(b for _, (_, b, _) in plan_bytes(H, g).items())
 
     if name in ("poly", "poly64"):
         from cudacaml_amd.examples import refbench as RB
@@ -507,27 +513,29 @@ def kernel_elements(H, w, kernel):
 
 
 def kernel_table(H, w):
+    """{kernel: (template, moved bytes, compiled, root bytes)} over the
+    workload's programs."""
     kinfo = {}
     for g, c, _, _ in w.programs:
-        for k, (role, b) in plan_bytes(H, g).items():
-            kinfo[k] = (role, b, c)
+        for k, (role, b, m) in plan_bytes(H, g).items():
+            kinfo[k] = (role, m, c, b)
     return kinfo
 
 
 def dominant(H, w, config, timed=True):
-    """Of the kernels that carry a root's algorithmic bytes, the one that
-    takes the most time per step (one timed step per kernel, HIP events
-    around its launches), or, without timing, the one with the most bytes
-    (the matmul for matmul configs): (name, role, bytes, compiled, table).
-    Helper kernels (a scatter's counts and accumulate, a split reduction's
-    fold) carry no bytes of their own, so no roofline can be put on them;
-    the profiles list their times."""
+    """Of the kernels that move a root's bytes, the one that takes the most
+    time per step (one timed step per kernel, HIP events around its
+    launches), or, without timing, the one with the most bytes (the matmul
+    for matmul configs): (name, role, moved bytes, compiled, root bytes,
+    table). Helper kernels (a scatter's counts and accumulate, a split
+    reduction's fold) carry no bytes of their own, so no roofline can be put
+    on them; the profiles list their times."""
     kinfo = kernel_table(H, w)
     if timed:
         from cudacaml_amd.runtime import Device
 
         best, best_ms = None, -1.0
-        for k, (role, b, c) in kinfo.items():
+        for k, (role, b, c, _) in kinfo.items():
             if b <= 0:
                 continue
             H.time_kernel(c, k)
@@ -580,6 +588,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
     ap.add_argument("--no-whole-run", action="store_true", help="skip the host-to-host run timing")
+    ap.add_argument("--pinned", action="store_true",
+                    help="poly/poly64: page-locked host memory for the whole runs (the reference's --pinned)")
     ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -612,7 +622,7 @@ def main():
     for _ in range(args.warmup):
         step(H, w)
     Device.synchronize()
-    dom, dom_role, dom_bytes, dom_c, kinfo = dominant(H, w, args.config)
+    dom, dom_role, dom_bytes, dom_c, dom_root_bytes, kinfo = dominant(H, w, args.config)
     traffic, traffic_detail = traffic_of(counters, dom)
     log("traffic:", traffic, traffic_detail)
     Device.synchronize()
@@ -628,9 +638,14 @@ def main():
     step(H, w, sync=True)  # surfaces any device-side error of the timed runs
 
     ms_per_step = elapsed * 1e3 / args.steps
-    total_bytes = sum(b for _, (_, b, _) in kinfo.items())
+    plan_total = sum(rb for _, (_, _, _, rb) in kinfo.items())
+    moved_total = sum(m for _, (_, m, _, _) in kinfo.items())
     if w.unit == "GB/s":
-        value = total_bytes * args.steps / elapsed / 1e9
+        # HBM bytes the step's kernels read and write (inputs resident)
+        value = moved_total * args.steps / elapsed / 1e9
+        if value > HBM_PEAK_GBS:
+            raise SystemExit("bench.py: %.1f GB/s is above the %.0f GB/s HBM peak: the moved bytes of %s "
+                             "overcount what its kernels read and write" % (value, HBM_PEAK_GBS, args.config))
     elif w.unit == "TFLOP/s":
         flops = 0
         for g, c, _, _ in w.programs:
@@ -699,6 +714,8 @@ def main():
     roof["kernel"] = dom
     roof["template"] = dom_role
     roof["algorithmic_bytes"] = dom_bytes
+    if dom_root_bytes != dom_bytes:
+        roof["root_bytes"] = dom_root_bytes
     roof["launches"] = len(each)
     roof["launch_ms"] = round(dom_avg_ms, 4)
     if each:
@@ -723,7 +740,7 @@ def main():
         from cudacaml_amd.ir import F32, F64
 
         dts = "f64" if args.config == "poly64" else "f32"
-        whole = refbench_whole_runs(H, F64 if dts == "f64" else F32)
+        whole = refbench_whole_runs(H, F64 if dts == "f64" else F32, pinned=args.pinned)
         whole["what"] = ("the reference benchmark's RESULT fields, measured as bench/bench.ml:227-300 does: "
                          "best of 5 whole runs, host arrays in and out")
         pub = RB.PUBLISHED_A100[dts]
@@ -757,8 +774,9 @@ def main():
         "vs_baseline": vs_baseline,
         "dtype": w.dtype,
         "data": "synthetic (Philox-4x32-10 inputs generated on the device)",
-        "config": {"workload": w.describe, "parallelism": "single GPU", "algorithmic_bytes_per_step": total_bytes,
-                   "moved_bytes_per_step": total_bytes - sum(folded_reads(H, g) for g, _, _, _ in w.programs)},
+        "config": {"workload": w.describe, "parallelism": "single GPU", "moved_bytes_per_step": moved_total,
+                   "plan_bytes_per_step": plan_total,
+                   "plan_gbs": round(plan_total * args.steps / elapsed / 1e9, 2)},
         "roofline": roof,
         "cpu_baseline": cpu,
         "whole_run": whole,

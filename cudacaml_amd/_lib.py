@@ -84,7 +84,8 @@ SIGNATURES = {
     "cchip_job_free": (c_int, [c_vp]),
     "cchip_program_run_resident": (c_int, [c_vp, c_int, P(c_cp), P(c_vp), P(c_size), P(c_vp)]),
     "cchip_program_run_resident_into": (c_int, [c_vp, c_int, P(c_cp), P(c_vp), P(c_size), P(c_vp), c_int]),
-    "cchip_program_run_resident_noalloc": (c_int, [c_vp, c_int, P(c_cp), P(c_vp), P(c_size), P(c_vp), c_vp]),
+    "cchip_program_run_resident_noalloc": (c_int, [c_vp, c_int, P(c_cp), P(c_vp), P(c_size), P(c_vp), c_vp, c_vp]),
+    "cchip_error_word_status": (c_int, [c_int]),
     "cchip_program_stream": (c_int, [c_vp, c_int, P(c_vp)]),
     "cchip_program_time_kernel": (c_int, [c_vp, c_cp]),
     "cchip_program_timing": (c_int, [c_vp, P(c_int), P(ctypes.c_double)]),

@@ -309,17 +309,30 @@ def run_resident_into(c, inputs, outputs, sync=True):
     check(lib().cchip_program_run_resident_into(c.handle, n, names, ptrs, sizes, arr, 1 if sync else 0))
 
 
-def run_resident_noalloc(c, inputs, outputs, stream=None):
+def run_resident_noalloc(c, inputs, outputs, stream=None, err=None):
     """Extension (no reference counterpart), for callers that cannot
     allocate device memory: ``run_resident_into`` without synchronising, on
     ``stream`` (a raw HIP stream pointer; None is the default stream), with
     the template scratch taken from the library's static 32 MiB array.
-    Only issues the work: synchronise the stream before reading outputs."""
+    Only issues the work: synchronise the stream before reading outputs.
+    ``err``, a device buffer of at least 4 bytes the caller owns, receives
+    this call's device-side error word (0: none; ``raise_error_word``
+    turns it into the exception a synchronous run raises); without it the
+    call's index errors are dropped, never reported by another run."""
     if c.released:
         raise RuntimeError("Executor.run_resident: this executor has been released")
     n, names, ptrs, sizes = _bind_resident(c, inputs, "Executor.run_resident")
     arr = _bind_outputs(c, outputs)
-    check(lib().cchip_program_run_resident_noalloc(c.handle, n, names, ptrs, sizes, arr, stream))
+    if err is not None and err.nbytes < 4:
+        raise ValueError("run_resident_noalloc: the error buffer needs 4 bytes")
+    check(lib().cchip_program_run_resident_noalloc(c.handle, n, names, ptrs, sizes, arr, stream,
+                                                   None if err is None else err.ptr))
+
+
+def raise_error_word(code):
+    """Raise what a synchronous run raises for the device error flags
+    ``code`` (an allocation-free call's error word); nothing for 0."""
+    check(lib().cchip_error_word_status(int(code)))
 
 
 def time_kernel(c, kernel_name):

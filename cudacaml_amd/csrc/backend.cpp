@@ -300,6 +300,16 @@ void queue_err_read(cchip_program *p, Executor &e, int *slot) {
   queue_err_reset(p, e);
 }
 
+// A run that failed after some of its work was queued: wait for that work,
+// then clear the lane's error word, so that flags its kernels may have set
+// are not reported by the next run on the lane.
+void discard_err(cchip_program *p, Executor &e) {
+  (void)hipStreamSynchronize(e.stream);
+  if (p->ir.err_buf < 0 || p->ir.err_buf >= (int)e.bufs.size()) return;
+  if (hipMemsetAsync(e.bufs[p->ir.err_buf], 0, sizeof(int), e.stream) == hipSuccess)
+    (void)hipStreamSynchronize(e.stream);
+}
+
 // After the run's stream has been waited on: raise the interpreter's error
 // for the flags its slot received.
 void raise_err_slot(cchip_program *p, int *slot) {
@@ -411,19 +421,22 @@ void run_resident_impl(cchip_program *p, int n, const char *const *names, void *
       raise_err_slot(p, e.err_host);
     }
   } catch (...) {
-    if (sync) (void)hipStreamSynchronize(e.stream);
+    if (sync) discard_err(p, e);
     for (void *f : fresh) rt_free(f);
     throw;
   }
 }
 
-// Host-side layout of an allocation-free run, fixed at compile time:
-// scratch buffers packed 256-byte aligned into the static scratch, in
-// buffer order (all of them at once, as the pool holds them).
+// Host-side layout of an allocation-free run, fixed at compile time: the
+// call's own error word in the first 256 bytes of the static scratch (every
+// program has the slot, so a caller's err_out always receives a defined
+// word), then the scratch buffers packed 256-byte aligned, in buffer order
+// (all of them at once, as the pool holds them).
 void prepare_noalloc(cchip_program *p) {
   const ProgramIR &ir = p->ir;
   p->na_off.assign(ir.bufs.size(), -1);
-  int64_t at = 0;
+  if (ir.err_buf >= 0) p->na_off[ir.err_buf] = 0;
+  int64_t at = 256;
   for (size_t b = 0; b < ir.bufs.size(); b++)
     if (ir.bufs[b].role == BufRole::Scratch) {
       p->na_off[b] = at;
@@ -605,10 +618,16 @@ int cchip_program_run(cchip_program *p, int n, const char *const *names, const v
   return guarded([&] {
     std::lock_guard<std::mutex> lk(p->mu);
     DeviceGuard dg(p->device);
-    issue_host_run(p, 0, n, names, host, bytes, outputs, true, p->execs.empty() ? nullptr : p->execs[0].err_host);
-    Executor &e = p->execs[0];
-    check_hip(hipStreamSynchronize(e.stream), "hipStreamSynchronize");
-    finish_staged(p, e, outputs);
+    try {
+      issue_host_run(p, 0, n, names, host, bytes, outputs, true, p->execs.empty() ? nullptr : p->execs[0].err_host);
+      check_hip(hipStreamSynchronize(p->execs[0].stream), "hipStreamSynchronize");
+    } catch (const InvalidArgument &) {
+      throw;  // a caller mistake, found before any device work
+    } catch (...) {
+      if (!p->released && !p->execs.empty()) discard_err(p, p->execs[0]);
+      throw;
+    }
+    finish_staged(p, p->execs[0], outputs);
   });
 }
 
@@ -626,9 +645,14 @@ int cchip_program_run_async(cchip_program *p, int n, const char *const *names, c
       issue_host_run(p, lane, n, names, host, bytes, outputs, false, j->err);
       check_hip(hipEventCreateWithFlags(&j->done, hipEventDisableTiming), "hipEventCreate");
       check_hip(hipEventRecord(j->done, p->execs[lane].stream), "hipEventRecord");
+    } catch (const InvalidArgument &) {
+      // a caller mistake, found before any device work
+      err_slot_put(j->err);
+      throw;
     } catch (...) {
-      // work already queued may still write the slot: let it land first
-      (void)hipStreamSynchronize(p->execs[lane].stream);
+      // work already queued may still write the slot: let it land first,
+      // and leave the lane's word clear for the next job
+      discard_err(p, p->execs[lane]);
       err_slot_put(j->err);
       if (j->done) (void)hipEventDestroy(j->done);
       throw;
@@ -689,7 +713,7 @@ int cchip_program_run_resident_into(cchip_program *p, int n, const char *const *
 }
 
 int cchip_program_run_resident_noalloc(cchip_program *p, int n, const char *const *names, void *const *dev_inputs,
-                                       const size_t *bytes, void *const *dev_outputs, void *stream) {
+                                       const size_t *bytes, void *const *dev_outputs, void *stream, int *err_out) {
   return guarded([&] {
     std::lock_guard<std::mutex> lk(p->mu);
     if (p->released) throw Failure("Executor.run_resident: this executor has been released");
@@ -741,6 +765,16 @@ int cchip_program_run_resident_noalloc(cchip_program *p, int n, const char *cons
         check_hip(hipMemcpyAsync(dev_outputs[o], p->na_ptr[ir.outputs[o].buf], nb, hipMemcpyDeviceToDevice, st),
                   "copy_device");
     }
+    // this call's error word (the first word of the static scratch, cleared
+    // above with the rest), for the caller to read after synchronising
+    if (err_out)
+      check_hip(hipMemcpyAsync(err_out, base, sizeof(int), hipMemcpyDeviceToDevice, st), "copy error word");
+  });
+}
+
+int cchip_error_word_status(int code) {
+  return guarded([&] {
+    if (code) throw InvalidArgument(err_message(code));
   });
 }
 

@@ -1306,6 +1306,9 @@ struct Lowering {
       if (!helper) main = k;
     }
     prog.kernels[main].algo_bytes = bytes;
+    // a reduction folded inside its input's map reads only the partials
+    // (scratch): it moves its output alone
+    prog.kernels[main].moved_bytes = n.kind == TK::Reduce && fused_part_of_red.count(r) ? out : bytes;
   }
 
   // ---- element-wise root (K1 -> vectorised map, one 16-byte group a lane) ---
@@ -4596,7 +4599,7 @@ std::string plan_to_string(const ProgramIR &p) {
   }
   for (auto &k : p.kernels) {
     os << "kernel " << k.name << " " << k.role << " grid " << k.grid << " " << k.grid_y << " block " << k.block
-       << " bytes " << k.algo_bytes << " args";
+       << " bytes " << k.algo_bytes << " moved " << k.moved_bytes << " args";
     for (int a : k.args) os << " " << a;
     os << "\n";
   }

@@ -146,6 +146,12 @@ struct KernelSpec {
   // root reads counted once, its output written once), on the root's main
   // kernel; 0 on helper kernels (look-back init, scatter bookkeeping, ...).
   int64_t algo_bytes = 0;
+  // Bytes the kernel itself reads from and writes to materialised tensors
+  // (scratch excluded), each tensor read once: the root's algorithmic
+  // bytes, less reads the lowering made unnecessary (a reduction folded
+  // inside the map that writes its input reads nothing back; roots over
+  // one input fused into one kernel read it once). 0 on helper kernels.
+  int64_t moved_bytes = 0;
 };
 
 enum class OpK { Alloc, Upload, Launch, Download, Free };

@@ -116,13 +116,24 @@ int cchip_program_run_resident_into(cchip_program *program, int n_inputs, const 
    any device work. All calls on one GPU share that array, and each uses the
    program's executor-0 pool for its intermediates: calls that overlap on
    one GPU (any program), or that overlap another run of the same program,
-   race. Device-side index errors are reported by the program's next
-   synchronising run on executor 0, after the caller has synchronised
-   `stream`. Work is only issued; synchronise `stream` before reading the
-   outputs. */
+   race. Device-side index errors stay with the call: its error word is the
+   first word of the static scratch, cleared at the start of the call, and
+   never the program's own, so no other run reports them. When `err_out` (a
+   device int the caller owns) is not NULL, the call copies its word there
+   after its kernels, on `stream`; 0 means no error, and
+   cchip_error_word_status turns any other value into the status and
+   message a synchronous run would have given. With `err_out` NULL the
+   flags are dropped. Work is only issued; synchronise `stream` before
+   reading the outputs or `err_out`. */
 int cchip_program_run_resident_noalloc(cchip_program *program, int n_inputs, const char *const *names,
                                        void *const *dev_inputs, const size_t *bytes, void *const *dev_outputs,
-                                       void *stream);
+                                       void *stream, int *err_out);
+/* No counterpart in the reference; the companion of the allocation-free
+   run. CCHIP_OK for 0; otherwise CCHIP_INVALID_ARGUMENT with
+   cchip_last_error() set to the interpreter's message for the device-side
+   error flags in `code` (gather or scatter_add index out of bounds, or a
+   look-back scan that did not complete). */
+int cchip_error_word_status(int code);
 
 /* The stream executor `lane` issues its work on (NULL for lane 0). */
 int cchip_program_stream(const cchip_program *program, int lane, void **stream);

@@ -36,3 +36,19 @@ def test_no_device_queries_are_safe():
 
     assert Device.available() in (True, False)
     assert _lib.lib().cchip_buffer_live_count() >= 0
+
+
+def test_error_word_status_gives_the_interpreters_messages():
+    """The allocation-free call's error word maps to the exceptions a
+    synchronous run raises; no device is touched."""
+    import pytest
+
+    from cudacaml_amd import backend_hip as H
+
+    H.raise_error_word(0)
+    with pytest.raises(ValueError, match="gather index out of bounds"):
+        H.raise_error_word(1)
+    with pytest.raises(ValueError, match="scatter_add index out of bounds"):
+        H.raise_error_word(2)
+    with pytest.raises(ValueError, match="look-back did not complete"):
+        H.raise_error_word(4)

@@ -85,6 +85,55 @@ def band(got, exact, tol):
     return float(np.max(np.abs(g - e) / (1.0 + np.abs(e)))) if g.size else 0.0
 
 
+# ---- config 1: saxpy and the 5-map chain -----------------------------------------
+
+
+def test_config1_saxpy_2_24_as_benchmarked(device):
+    """The saxpy graph bench.py times, on its own inputs (x seed 1, y seed
+    2, n = 2^24): r bit for bit against the oracle (one rounding per op,
+    R1); s within the f32 reduction band of the exact sum of r (math.fsum
+    over the f32 values of r). The oracle's own s, a sequential f32 fold
+    over 2^24 terms, is checked against the same exact sum; the three
+    distances are printed (oracle vs exact, device vs exact, device vs
+    oracle), and the device must be no further from the exact sum than the
+    band."""
+    n = C.N1
+    x = gen(C.gen_uniform_pm1((n,)), 1)
+    y = gen(C.gen_uniform_pm1((n,)), 2)
+    pin(x, 1, uniform_of)
+    pin(y, 2, uniform_of)
+    g = C.saxpy()
+    assert roles(g) == ["map", "reduce_split_fold", "reduce_split_fold"]
+    exp = dict(oracle.run(g, [("x", x), ("y", y)]))
+    got = run_dev(g, [("x", x), ("y", y)])
+    np.testing.assert_array_equal(got["r"], exp["r"])
+    exact = math.fsum(exp["r"].astype(np.float64).tolist())
+    d_oe = band(exp["s"], exact, 1e-4)
+    d_de = band(got["s"], exact, 1e-4)
+    d_do = band(got["s"], exp["s"], 1e-4)
+    print("config1 s at 2^24: exact %.9g oracle %.9g device %.9g | band distance oracle-exact %.3g, "
+          "device-exact %.3g, device-oracle %.3g" % (exact, float(exp["s"]), float(got["s"]), d_oe, d_de, d_do))
+    assert d_de <= 1e-4
+
+
+def test_config1_chain_2_24_bit_exact(device):
+    """The 5-map chain ((-((x+1)^2))-1)*0.5 bench.py times, fused into one
+    kernel, over its own 2^24 inputs (seed 1): bit for bit against the
+    oracle, which rounds once per op."""
+    n = C.N1
+    x = gen(C.gen_uniform_pm1((n,)), 1)
+    pin(x, 1, uniform_of)
+    g = C.chain()
+    assert roles(g) == ["map"]
+    exp = dict(oracle.run(g, [("x", x)]))
+    got = run_dev(g, [("x", x)])
+    for name, e in exp.items():
+        np.testing.assert_array_equal(got[name], e, err_msg=name)
+    # the closed form in float64, as a check on the oracle's own formula
+    x64 = x.astype(np.float64)
+    np.testing.assert_allclose(got[next(iter(exp))], (-((x64 + 1) ** 2) - 1) * 0.5, rtol=3e-7, atol=3e-7)
+
+
 # ---- config 2: the headline workload ------------------------------------------
 
 
@@ -189,6 +238,26 @@ def test_config4_matmul_f64_2048_vs_exact(device):
     for i, j in zip(r.integers(0, n, 64), r.integers(0, n, 64)):
         exact = float(sum(Fraction(float(x)) * Fraction(float(y)) for x, y in zip(a[i], b[:, j])))
         assert abs(got[i, j] - exact) <= 1e-12 * (1 + abs(exact)), (i, j)
+
+
+def test_config4_matmul_f32_4096_normals_vs_exact(device):
+    """The forward f32 4096^3 product bench.py times, on its own N(0,1)
+    draws (seeds 8 and 9): every entry within the f32 band of the float64
+    product of the same f32 inputs (whose own error is far below it); the
+    worst entry and the normwise error are printed."""
+    n = C.MM_F32
+    a = gen(C.gen_normals((n, n), F32), 8)
+    b = gen(C.gen_normals((n, n), F32), 9)
+    pin(a, 8, normal_of(F32), exact=False, rtol=2e-6)
+    pin(b, 9, normal_of(F32), exact=False, rtol=2e-6)
+    g = C.matmul(n, F32)
+    assert roles(g) == ["matmul_mfma_f32_a0b0"]
+    got = run_dev(g, [("a", a), ("b", b)])["c"].astype(np.float64)
+    exact = a.astype(np.float64) @ b.astype(np.float64)
+    err = np.abs(got - exact) / (1.0 + np.abs(exact))
+    print("config4 f32 4096^3 on N(0,1): max band distance %.3g at |e| = %.3g, normwise %.3g"
+          % (err.max(), abs(exact.flat[err.argmax()]), np.linalg.norm(got - exact) / np.linalg.norm(exact)))
+    assert err.max() <= 1e-4, err.max()
 
 
 @pytest.mark.parametrize("dtype,n,tol", [(F32, C.MM_F32, 1e-4), (F64, C.MM_F64, 1e-12)], ids=["f32", "f64"])

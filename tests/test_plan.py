@@ -227,8 +227,8 @@ def test_jit_reports_compile_errors():
         runtime.Jit.check("bad", "this is not HIP")
 
 
-def _bytes(g):
-    return {k[2]: int(k[k.index("bytes") + 1]) for k in
+def _bytes(g, field="bytes"):
+    return {k[2]: int(k[k.index(field) + 1]) for k in
             (l.split() for l in H.plan(g).splitlines() if l.startswith("kernel"))}
 
 
@@ -241,9 +241,13 @@ def test_algorithmic_bytes_per_kernel(monkeypatch):
     n = 1 << 20
     b = _bytes(sx.program(n, 2.0))
     assert b["map"] == 3 * 4 * n and b["reduce_split_fold"] == 4 * n + 4
+    # ... but reads nothing back: it moves its one output value
+    m = _bytes(sx.program(n, 2.0), "moved")
+    assert m["map"] == 3 * 4 * n and m["reduce_split_fold"] == 4
     monkeypatch.setenv("CCHIP_TUNE", "fuse_reduce=0")
     b = _bytes(sx.program(n, 2.0))
     assert b["map"] == 3 * 4 * n and b["reduce_split"] == 4 * n + 4
+    assert _bytes(sx.program(n, 2.0), "moved") == b
     monkeypatch.delenv("CCHIP_TUNE")
     b = _bytes(C.global_scan(n))
     assert b["scan_lookback"] == 8 * n and b["scan_init"] == 0

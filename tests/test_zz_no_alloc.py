@@ -173,3 +173,57 @@ def test_noalloc_rejects_programs_beyond_the_static_scratch(device):
         c.release()
     with pytest.raises(RuntimeError, match="released"):
         H.run_resident_noalloc(c, res, outs)
+
+
+def test_noalloc_index_errors_stay_with_the_call(device):
+    """An out-of-range scatter index in an allocation-free call is reported
+    through that call's own error word (the caller's err buffer), and
+    never by a later run: a clean synchronous run_resident_into and a clean
+    run_async job on the same program succeed afterwards, and a clean
+    allocation-free call returns a zero word (the scratch's word was
+    cleared at the start of the call). The kernels bounds-check the index
+    and skip it, as in test_scatter_out_of_range_raises."""
+    n, bins = (1 << 16) + 5, 1 << 12
+    c = H.compile(program(n, bins))
+    bad = inputs(n, bins, seed=7)
+    bad[2][1][[3, n - 2]] = [bins, -1]
+    good = inputs(n, bins, seed=8)
+    res_bad = [(nm, H.upload(v)) for nm, v in bad]
+    res_good = [(nm, H.upload(v)) for nm, v in good]
+    outs, want_o = outputs_of(c), outputs_of(c)
+    err = Buffer.alloc(4)
+    stream = Stream.create()
+    try:
+        H.run_resident_noalloc(c, res_bad, outs, stream.ptr, err=err)
+        stream.synchronize()
+        code = _word(err)
+        assert code & 2, code
+        with pytest.raises(ValueError, match="scatter_add index out of bounds"):
+            H.raise_error_word(code)
+        # later runs of the same program do not see the call's flags
+        H.run_resident_into(c, res_good, want_o, sync=True)
+        H.wait(H.run_async(c, good))
+        H.run_resident_noalloc(c, res_good, outs, stream.ptr, err=err)
+        stream.synchronize()
+        assert _word(err) == 0
+        H.raise_error_word(0)
+        for (nm, w), (_, g) in zip(want_o, outs):
+            np.testing.assert_array_equal(H.download(g), H.download(w), err_msg=nm)
+        # and without an err buffer the flags are dropped, not passed on
+        H.run_resident_noalloc(c, res_bad, outs, stream.ptr)
+        stream.synchronize()
+        H.run_resident_into(c, res_good, want_o, sync=True)
+        H.run(c, good)
+    finally:
+        err.free()
+        free_all(res_bad)
+        free_all(res_good)
+        free_all(outs)
+        free_all(want_o)
+        c.release()
+
+
+def _word(buf):
+    out = np.zeros(1, np.int32)
+    buf.download(out)
+    return int(out[0])
