@@ -1060,6 +1060,13 @@ struct Lowering {
   };
   std::map<int, int> fused_red_of_map;
   std::map<int, FusedPartials> fused_part_of_red;
+  // Row roots over one tensor fused into one kernel: a row scan that takes
+  // the one-workgroup-a-row tile template, and the reductions of the same
+  // tensor's rows that fold as a tree. The group's first root in the plan
+  // (lead) launches the kernel; the others launch nothing.
+  std::map<int, std::vector<int>> sib_reds;  // scan root -> its reductions
+  std::map<int, int> sib_lead;               // first root of a group -> scan root
+  std::set<int> sib_member;                  // every root of a group but the lead
 
   explicit Lowering(const Graph &gr) : g(gr), plan(fusion_plan(gr)), gen(gr, plan, buf_of) {
     gen.bufdt_ = [this](int b) { return prog.bufs[b].dt; };
@@ -1274,8 +1281,45 @@ struct Lowering {
     }
   }
 
+  // A fused group of sibling row roots: the kernel carries every member
+  // root's algorithmic bytes, and moves the shared tensor's reads once plus
+  // every member's output.
+  void attribute_group_bytes(int scan, const std::vector<int> &reds, const std::vector<int> &ks) {
+    if (ks.empty()) return;
+    const TNode &sn = g.ts[scan];
+    int64_t algo = root_bytes(scan), moved = fn_bytes(gen.element_fn("ab_", sn.a, false, true), g.ts[sn.a].numel) +
+                                              sn.numel * dt_size(sn.dt);
+    for (int r : reds) {
+      algo += root_bytes(r);
+      moved += g.ts[r].numel * dt_size(g.ts[r].dt);
+    }
+    prog.kernels[ks.back()].algo_bytes = algo;
+    prog.kernels[ks.back()].moved_bytes = moved;
+  }
+
   void attribute_bytes(int r, const std::vector<int> &ks) {
     if (ks.empty()) return;
+    const TNode &n = g.ts[r];
+    const int64_t out = n.numel * dt_size(n.dt);
+    const int64_t bytes = root_bytes(r);
+    static const char *helpers[] = {"scan_init",          "scatter_zero",   "scatter_count",  "scatter_colscan",
+                                    "scatter_bscan",      "scatter_accumulate", "scatter_reduce", "matmul_ksum",
+                                    "reduce_split_fold",  "scatter_coarse",     "gather_slices",  "scatter_windows"};
+    int main = ks.back();
+    for (int k : ks) {
+      bool helper = false;
+      for (const char *h : helpers) helper |= prog.kernels[k].role == h;
+      if (!helper) main = k;
+    }
+    prog.kernels[main].algo_bytes = bytes;
+    // a reduction folded inside its input's map reads only the partials
+    // (scratch): it moves its output alone
+    prog.kernels[main].moved_bytes = n.kind == TK::Reduce && fused_part_of_red.count(r) ? out : bytes;
+  }
+
+  // The fusion plan's algorithmic bytes of root r: each element it reads
+  // counted once, its output written once.
+  int64_t root_bytes(int r) {
     const TNode &n = g.ts[r];
     const int64_t out = n.numel * dt_size(n.dt);
     int64_t bytes = 0;
@@ -1296,19 +1340,7 @@ struct Lowering {
       }
       default: bytes = fn_bytes(gen.element_fn("ab_", r, true, true), n.numel) + out;
     }
-    static const char *helpers[] = {"scan_init",          "scatter_zero",   "scatter_count",  "scatter_colscan",
-                                    "scatter_bscan",      "scatter_accumulate", "scatter_reduce", "matmul_ksum",
-                                    "reduce_split_fold",  "scatter_coarse",     "gather_slices",  "scatter_windows"};
-    int main = ks.back();
-    for (int k : ks) {
-      bool helper = false;
-      for (const char *h : helpers) helper |= prog.kernels[k].role == h;
-      if (!helper) main = k;
-    }
-    prog.kernels[main].algo_bytes = bytes;
-    // a reduction folded inside its input's map reads only the partials
-    // (scratch): it moves its output alone
-    prog.kernels[main].moved_bytes = n.kind == TK::Reduce && fused_part_of_red.count(r) ? out : bytes;
+    return bytes;
   }
 
   // ---- element-wise root (K1 -> vectorised map, one 16-byte group a lane) ---
@@ -2013,7 +2045,87 @@ struct Lowering {
   }
 
   // ---- Scan root (K5-K8 -> wave / block / decoupled look-back scans) -----
-  std::vector<int> lower_scan(int t) {
+  // The tile templates' shape for a row of `len` elements of `dt`: NW waves
+  // a workgroup, U slices of SL = 256 NW elements a tile, tiles per row.
+  struct TileShape {
+    int64_t NW, U, SL, tile, tpr;
+  };
+  static TileShape tile_shape(int64_t len, DT dt) {
+    const bool wide = dt_size(dt) == 8;
+    TileShape s;
+    s.NW = tune("lb_waves", 8) == 8 ? 8 : 4;
+    int64_t Umax = tune(wide ? "lb_slices8" : "lb_slices4", wide ? 8 : (s.NW == 8 ? 13 : 22));
+    if (Umax < 1) throw InvalidArgument("CCHIP_TUNE: look-back slices must be >= 1");
+    s.SL = 256 * s.NW;
+    s.U = std::min<int64_t>(Umax, std::max<int64_t>(1, cdiv(len, s.SL)));
+    s.tile = s.SL * s.U;
+    s.tpr = cdiv(len, s.tile);
+    return s;
+  }
+
+  // Whether a scan root takes the tile template with one tile a row (one
+  // workgroup scans a whole row), as lower_scan decides.
+  bool scan_is_row_tile(int t) const {
+    const TNode &n = g.ts[t];
+    const int64_t len = row_length(n.shape);
+    if (len <= 64 || n.numel == 0 || n.dt == DT::BOOL) return false;
+    const int64_t rows = n.numel / len;
+    if (rows >= 1024 &&
+        !(tune("rs_tree", 1) && len >= tune("rs_tree_len", 2048) && any_order(n.body, n.dt, true)))
+      return false;
+    return tile_shape(len, n.dt).tpr == 1;
+  }
+
+  // Whether a reduce root folds its rows as a tree (wave, block or split
+  // templates), as lower_reduce decides, rather than in order.
+  bool reduce_is_tree(int t) const {
+    const TNode &n = g.ts[t];
+    const int64_t len = row_length(g.ts[n.a].shape);
+    if (n.numel == 0 || len == 0 || n.dt == DT::BOOL) return false;
+    const int64_t tree = tune("rr_tree", 2);
+    const bool as_tree = tree >= 1 && len >= tune("rr_tree_len", 1024) && any_order(n.body, n.dt, tree >= 2);
+    return !(n.numel >= 1024 && !as_tree);
+  }
+
+  // Groups of sibling row roots (sibling_fuse=0 keeps every root its own
+  // kernels). A reduction joins a scan's group when it reads the same
+  // tensor node with the same row shape and would fold as a tree anyway:
+  // the fused kernel folds each row's elements in a tree of another shape
+  // (each lane its elements in order, then the wave, then the waves in
+  // order), so max, min and integer results are the same bits and float
+  // add and mul differ by rounding only. The group's kernel runs at its
+  // first root's place in the plan: every member reads only what the
+  // shared tensor reads, which is ready by then.
+  void find_sibling_groups() {
+    if (!tune("sibling_fuse", 1)) return;
+    std::map<int, size_t> pos;
+    for (size_t i = 0; i < plan.roots.size(); i++) pos[plan.roots[i]] = i;
+    std::set<int> folded_in_map;
+    for (auto &fr : fused_red_of_map) folded_in_map.insert(fr.second);
+    for (int s : plan.roots) {
+      const TNode &sn = g.ts[s];
+      if (sn.kind != TK::Scan || !scan_is_row_tile(s)) continue;
+      const int64_t len = row_length(sn.shape), rows = sn.numel / len;
+      std::vector<int> reds;
+      for (int r : plan.roots) {
+        const TNode &rn = g.ts[r];
+        if (rn.kind != TK::Reduce || rn.a != sn.a || sib_member.count(r) || folded_in_map.count(r)) continue;
+        if (row_length(g.ts[rn.a].shape) != len || rn.numel != rows || !reduce_is_tree(r)) continue;
+        reds.push_back(r);
+      }
+      if (reds.empty()) continue;
+      int lead = s;
+      for (int r : reds)
+        if (pos[r] < pos[lead]) lead = r;
+      sib_reds[s] = reds;
+      sib_lead[lead] = s;
+      if (lead != s) sib_member.insert(s);
+      for (int r : reds)
+        if (r != lead) sib_member.insert(r);
+    }
+  }
+
+  std::vector<int> lower_scan(int t, const std::vector<int> &reds = {}) {
     const TNode &n = g.ts[t];
     std::string id = std::to_string(n.id);
     std::string kname = "k_" + id;
@@ -2023,6 +2135,18 @@ struct Lowering {
     int64_t rows = len == 0 ? 0 : n.numel / len;
     std::string cmb = "c_" + id, ini = "z_" + id;
     src << gen.combine_fn(cmb, n.body, n.dt) << gen.const_fn(ini, n.init, n.dt);
+    // sibling reductions folded in this kernel: their combines, inits, types
+    std::vector<std::string> rcmb, rini, rT;
+    std::vector<int> rout;
+    for (int r : reds) {
+      const TNode &rn = g.ts[r];
+      const std::string rid = std::to_string(rn.id);
+      rcmb.push_back("c_" + rid);
+      rini.push_back("z_" + rid);
+      rT.push_back(dt_ctype(rn.dt));
+      rout.push_back(buf_of[r]);
+      src << gen.combine_fn(rcmb.back(), rn.body, rn.dt) << gen.const_fn(rini.back(), rn.init, rn.dt);
+    }
     if (rows == 0) return {};
     ElemFn f = gen.element_fn("f_" + id, n.a, false, true);
     src << f.code;
@@ -2105,15 +2229,11 @@ struct Lowering {
     // 12, 14, 15 and 16 slices. 8-byte values over 8 slices: 2^27 i64 or
     // f64 in 472-476 us, against 552 us for 4 waves (6 slices: the same;
     // 4, 5 and 7 slices: 545, 493-519 and 485 us).
-    const int64_t NW = tune("lb_waves", 8) == 8 ? 8 : 4;
-    int64_t Umax = tune(wide ? "lb_slices8" : "lb_slices4", wide ? 8 : (NW == 8 ? 13 : 22));
-    if (Umax < 1) throw InvalidArgument("CCHIP_TUNE: look-back slices must be >= 1");
-    const int64_t SL = 256 * NW, NT = 64 * NW;
-    int64_t U = std::min<int64_t>(Umax, std::max<int64_t>(1, cdiv(len, SL)));
-    int64_t tile = SL * U;
-    int64_t tpr = cdiv(len, tile);
+    const TileShape ts = tile_shape(len, n.dt);
+    const int64_t NW = ts.NW, SL = ts.SL, NT = 64 * NW, U = ts.U, tile = ts.tile, tpr = ts.tpr;
     int64_t tiles = rows * tpr;
     bool chained = tpr > 1;
+    if (!reds.empty() && chained) throw Failure("Lower: sibling reductions need one tile a row");
     bool vec = len % 4 == 0;
     int words = wide ? 2 : 1;
     const bool selfsched = chained && !wide && tune("lb_counter", 0) == 0;
@@ -2140,6 +2260,7 @@ struct Lowering {
     Params p;
     add_in(p, f);
     p.out.push_back(out);
+    for (int o : rout) p.out.push_back(o);
     if (chained) p.err = true;
     std::vector<int> args;
     std::string params = param_list(p, args);
@@ -2198,6 +2319,9 @@ struct Lowering {
       << "  __shared__ " << T << " wsum[" << U << "][" << NW << "];\n"
       << "  __shared__ " << T << " s_prefix;\n"
       << "  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;\n";
+    for (size_t j = 0; j < reds.size(); j++)
+      k << "  __shared__ " << rT[j] << " rpart" << j << "[" << NW << "];\n"
+        << "  __shared__ bool rhas" << j << "[" << NW << "];\n";
     if (chained && !selfsched) {
       k << "  __shared__ int s_tile;\n"
         << "  if (threadIdx.x == 0) s_tile = atomicAdd(ctr, 1);\n"
@@ -2238,8 +2362,30 @@ struct Lowering {
         k << "    { const bool ok = e + " << c << " < tl; const int i = base + (ok ? e + " << c << " : 0); v[u][" << c
           << "] = ok ? " << f.call_scalar("i") << " : " << ini << "(); }\n";
     }
-    k << "  }\n"
-      << "  if (tin == 0 && threadIdx.x == 0) v[0][0] = " << cmb << "(" << ini << "(), v[0][0]);\n"
+    k << "  }\n";
+    // Sibling reductions: each lane folds its elements in row order (slice
+    // by slice) before the scan changes them, then the wave in a butterfly;
+    // one partial a wave goes to LDS with the scan's wave totals.
+    for (size_t j = 0; j < reds.size(); j++) {
+      const std::string A = "racc" + std::to_string(j), Hs = "rh" + std::to_string(j);
+      k << "  " << rT[j] << " " << A << " = " << rini[j] << "();\n"
+        << "  bool " << Hs << " = false;\n"
+        << "#pragma unroll\n"
+        << "  for (int u = 0; u < " << U << "; u++) {\n"
+        << "    const int e = threadIdx.x * 4 + " << SL << " * u;\n"
+        << "#pragma unroll\n"
+        << "    for (int c = 0; c < 4; c++) {\n"
+        << "      const bool ok_ = e + c < tl;\n"
+        << "      const " << rT[j] << " y_ = " << Hs << " ? " << rcmb[j] << "(" << A << ", v[u][c]) : v[u][c];\n"
+        << "      " << A << " = ok_ ? y_ : " << A << "; " << Hs << " = " << Hs << " || ok_;\n"
+        << "    }\n"
+        << "  }\n"
+        << "  for (int off = 32; off > 0; off >>= 1) { const " << rT[j] << " o_ = __shfl_xor(" << A
+        << ", off); const bool oh_ = __shfl_xor((int)" << Hs << ", off) != 0; if (oh_) { " << A << " = " << Hs
+        << " ? " << rcmb[j] << "(" << A << ", o_) : o_; " << Hs << " = true; } }\n"
+        << "  if (lane == 0) { rpart" << j << "[wid] = " << A << "; rhas" << j << "[wid] = " << Hs << "; }\n";
+    }
+    k << "  if (tin == 0 && threadIdx.x == 0) v[0][0] = " << cmb << "(" << ini << "(), v[0][0]);\n"
       << "#pragma unroll\n"
       << "  for (int u = 0; u < " << U << "; u++) {\n"
       << "    v[u][1] = " << cmb << "(v[u][0], v[u][1]);\n"
@@ -2271,6 +2417,16 @@ struct Lowering {
       << "    for (int w = 1; w < " << NW << "; w++) su = " << cmb << "(su, wsum[u][w]);\n"
       << "    run = u > 0 ? " << cmb << "(run, su) : su;\n"
       << "  }\n";
+    // the sibling reductions' wave partials, in wave order (the barrier
+    // above made them visible); init once, to the row's total
+    for (size_t j = 0; j < reds.size(); j++)
+      k << "  if (threadIdx.x == 0) {\n"
+        << "    " << rT[j] << " t = " << rini[j] << "();\n"
+        << "    bool th = false;\n"
+        << "    for (int w = 0; w < " << NW << "; w++) if (rhas" << j << "[w]) { t = th ? " << rcmb[j] << "(t, rpart"
+        << j << "[w]) : rpart" << j << "[w]; th = true; }\n"
+        << "    b" << rout[j] << "[row] = th ? " << rcmb[j] << "(" << rini[j] << "(), t) : " << rini[j] << "();\n"
+        << "  }\n";
     if (chained) {
       k << "  if (threadIdx.x == 0) " << publish("tile", "tin == 0 ? 2 : 1", "run") << ";\n"
         << "  if (tin > 0) {\n"
@@ -2437,7 +2593,8 @@ struct Lowering {
     k << "  }\n"
       << "}\n";
     src << k.str();
-    int kscan = add_kernel(kname, args, (int)tiles, (int)NT, chained ? "scan_lookback" : "scan_tile");
+    int kscan = add_kernel(kname, args, (int)tiles, (int)NT,
+                           chained ? "scan_lookback" : reds.empty() ? "scan_tile" : "scan_tile_fold");
     if (chained) return {kinit, kscan};
     return {kscan};
   }
@@ -4522,12 +4679,19 @@ struct Lowering {
         if (std::count(code.begin(), code.end(), '\n') >= 48) continue;
         fused_red_of_map[m] = r;
       }
+    find_sibling_groups();
     std::vector<std::vector<int>> launches;
     std::vector<std::vector<int>> scratch_of;
     for (int r : plan.roots) {
       size_t before = prog.bufs.size();
       std::vector<int> ks;
-      switch (g.ts[r].kind) {
+      if (sib_member.count(r)) {
+        // lowered with its group's lead
+      } else if (sib_lead.count(r)) {
+        const int sc = sib_lead[r];
+        ks = lower_scan(sc, sib_reds[sc]);
+        attribute_group_bytes(sc, sib_reds[sc], ks);
+      } else switch (g.ts[r].kind) {
         case TK::Gather: {
           auto it = gather_back.find(g.ts[r].b);
           auto ro = gbp_root_of.find(g.ts[r].b);
@@ -4546,7 +4710,7 @@ struct Lowering {
         case TK::Matmul: ks = lower_matmul(r); break;
         default: throw Failure("Lower: a Param never gets a kernel");
       }
-      attribute_bytes(r, ks);
+      if (!sib_member.count(r) && !sib_lead.count(r)) attribute_bytes(r, ks);
       std::vector<int> sc;
       for (size_t b = before; b < prog.bufs.size(); b++)
         if (prog.bufs[b].role == BufRole::Scratch) sc.push_back((int)b);

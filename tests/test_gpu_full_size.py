@@ -175,7 +175,7 @@ def test_config2_rows_8192_as_benchmarked(device):
     x = gen(C.gen_uniform_pm1((C.ROWS2, C.ROWS2)), 3)
     pin(x, 3, uniform_of)
     g = C.rows()
-    assert roles(g) == ["reduce_block", "reduce_block", "scan_tile"]
+    assert roles(g) == ["scan_tile_fold"]
     exp = dict(oracle.run(g, [("x", x)]))
     got = run_dev(g, [("x", x)])
     e64 = x.astype(np.float64).sum(axis=1)

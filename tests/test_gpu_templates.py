@@ -192,6 +192,88 @@ def test_scan_init_applied_once(device, monkeypatch, rows, n, dtype, tpl):
     check_scans(monkeypatch, g, [("x", data(dtype, (rows, n), 15))], tpl, 7)
 
 
+SIBLING_CASES = [
+    # (rows, len, dtype): ragged rows (not a multiple of 4: scalar loads),
+    # short rows (the reductions alone would take reduce_wave), 1024 rows
+    # or more, the longest one-tile rows (26624 elements of 4 bytes, 16384
+    # of 8 bytes)
+    (600, 3001, F32),
+    (300, 100, F32),
+    (1030, 9000, I32),
+    (2000, 2048, I64),
+    (513, 26624, I32),
+    (700, 16384, F64),
+    (257, 26623, F32),
+]
+
+
+def sibling_graph(dtype, rows, n):
+    """A row scan and three row reductions of the same tensor, with
+    non-identity inits: config 2's shape, plus min."""
+    x = D.param("x", dtype, (rows, n))
+    lo = -(1 << 30) if dtype.name in ("i32", "i64") else -1e30
+    return Graph.create("sib", [("s", D.reduce_rows(D.add, D.const(dtype, 5), x)),
+                                ("m", D.reduce_rows(D.max, D.const(dtype, lo), x)),
+                                ("p", D.scan_rows(D.add, D.const(dtype, 7), x)),
+                                ("n", D.reduce_rows(D.min, D.const(dtype, 3), x))])
+
+
+def check_siblings(g, inputs, init_s, init_p):
+    """Integer outputs, max and min against the oracle bit for bit; a float
+    sum and prefix sum against float64 within the policy's band (the
+    interpreter's in-order f32 folds drift beyond it over long rows)."""
+    exp = dict(oracle.run(g, inputs))
+    c = H.compile(g)
+    try:
+        got = dict(H.run(c, inputs))
+    finally:
+        c.release()
+    x = inputs[0][1]
+    fl = x.dtype.kind == "f"
+    for name in ("m", "n") if fl else ("s", "m", "p", "n"):
+        np.testing.assert_array_equal(got[name], exp[name], err_msg=name)
+    if fl:
+        tol = 1e-4 if x.dtype == np.float32 else 1e-12
+        x64 = x.astype(np.float64)
+        e = x64.sum(axis=1) + init_s
+        assert np.max(np.abs(got["s"] - e) / (1 + np.abs(e))) <= tol
+        e = np.cumsum(x64, axis=1) + init_p
+        assert np.max(np.abs(got["p"] - e) / (1 + np.abs(e))) <= tol
+    return got
+
+
+@pytest.mark.parametrize("rows,n,dtype", SIBLING_CASES, ids=lambda v: str(v))
+def test_sibling_row_roots_one_kernel(device, monkeypatch, rows, n, dtype):
+    """The row scan and the reductions of the same tensor in one kernel
+    (each row read once), against the oracle; then the same graph with
+    sibling_fuse=0 (each root its own kernels): integer results equal bit
+    for bit."""
+    g = sibling_graph(dtype, rows, n)
+    assert templates(g) == ["scan_tile_fold"], templates(g)
+    ins = [("x", data(dtype, (rows, n), 61))]
+    got = check_siblings(g, ins, 5, 7)
+    monkeypatch.setenv("CCHIP_TUNE", "sibling_fuse=0")
+    assert "scan_tile_fold" not in templates(g)
+    sep = check_siblings(g, ins, 5, 7)
+    for name in ("m", "n") if dtype in (F32, F64) else ("s", "m", "p", "n"):
+        np.testing.assert_array_equal(got[name], sep[name], err_msg=name)
+
+
+def test_sibling_group_runs_before_a_consumer_of_its_first_root(device):
+    """The group's kernel runs where its first root stands in the plan: a
+    root between the reduction and the scan reads the reduction's output,
+    and a map read twice (materialised) is the shared tensor."""
+    rows, n = 700, 5000
+    x = D.param("x", F32, (rows, n))
+    m = D.map(lambda v: D.add(D.mul(v, v), D.const(F32, 0.25)), x)
+    s = D.reduce_rows(D.max, D.const(F32, 0.0), m)
+    t = D.map(lambda v: D.mul(v, D.const(F32, 3.0)), s)
+    p = D.scan_rows(D.max, D.const(F32, -1.0), m)
+    g = Graph.create("sib2", [("s", s), ("t", t), ("p", p)])
+    assert templates(g) == ["map", "scan_tile_fold", "map"], templates(g)
+    check(g, [("x", data(F32, (rows, n), 62))], ["scan_tile_fold"])
+
+
 FOLDED_CASES = [((1 << 16) + 3, F32, "add"), ((1 << 22) + 5, F32, "add"), ((1 << 20) + 2, F64, "add"),
                 (300 * 1024 + 5, F32, "add"), (1 << 18, F32, "add"), (102421, F32, "max"),
                 ((1 << 22) + 1, I32, "add"), ((1 << 20) + 7, F32, "max"), (1 << 23, I32, "max"),
@@ -252,6 +334,36 @@ def test_rows_max_min_tree_edges(device):
     g = Graph.create("mm", [("mx", D.reduce_rows(D.max, D.const(F32, -0.0), x)),
                             ("mn", D.reduce_rows(D.min, D.const(F32, 0.0), x))])
     assert templates(g) == ["reduce_block", "reduce_block"]
+    exp = oracle.run(g, [("x", v)])
+    c = H.compile(g)
+    try:
+        got = H.run(c, [("x", v)])
+    finally:
+        c.release()
+    for (name, e), (_, d) in zip(exp, got):
+        assert np.array_equal(np.isnan(e), np.isnan(d)), name
+        ok = ~np.isnan(e)
+        np.testing.assert_array_equal(e[ok].view(np.uint32), d[ok].view(np.uint32), err_msg=name)
+
+
+def test_sibling_max_min_and_max_scan_edges(device):
+    """The fused sibling kernel on the same edge values: row max and min
+    and a max scan of rows of zeros of both signs, infinities and NaNs,
+    bit for bit against the interpreter's in-order folds and scan."""
+    rows, n = 1024, 5000
+    v = data(F32, (rows, n), 36)
+    r = np.random.default_rng(6)
+    v[r.integers(0, rows, 40), r.integers(0, n, 40)] = np.nan
+    v[v > 0.999] = np.inf
+    v[v < -0.999] = -np.inf
+    v[100:110] = 0.0
+    v[100:110, ::3] = -0.0
+    v[200:210] = -0.0
+    x = D.param("x", F32, (rows, n))
+    g = Graph.create("mm", [("mx", D.reduce_rows(D.max, D.const(F32, -0.0), x)),
+                            ("q", D.scan_rows(D.max, D.const(F32, -0.0), x)),
+                            ("mn", D.reduce_rows(D.min, D.const(F32, 0.0), x))])
+    assert templates(g) == ["scan_tile_fold"]
     exp = oracle.run(g, [("x", v)])
     c = H.compile(g)
     try:

@@ -150,8 +150,9 @@ def test_scan_template_choice(rows, n, tpls):
 
 def test_config_plans():
     # rows of 8192 fold as trees, a workgroup a row (the adds within the
-    # rounding of another grouping, the max bit-exact)
-    assert [t for _, t in kernels_of(C.rows())] == ["reduce_block", "reduce_block", "scan_tile"]
+    # rounding of another grouping, the max bit-exact), all three roots in
+    # one kernel that reads each row once
+    assert [t for _, t in kernels_of(C.rows())] == ["scan_tile_fold"]
     # the gather back reads the scatter's partition: the table slice by
     # slice from LDS, then each tile's values back in element order; 128
     # slices, so the partition keeps each tile's pairs in the tile's region
@@ -259,6 +260,35 @@ def test_algorithmic_bytes_per_kernel(monkeypatch):
     # the price reduces the gathered last column only, not the whole path matrix
     b = _bytes(C.mc_paths(4096, 64))
     assert b["reduce_split"] < 4 * 4096 + 64
+
+
+def test_sibling_row_roots_share_one_kernel(monkeypatch):
+    """A row scan taking the one-tile-a-row template and the tree-folded
+    reductions of the same tensor's rows are one kernel: it carries every
+    root's algorithmic bytes and moves the tensor once plus the outputs.
+    Reductions of another tensor, or of the same one in order, keep their
+    own kernels; sibling_fuse=0 keeps every root its own."""
+    n = C.ROWS2
+    b, m = _bytes(C.rows()), _bytes(C.rows(), "moved")
+    assert b == {"scan_tile_fold": 3 * 4 * n * n + 4 * n * n + 2 * 4 * n}
+    assert m == {"scan_tile_fold": 4 * n * n + 4 * n * n + 2 * 4 * n}
+    x, y = D.param("x", F32, (600, 3000)), D.param("y", F32, (600, 3000))
+    g = Graph.create("g", [("a", D.reduce_rows(D.add, D.const(F32, 0.0), y)),
+                           ("p", D.scan_rows(D.add, D.const(F32, 0.0), x)),
+                           ("b", D.reduce_rows(D.max, D.const(F32, 0.0), x)),
+                           ("c", D.reduce(D.add, D.const(F32, 0.0), x))])
+    assert [t for _, t in kernels_of(g)] == ["reduce_block", "scan_tile_fold", "reduce_split", "reduce_split_fold"]
+    monkeypatch.setenv("CCHIP_TUNE", "sibling_fuse=0")
+    assert [t for _, t in kernels_of(C.rows())] == ["reduce_block", "reduce_block", "scan_tile"]
+    # in order (the interpreter's exact folds): nothing to share
+    monkeypatch.setenv("CCHIP_TUNE", "rr_tree=1,rs_tree=0")
+    assert [t for _, t in kernels_of(C.rows())] == ["reduce_rowseq", "reduce_block", "scan_rowseq"]
+    # a look-back scan (several tiles a row) keeps the reductions apart
+    monkeypatch.delenv("CCHIP_TUNE")
+    z = D.param("z", I32, (4, 100000))
+    g = Graph.create("lb", [("p", D.scan_rows(D.add, D.const(I32, 0), z)),
+                            ("s", D.reduce_rows(D.add, D.const(I32, 0), z))])
+    assert "scan_tile_fold" not in [t for _, t in kernels_of(g)]
 
 
 def _launch_uses_live_buffers(g):
