@@ -392,10 +392,19 @@ COPY_BYTES = (1 << 28) * 4  # read once and written once by the calibration kern
 
 
 # Configs whose dominant kernel is bound by instruction issue rather than
-# HBM: a third counter pass counts its VALU instructions and clocks. The
-# issue limit is one wave64 VALU instruction per SIMD every 4 clocks
-# (packed FP32 is off in every build here, so it is not counted).
+# HBM: two more counter passes. A SIMD issues one wave64 VALU instruction a
+# quad-cycle (4 clocks), and gfx950 issues a second one in the same
+# quad-cycle where the pair allows it (SQ_ACTIVE_INST_VALU2 counts those
+# quad-cycles). SQ_ACTIVE_INST_VALU counts the quad-cycles of each VALU
+# instruction, so the quad-cycles in which a SIMD issues VALU work at all
+# are ACTIVE_INST_VALU - ACTIVE_INST_VALU2; over the dispatch's SIMD
+# quad-cycles that is the share of the issue ceiling the kernel uses (1.0:
+# a VALU instruction issued every quad-cycle on every SIMD). The second
+# pass splits the VALU instructions by class. Packed FP32 is off in every
+# build here, so it is not counted.
 VALU_CONFIGS = ("poly", "poly64", "mc", "mc64", "mc_greeks", "bs", "bs64", "bs_greeks", "bs_greeks64")
+VALU_CLASSES = ("SQ_INSTS_VALU_INT32", "SQ_INSTS_VALU_INT64", "SQ_INSTS_VALU_FMA_F32", "SQ_INSTS_VALU_FMA_F64",
+                "SQ_INSTS_VALU_TRANS_F32", "SQ_INSTS_VALU_TRANS_F64", "SQ_INSTS_VALU_CVT", "SQ_INSTS_VALU_ADD_F64")
 
 
 # Matmul configs: one more counter pass for the matrix cores.
@@ -417,7 +426,8 @@ def counter_passes(config):
     cycle count (matmul configs)."""
     passes = [["FETCH_SIZE"], ["WRITE_SIZE"]]
     if config in VALU_CONFIGS:
-        passes.append(["SQ_INSTS_VALU", "GRBM_GUI_ACTIVE"])
+        passes.append(["SQ_INSTS_VALU", "SQ_ACTIVE_INST_VALU", "SQ_ACTIVE_INST_VALU2", "GRBM_GUI_ACTIVE"])
+        passes.append(list(VALU_CLASSES) + ["GRBM_GUI_ACTIVE"])
     if config in MFMA_CONFIGS:
         passes.append(["SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_F32", "SQ_INSTS_VALU_MFMA_MOPS_F64",
                        "GRBM_GUI_ACTIVE"])
@@ -675,22 +685,32 @@ def main():
     per = counters[0] or {}
     simds = info.multiprocessors * SIMDS_PER_CU
     dc = per.get(dom, {})
-    if args.config in VALU_CONFIGS and "SQ_INSTS_VALU" in dc and dc.get("GRBM_GUI_ACTIVE"):
-        # Issue-bound kernels: wave64 VALU instructions (SQ_INSTS_VALU)
-        # against the issue limit of one per SIMD every 4 clocks, over the
-        # clocks of the same dispatches (GRBM_GUI_ACTIVE, same pass), so no
-        # clock rate is assumed; lane-instructions per element of the
-        # kernel's output; the clock those cycles imply over this run's
-        # HIP-event time, for reference.
-        winst = dc["SQ_INSTS_VALU"]
+    if (args.config in VALU_CONFIGS and "SQ_ACTIVE_INST_VALU" in dc and "SQ_ACTIVE_INST_VALU2" in dc
+            and dc.get("GRBM_GUI_ACTIVE")):
+        # Issue-bound kernels: the quad-cycles in which each SIMD issued VALU
+        # work (ACTIVE_INST_VALU less the quad-cycles that issued two) over
+        # the dispatch's SIMD quad-cycles (GRBM_GUI_ACTIVE of the same
+        # pass), so no clock rate is assumed; also the wave64 instructions,
+        # lane-instructions per element of the kernel's output, the share of
+        # VALU quad-cycles that issued two, the instructions by class, and
+        # the clock those cycles imply over this run's HIP-event time.
+        winst = dc.get("SQ_INSTS_VALU", 0.0)
+        active, dual = dc["SQ_ACTIVE_INST_VALU"], dc["SQ_ACTIVE_INST_VALU2"]
         cycles = dc["GRBM_GUI_ACTIVE"] / XCC_COUNT
+        quads = simds * cycles / 4
         n_el = kernel_elements(H, w, dom)
-        roof["valu"] = {"wave_instructions": int(winst), "cycles": int(cycles),
+        roof["valu"] = {"frac": round((active - dual) / quads, 4),
+                        "issue_quads": int(active - dual), "simd_quads": int(quads),
+                        "dual_issue_share": round(dual / max(1.0, active), 4),
+                        "wave_instructions": int(winst), "cycles": int(cycles),
                         "lane_instructions_per_element": round(winst * 64 / max(1, n_el), 1),
-                        "issue_limit_wave_instructions": int(simds * cycles / 4),
-                        "frac": round(winst / (simds * cycles / 4), 4),
                         "clock_ghz_implied": round(cycles / (dom_avg_ms * 1e-3) / 1e9, 3),
-                        "how": "SQ_INSTS_VALU / (SIMDs x GRBM_GUI_ACTIVE/8 / 4), one rocprofv3 pass"}
+                        "how": "(SQ_ACTIVE_INST_VALU - SQ_ACTIVE_INST_VALU2) / (SIMDs x GRBM_GUI_ACTIVE/8 / 4), "
+                               "one rocprofv3 pass: the share of SIMD issue quad-cycles with VALU work"}
+        classes = {c[len("SQ_INSTS_VALU_"):].lower(): round(dc[c] * 64 / max(1, n_el), 2)
+                   for c in VALU_CLASSES if c in dc}
+        if classes:
+            roof["valu"]["lane_instructions_per_element_by_class"] = classes
         if args.config in ("poly", "poly64"):
             from cudacaml_amd.examples import refbench as RB
 

@@ -1531,6 +1531,8 @@ struct Lowering {
     for (int b : f.ident)
       if (prog.bufs[b].dt == DT::BOOL) rs_nt &= 1;
     const bool nt_loads = (rs_nt & (scan ? 4 : 2)) != 0, nt_stores = scan && (rs_nt & 1);
+    // 8-byte scans store pairs (rs_pairs8=0: 4-element groups)
+    const bool pairs8 = tune("rs_pairs8", 1) != 0;
     Params p;
     add_in(p, f);
     p.out.push_back(out);
@@ -1642,6 +1644,38 @@ struct Lowering {
     // taking the same groups it moved into LDS.
     auto store_tile = [&](const std::string &ktx, const std::string &tid, const std::string &buf) {
       std::ostringstream b;
+      if (vec && dt_size(n.dt) == 8 && pairs8) {
+        // 8-byte values in pairs: one 16-byte access a lane, consecutive
+        // lanes at consecutive addresses, so each store instruction writes
+        // whole lines (a 4-element group of 8-byte values is two 16-byte
+        // accesses 32 bytes apart, half-line writes in each instruction)
+        const std::string V2 = "cc_v2<" + T + ">";
+        // pair u of a lane lies 512 u elements past pair 0, 512 / W rows
+        // further down in the same column where W divides 512
+        const bool rows_step = 512 % W == 0;
+        b << "      {\n"
+          << "      const int q0_ = 2 * (int)(" << tid << "), rr0_ = q0_ / " << W << ", j0_ = q0_ - rr0_ * " << W << ";\n"
+          << "#pragma unroll\n"
+          << "      for (int u = 0; u < " << 2 * E << "; u++) {\n"
+          << "        const int c0 = (" << ktx << ") * " << W << ";\n"
+          << "        const int q = q0_ + 512 * u;\n";
+        if (rows_step)
+          b << "        const int rr = rr0_ + " << 512 / W << " * u, j = j0_;\n";
+        else
+          b << "        const int rr = q / " << W << ", j = q - rr * " << W << ";\n";
+        b << "        const int row = g0 + rr;\n"
+          << "        if (q < " << elems << " && row < " << rows << ") {\n"
+          << "          const int i = row * " << len << " + c0 + j;\n"
+          << "          const " << V2 << " o = ((const " << V2 << "*)" << buf << ")[(rr * " << S << " + j) / 2];\n";
+        if (nt_stores)
+          b << "          if (c0 + j < " << len << ") cc_st2_nt(b" << out << " + i, o);\n";
+        else
+          b << "          if (c0 + j < " << len << ") *(" << V2 << "*)(b" << out << " + i) = o;\n";
+        b << "        }\n"
+          << "      }\n"
+          << "      }\n";
+        return b.str();
+      }
       b << "#pragma unroll\n"
         << "      for (int u = 0; u < " << E << "; u++) {\n"
         << "        const int c0 = (" << ktx << ") * " << W << ";\n"
