@@ -2686,7 +2686,7 @@ struct Lowering {
   }
 
   // The runs of slice q over tiles [t_lo, t_hi) of a tile-local partition
-  // (`o`), 8 elements a lane, two groups of 8 a lane in flight. Each wave
+  // (`o`), 8 elements a lane, `ug` groups of 8 a lane in flight (UG_). Each wave
   // takes `tpw` tiles at a time (64, or fewer where a workgroup is expected
   // to have few tiles, so that every wave gets some): their run lengths in
   // groups of 8 are summed across the wave, and a lane finds its group's
@@ -2694,9 +2694,9 @@ struct Lowering {
   // consecutive groups. `loads` then `body` are emitted with pos_[u] (the
   // group's first element) and nv_[u] (its valid elements; 0 for a lane
   // without a group, whose pos_ still points into the pair arrays) for
-  // u = 0, 1 in scope.
+  // u in [0, UG_) in scope.
   static std::string runs_walk(const PassOut &o, int64_t threads, int64_t tiles_per_wg, const std::string &loads,
-                               const std::string &body) {
+                               const std::string &body, int64_t ug = 2) {
     int64_t tpw = 64;
     while (tpw > 1 && tpw * (threads / 64) > tiles_per_wg) tpw /= 2;
     std::ostringstream l;
@@ -2715,11 +2715,12 @@ struct Lowering {
       << "        if (lane_ >= d) in_ += o_;\n"
       << "      }\n"
       << "      const int tot_ = __shfl(in_, 63), ex_ = in_ - ng_;\n"
-      << "      for (int k0 = 0; k0 < tot_; k0 += 128) {\n"
-      << "        size_t pos_[2];\n"
-      << "        int nv_[2];\n"
+      << "      constexpr int UG_ = " << ug << ";\n"
+      << "      for (int k0 = 0; k0 < tot_; k0 += 64 * UG_) {\n"
+      << "        size_t pos_[UG_];\n"
+      << "        int nv_[UG_];\n"
       << "#pragma unroll\n"
-      << "        for (int u = 0; u < 2; u++) {\n"
+      << "        for (int u = 0; u < UG_; u++) {\n"
       << "          const int j = k0 + u * 64 + lane_;\n"
       << "          int i = 0;\n"
       << "#pragma unroll\n"
@@ -3543,6 +3544,9 @@ struct Lowering {
       // bin) runs here, in a second walk over the same pairs.
       const bool fuse_back = W == 1 && gather_back.count(t) > 0 && tune("scatter_fuse_back", 1) != 0;
       if (fuse_back) gather_back[t].fused = true;
+      // groups of 8 pairs a lane keeps in flight in the walks over the runs
+      const int64_t acc_groups = std::max<int64_t>(1, std::min<int64_t>(8, tune("acc_groups", 2)));
+      const int64_t back_groups = std::max<int64_t>(1, std::min<int64_t>(8, tune("gb_groups", 2)));
       std::ostringstream k;
       k << "extern \"C\" __global__ __launch_bounds__(" << AT << ") void " << kname << "_accumulate(const int* __restrict__ b"
         << lead << ", const int* __restrict__ b" << key << ", " << (fuse_back ? "" : "const ") << T << "* __restrict__ b"
@@ -3573,37 +3577,37 @@ struct Lowering {
           << "  typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));\n"
           << "  typedef __attribute__((ext_vector_type(4))) " << T << " v4;\n"
           << runs_walk(fin, AT, fin.windows ? cdiv(cdiv(N, fin.TILE), fin.P1) / W : fin.NTT / W,
-                       "        u16x8 kv[2];\n"
-                       "        v4 xa[2], xb[2];\n"
+                       "        u16x8 kv[UG_];\n"
+                       "        v4 xa[UG_], xb[UG_];\n"
                        "#pragma unroll\n"
-                       "        for (int u = 0; u < 2; u++) {\n"
+                       "        for (int u = 0; u < UG_; u++) {\n"
                        "          kv[u] = *(const u16x8*)(keys + pos_[u]);\n"
                        "          xa[u] = *(const v4*)(vals + pos_[u]);\n"
                        "          xb[u] = *(const v4*)(vals + pos_[u] + 4);\n"
                        "        }\n",
                        "#pragma unroll\n"
-                       "        for (int u = 0; u < 2; u++)\n"
+                       "        for (int u = 0; u < UG_; u++)\n"
                        "#pragma unroll\n"
                        "          for (int e = 0; e < 8; e++) {\n"
                        "            const bool in = e < nv_[u];\n"
                        "            cc_lds_add(&h[in ? kv[u][e] : 0], in ? (e < 4 ? xa[u][e] : xb[u][e - 4]) : " + z + ");\n"
-                       "          }\n")
+                       "          }\n", acc_groups)
           << "  __syncthreads();\n";
         if (fuse_back)
           k << "  " << T << "* const valw = b" << val << ";\n"
             << runs_walk(fin, AT, fin.windows ? cdiv(cdiv(N, fin.TILE), fin.P1) / W : fin.NTT / W,
-                         "        u16x8 kv[2];\n"
+                         "        u16x8 kv[UG_];\n"
                          "#pragma unroll\n"
-                         "        for (int u = 0; u < 2; u++) kv[u] = *(const u16x8*)(keys + pos_[u]);\n",
+                         "        for (int u = 0; u < UG_; u++) kv[u] = *(const u16x8*)(keys + pos_[u]);\n",
                          "#pragma unroll\n"
-                         "        for (int u = 0; u < 2; u++)\n"
+                         "        for (int u = 0; u < UG_; u++)\n"
                          "          if (nv_[u] > 0) {\n"
                          "            " + T + " x[8];\n"
                          "#pragma unroll\n"
                          "            for (int e = 0; e < 8; e++) x[e] = h[e < nv_[u] ? kv[u][e] : 0];\n"
                          "            *(v4*)(valw + pos_[u]) = (v4){x[0], x[1], x[2], x[3]};\n"
                          "            *(v4*)(valw + pos_[u] + 4) = (v4){x[4], x[5], x[6], x[7]};\n"
-                         "          }\n");
+                         "          }\n", back_groups);
       } else {
       k << "  const int s0 = b" << start << "[q], len = b" << start << "[q + 1] - s0;\n"
         << "  const int lo = s0 + (int)((long long)len * w / " << W << ");\n"
@@ -3956,18 +3960,18 @@ struct Lowering {
         k << "  const unsigned short* const keys = (const unsigned short*)b" << f.key << ";\n"
           << "  " << T << "* const vals = b" << f.val << ";\n"
           << runs_walk(f, GT, f.windows ? cdiv(cdiv(gb.N, f.TILE), f.P1) / Wg : f.NTT / Wg,
-                       "        u16x8 kv[2];\n"
+                       "        u16x8 kv[UG_];\n"
                        "#pragma unroll\n"
-                       "        for (int u = 0; u < 2; u++) kv[u] = *(const u16x8*)(keys + pos_[u]);\n",
+                       "        for (int u = 0; u < UG_; u++) kv[u] = *(const u16x8*)(keys + pos_[u]);\n",
                        "#pragma unroll\n"
-                       "        for (int u = 0; u < 2; u++)\n"
+                       "        for (int u = 0; u < UG_; u++)\n"
                        "          if (nv_[u] > 0) {\n"
                        "            " + T + " x[8];\n"
                        "#pragma unroll\n"
                        "            for (int e = 0; e < 8; e++) x[e] = tab[e < nv_[u] ? kv[u][e] : 0];\n"
                        "            *(v4*)(vals + pos_[u]) = (v4){x[0], x[1], x[2], x[3]};\n"
                        "            *(v4*)(vals + pos_[u] + 4) = (v4){x[4], x[5], x[6], x[7]};\n"
-                       "          }\n")
+                       "          }\n", tune("gb_groups", 2))
           << "}\n";
       } else {
       k << "  const int s0 = b" << f.start << "[q], len = b" << f.start << "[q + 1] - s0;\n"
