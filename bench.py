@@ -703,12 +703,15 @@ def main():
                         "issue_quads": int(active - dual), "simd_quads": int(quads),
                         "dual_issue_share": round(dual / max(1.0, active), 4),
                         "wave_instructions": int(winst), "cycles": int(cycles),
-                        "lane_instructions_per_element": round(winst * 64 / max(1, n_el), 1),
+                        "lane_instructions_per_element": round(winst * 64 / n_el, 1) if n_el >= 65536 else None,
                         "clock_ghz_implied": round(cycles / (dom_avg_ms * 1e-3) / 1e9, 3),
                         "how": "(SQ_ACTIVE_INST_VALU - SQ_ACTIVE_INST_VALU2) / (SIMDs x GRBM_GUI_ACTIVE/8 / 4), "
                                "one rocprofv3 pass: the share of SIMD issue quad-cycles with VALU work"}
-        classes = {c[len("SQ_INSTS_VALU_"):].lower(): round(dc[c] * 64 / max(1, n_el), 2)
-                   for c in VALU_CLASSES if c in dc}
+        # per element of the kernel's largest non-scratch operand; a kernel
+        # whose operands are all small (a reduction of values generated in
+        # the kernel) has no such count
+        classes = {c[len("SQ_INSTS_VALU_"):].lower(): round(dc[c] * 64 / n_el, 2)
+                   for c in VALU_CLASSES if c in dc} if n_el >= 65536 else {}
         if classes:
             roof["valu"]["lane_instructions_per_element_by_class"] = classes
         if args.config in ("poly", "poly64"):
