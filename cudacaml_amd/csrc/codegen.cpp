@@ -2086,15 +2086,18 @@ struct Lowering {
   };
   static TileShape tile_shape(int64_t len, DT dt) {
     const bool wide = dt_size(dt) == 8;
-    TileShape s;
-    s.NW = tune("lb_waves", 8) == 8 ? 8 : 4;
-    int64_t Umax = tune(wide ? "lb_slices8" : "lb_slices4", wide ? 8 : (s.NW == 8 ? 13 : 22));
-    if (Umax < 1) throw InvalidArgument("CCHIP_TUNE: look-back slices must be >= 1");
-    s.SL = 256 * s.NW;
-    s.U = std::min<int64_t>(Umax, std::max<int64_t>(1, cdiv(len, s.SL)));
-    s.tile = s.SL * s.U;
-    s.tpr = cdiv(len, s.tile);
-    return s;
+    auto shape = [&](int64_t NW) {
+      TileShape s;
+      s.NW = NW;
+      int64_t Umax = tune(wide ? "lb_slices8" : "lb_slices4", wide ? 8 : (s.NW == 8 ? 13 : 22));
+      if (Umax < 1) throw InvalidArgument("CCHIP_TUNE: look-back slices must be >= 1");
+      s.SL = 256 * s.NW;
+      s.U = std::min<int64_t>(Umax, std::max<int64_t>(1, cdiv(len, s.SL)));
+      s.tile = s.SL * s.U;
+      s.tpr = cdiv(len, s.tile);
+      return s;
+    };
+    return shape(tune("lb_waves", 8) == 8 ? 8 : 4);
   }
 
   // Whether a scan root takes the tile template with one tile a row (one
@@ -2337,8 +2340,13 @@ struct Lowering {
                 prog.bufs[out].bytes() < (int64_t(1) << 31);
     for (int b : f.ident) bufx = bufx && dt_size(prog.bufs[b].dt) == 4 && prog.bufs[b].bytes() < (int64_t(1) << 31);
     // Streaming (non-temporal) accesses, a bit mask: 1 stores, 2 loads.
-    int64_t scan_nt = tune("scan_nt", -1);
-    if (scan_nt < 0) scan_nt = narrow(f, n.dt) && streams(fn_bytes(f, rows * len) + rows * len * dt_size(n.dt)) ? 3 : 0;
+    // Look-back scans stream both; one-tile-a-row scans stream their stores
+    // only (config 2's step 0.482-0.484 -> 0.475-0.477 ms, the rows kernel
+    // 96 -> 89 us: their plain loads leave clean lines in the MALL where
+    // streamed ones measured slower; rt_nt=3 streams both).
+    int64_t scan_nt = tune(chained ? "scan_nt" : "rt_nt", -1);
+    if (scan_nt < 0)
+      scan_nt = narrow(f, n.dt) && streams(fn_bytes(f, rows * len) + rows * len * dt_size(n.dt)) ? (chained ? 3 : 1) : 0;
     if (n.dt == DT::BOOL) scan_nt = 0;
     for (int b : f.ident)
       if (prog.bufs[b].dt == DT::BOOL) scan_nt &= ~int64_t(2);
