@@ -3278,11 +3278,16 @@ struct Lowering {
             << "      typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));\n"
             << "      typedef __attribute__((ext_vector_type(4))) " << T << " v4;\n"
             << "      const size_t rb = (size_t)tt * " << o.RS << ";\n"
-            << "      for (int s = 8 * (int)threadIdx.x; s < tc[" << PB << "]; s += " << 8 * NT << ") {\n"
-            << "        *(u16x8*)(keys + rb + s) = *(const u16x8*)(sj + s);\n"
-            << "        *(v4*)(b" << o.val << " + rb + s) = *(const v4*)(sx + s);\n"
-            << "        *(v4*)(b" << o.val << " + rb + s + 4) = *(const v4*)(sx + s + 4);\n"
-            << "      }\n"
+            << "      for (int s = 8 * (int)threadIdx.x; s < tc[" << PB << "]; s += " << 8 * NT << ") {\n";
+          if (tune("sp_nt", 0) & 2)
+            k << "        __builtin_nontemporal_store(*(const u16x8*)(sj + s), (u16x8*)(keys + rb + s));\n"
+              << "        __builtin_nontemporal_store(*(const v4*)(sx + s), (v4*)(b" << o.val << " + rb + s));\n"
+              << "        __builtin_nontemporal_store(*(const v4*)(sx + s + 4), (v4*)(b" << o.val << " + rb + s + 4));\n";
+          else
+            k << "        *(u16x8*)(keys + rb + s) = *(const u16x8*)(sj + s);\n"
+              << "        *(v4*)(b" << o.val << " + rb + s) = *(const v4*)(sx + s);\n"
+              << "        *(v4*)(b" << o.val << " + rb + s + 4) = *(const v4*)(sx + s + 4);\n";
+          k << "      }\n"
             << "    }\n"
             << "    __syncthreads();\n"
             << "  }\n"
@@ -3471,7 +3476,9 @@ struct Lowering {
       return t;
     };
     first.vload_j = [&, oneline](const std::string &i) { return oneline(vec_loads(fi, i, "", tyof())); };
-    first.vload_jx = [&, oneline](const std::string &i) { return oneline(vec_loads(fboth, i, "", tyof())); };
+    first.vload_jx = [&, oneline](const std::string &i) {
+      return oneline(vec_loads(fboth, i, "", tyof(), (tune("sp_nt", 0) & 1) != 0));
+    };
     first.jv = [&](const std::string &i, int k) { return lane_call(fi, i, k); };
     first.xv = [&](const std::string &i, int k) { return lane_call(fs, i, k); };
     first.nvalid = std::to_string(N);
@@ -3588,10 +3595,14 @@ struct Lowering {
                        "        u16x8 kv[UG_];\n"
                        "        v4 xa[UG_], xb[UG_];\n"
                        "#pragma unroll\n"
-                       "        for (int u = 0; u < UG_; u++) {\n"
+                       "        for (int u = 0; u < UG_; u++) {\n" +
+                       std::string(tune("acc_nt", 0) ?
+                       "          kv[u] = __builtin_nontemporal_load((const u16x8*)(keys + pos_[u]));\n"
+                       "          xa[u] = __builtin_nontemporal_load((const v4*)(vals + pos_[u]));\n"
+                       "          xb[u] = __builtin_nontemporal_load((const v4*)(vals + pos_[u] + 4));\n" :
                        "          kv[u] = *(const u16x8*)(keys + pos_[u]);\n"
                        "          xa[u] = *(const v4*)(vals + pos_[u]);\n"
-                       "          xb[u] = *(const v4*)(vals + pos_[u] + 4);\n"
+                       "          xb[u] = *(const v4*)(vals + pos_[u] + 4);\n") +
                        "        }\n",
                        "#pragma unroll\n"
                        "        for (int u = 0; u < UG_; u++)\n"
@@ -4036,6 +4047,12 @@ struct Lowering {
       }
       const int64_t KM = o.kmax();
       const int64_t E = o.TILE / GT, VB = cdiv(o.TILE, 8 * GT);  // slots, 8-element groups per thread
+      // Streaming: 1 the output's stores, 2 the slot and region loads. The
+      // tile-local unpartition streams both (config 3: 139 -> 121 us, and
+      // the next step's partition 201 -> 191, its lines no longer dirty in
+      // the MALL); the two-level passes keep plain accesses (3b's last
+      // unpartition 146 -> 156 us streamed). gb_nt sets it.
+      const int64_t gbnt = tune("gb_nt", o.local && !o.windows ? 3 : 0);
       const std::string zero = zero_of(n.dt);
       if (o.windows) {
         // a window's region, read whole into LDS; each element of the
@@ -4060,7 +4077,9 @@ struct Lowering {
           << "#pragma unroll\n"
           << "  for (int u = 0; u < " << VR << "; u++) {\n"
           << "    const int s = 8 * ((int)threadIdx.x + " << GT << " * u);\n"
-          << "    if (s < tot) { ra[u] = *(const v4*)(rg + s); rc[u] = *(const v4*)(rg + s + 4); }\n"
+          << ((gbnt & 2) ? "    if (s < tot) { ra[u] = __builtin_nontemporal_load((const v4*)(rg + s)); "
+                                       "rc[u] = __builtin_nontemporal_load((const v4*)(rg + s + 4)); }\n"
+                                     : "    if (s < tot) { ra[u] = *(const v4*)(rg + s); rc[u] = *(const v4*)(rg + s + 4); }\n")
           << "  }\n"
           << "#pragma unroll\n"
           << "  for (int u = 0; u < " << VR << "; u++) {\n"
@@ -4099,7 +4118,8 @@ struct Lowering {
           << "#pragma unroll\n"
           << "  for (int u = 0; u < " << VB << "; u++) {\n"
           << "    const int i = t0 + 8 * ((int)threadIdx.x + " << GT << " * u);\n"
-          << "    if (i + 8 <= hi) sv[u] = *(const u16x8*)(sl + i);\n"
+          << ((gbnt & 2) ? "    if (i + 8 <= hi) sv[u] = __builtin_nontemporal_load((const u16x8*)(sl + i));\n"
+                                       : "    if (i + 8 <= hi) sv[u] = *(const u16x8*)(sl + i);\n")
           << "    else sv[u] = (u16x8)(unsigned short)0xffffu;\n"
           << "  }\n"
           << "  const int tot = ((const int2*)b" << o.meta << ")[(size_t)" << o.PB * o.NTT << " + blockIdx.x].x;\n"
@@ -4108,7 +4128,9 @@ struct Lowering {
           << "#pragma unroll\n"
           << "  for (int u = 0; u < " << VR << "; u++) {\n"
           << "    const int s = 8 * ((int)threadIdx.x + " << GT << " * u);\n"
-          << "    if (s < tot) { ra[u] = *(const v4*)(rg + s); rc[u] = *(const v4*)(rg + s + 4); }\n"
+          << ((gbnt & 2) ? "    if (s < tot) { ra[u] = __builtin_nontemporal_load((const v4*)(rg + s)); "
+                                       "rc[u] = __builtin_nontemporal_load((const v4*)(rg + s + 4)); }\n"
+                                     : "    if (s < tot) { ra[u] = *(const v4*)(rg + s); rc[u] = *(const v4*)(rg + s + 4); }\n")
           << "  }\n"
           << "#pragma unroll\n"
           << "  for (int u = 0; u < " << VR << "; u++) {\n"
@@ -4196,8 +4218,10 @@ struct Lowering {
         << "        bad = bad || v == 0xffffu;\n"
         << "      }\n"
         << "      const v4 a = {x[0], x[1], x[2], x[3]}, c = {x[4], x[5], x[6], x[7]};\n"
-        << "      *(v4*)(dst + i) = a;\n"
-        << "      *(v4*)(dst + i + 4) = c;\n"
+        << ((gbnt & 1) ? "      __builtin_nontemporal_store(a, (v4*)(dst + i));\n"
+                                     "      __builtin_nontemporal_store(c, (v4*)(dst + i + 4));\n"
+                                   : "      *(v4*)(dst + i) = a;\n"
+                                     "      *(v4*)(dst + i + 4) = c;\n")
         << "    } else {\n"
         << "      for (int e = i; e < hi; e++) {\n"
         << "        const unsigned v = sl[e];\n"
