@@ -251,6 +251,18 @@ class Gen {
 
   std::set<std::pair<int, int>> wide_pairs_;  // I32 operand pairs of those products
 
+ public:
+  // Row scans that also store each row's last element (the row's fold) in
+  // a side buffer: scan tensor -> (side buffer, row length); and the
+  // gathers that read only those elements (index p * L + L - 1 over the
+  // scan's rows), which read the side buffer at p instead. The index
+  // strings such a gather passes down map back to their row index.
+  std::map<int, std::pair<int, int64_t>> rowlast_;
+  std::map<int, int> rowlast_gather_;  // gather tensor -> scan tensor
+
+ private:
+  std::map<std::string, std::string> rowlast_idx_;
+
   Val wide_product(const Val &a, const Val &b) {
     auto w = wide_.find({a.s, b.s});
     if (w == wide_.end()) w = wide_.find({b.s, a.s});
@@ -306,6 +318,11 @@ class Gen {
       // computed here (loop-invariant) in place of reading the tensor's
       // buffer, 4 or 8 bytes an element
       r = inline_node(t, idx);
+    } else if (p_.materialized[t] && rowlast_.count(t) && rowlast_idx_.count(idx.s)) {
+      // the row's last element, from the scan's side buffer
+      const int b = rowlast_.at(t).first;
+      add_unique(ptrs_, b);
+      r = def(storage_vc(g_.ts[t].dt), "b" + std::to_string(b) + "[" + rowlast_idx_.at(idx.s) + "]");
     } else if (p_.materialized[t]) {
       int b = buf_of_[t];
       DT d = g_.ts[t].dt;
@@ -338,6 +355,16 @@ class Gen {
         return expr(n.body, {a, b}, idx, memo);
       }
       case TK::Gather: {
+        // A gather of the last element of every row of a row scan (index
+        // p * L + L - 1, in range by construction) reads the scan's side
+        // buffer at p where it reaches the scan's buffer.
+        auto rl = rowlast_gather_.find(t);
+        if (rl != rowlast_gather_.end()) {
+          const int64_t L = rowlast_.at(rl->second).second;
+          const std::string jn = "(" + idx.s + " * " + std::to_string(L) + " + " + std::to_string(L - 1) + ")";
+          rowlast_idx_[jn] = idx.s;
+          return elem(n.b, Val{jn, VC::I32});
+        }
         // out[i] = src[idx[i]], bounds-checked against the source extent:
         // the interpreter raises on an index out of range (R8); here the
         // kernel raises a flag the host turns into the same error.
@@ -1313,8 +1340,12 @@ struct Lowering {
     }
     prog.kernels[main].algo_bytes = bytes;
     // a reduction folded inside its input's map reads only the partials
-    // (scratch): it moves its output alone
+    // (scratch): it moves its output alone; a scan with a side buffer of
+    // row-last elements also writes that
     prog.kernels[main].moved_bytes = n.kind == TK::Reduce && fused_part_of_red.count(r) ? out : bytes;
+    const auto rl = gen.rowlast_.find(r);
+    if (n.kind == TK::Scan && rl != gen.rowlast_.end())
+      prog.kernels[main].moved_bytes += prog.bufs[rl->second.first].bytes();
   }
 
   // The fusion plan's algorithmic bytes of root r: each element it reads
@@ -1533,9 +1564,13 @@ struct Lowering {
     const bool nt_loads = (rs_nt & (scan ? 4 : 2)) != 0, nt_stores = scan && (rs_nt & 1);
     // 8-byte scans store pairs (rs_pairs8=0: 4-element groups)
     const bool pairs8 = tune("rs_pairs8", 1) != 0;
+    // a scan's side buffer of row-last elements (Gen::rowlast_), if any
+    const auto sd = scan ? gen.rowlast_.find(t) : gen.rowlast_.end();
+    const int side = sd != gen.rowlast_.end() ? sd->second.first : -1;
     Params p;
     add_in(p, f);
     p.out.push_back(out);
+    if (side >= 0) p.out.push_back(side);
     std::vector<int> args;
     std::string params = param_list(p, args);
     static const char *comp[] = {"x", "y", "z", "w"};
@@ -1735,6 +1770,9 @@ struct Lowering {
         << "      {\n      const int kt = kt0;\n" << step(0) << "      }\n"
         << "      if (kt0 + 1 < " << NT << ") {\n      const int kt = kt0 + 1;\n" << step(1) << "      }\n"
         << "    }\n";
+      if (scan && side >= 0)
+        k << "    if (threadIdx.x < " << R << " && g0 + threadIdx.x < " << rows << ") b" << side
+          << "[g0 + threadIdx.x] = acc;\n";
       if (scan)
         k << "    if (threadIdx.x >= 64) {\n" << store_tile(std::to_string(NT - 1), "lt", (NT - 1) % 2 ? "sm4b" : "sm4a")
           << "    }\n"
@@ -1760,8 +1798,8 @@ struct Lowering {
         << body("rg" + std::to_string(d)) << "      }\n";
     }
     k << "    }\n";
-    if (!scan)
-      k << "    if (threadIdx.x < " << R << " && g0 + threadIdx.x < " << rows << ") b" << out
+    if (!scan || side >= 0)
+      k << "    if (threadIdx.x < " << R << " && g0 + threadIdx.x < " << rows << ") b" << (scan ? side : out)
         << "[g0 + threadIdx.x] = acc;\n";
     k << "  }\n}\n";
     src << k.str();
@@ -2159,6 +2197,49 @@ struct Lowering {
       if (lead != s) sib_member.insert(s);
       for (int r : reds)
         if (r != lead) sib_member.insert(r);
+    }
+  }
+
+  // Gathers of the last element of every row of a row scan that folds one
+  // lane a row (the Monte Carlo paths' final prices: index p * 64 + 63).
+  // The scan also stores each row's fold, which is that element, in a side
+  // buffer of one value a row, and the gather reads it there: one
+  // contiguous read instead of one cache line per row of the scan's output
+  // (rowlast=0 keeps the strided reads). Eligible where the gather's
+  // source reaches the scan through element-wise nodes only, so that the
+  // scan's buffer is read at the gather's index.
+  void find_rowlast_gathers() {
+    if (!tune("rowlast", 1)) return;
+    std::function<bool(int, int)> reaches = [&](int t, int s) {
+      if (t == s) return true;
+      if (plan.materialized[t]) return false;
+      const TNode &n = g.ts[t];
+      switch (n.kind) {
+        case TK::Map:
+        case TK::Reshape: return reaches(n.a, s);
+        case TK::Map2: return reaches(n.a, s) || reaches(n.b, s);
+        default: return false;
+      }
+    };
+    for (size_t gi = 0; gi < g.ts.size(); gi++) {
+      const TNode &gn = g.ts[gi];
+      if (gn.kind != TK::Gather) continue;
+      const Aff a = aff_t(gn.a);
+      if (!a.ok) continue;
+      for (int s : plan.roots) {
+        const TNode &sn = g.ts[s];
+        if (sn.kind != TK::Scan || !plan.materialized[s] || sn.numel == 0) continue;
+        const int64_t L = row_length(sn.shape), R = sn.numel / L;
+        if (L < 2 || a.a != L || a.b != L - 1 || gn.numel != R) continue;
+        // the template that folds one lane a row, as lower_scan chooses it
+        if (!(R >= 1024 && !(tune("rs_tree", 1) && L >= tune("rs_tree_len", 2048) && any_order(sn.body, sn.dt, true))))
+          continue;
+        if (!reaches(gn.b, s)) continue;
+        if (!gen.rowlast_.count(s))
+          gen.rowlast_[s] = {add_buf("t" + std::to_string(sn.id) + "_last", sn.dt, R, BufRole::Computed), L};
+        gen.rowlast_gather_[(int)gi] = s;
+        break;
+      }
     }
   }
 
@@ -3980,16 +4061,21 @@ struct Lowering {
           << "  " << T << "* const vals = b" << f.val << ";\n"
           << runs_walk(f, GT, f.windows ? cdiv(cdiv(gb.N, f.TILE), f.P1) / Wg : f.NTT / Wg,
                        "        u16x8 kv[UG_];\n"
-                       "#pragma unroll\n"
-                       "        for (int u = 0; u < UG_; u++) kv[u] = *(const u16x8*)(keys + pos_[u]);\n",
+                       "#pragma unroll\n" +
+                           std::string("        for (int u = 0; u < UG_; u++) kv[u] = ") +
+                           ((tune("gs_nt", 0) & 2) ? "__builtin_nontemporal_load((const u16x8*)(keys + pos_[u]));\n"
+                                                   : "*(const u16x8*)(keys + pos_[u]);\n"),
                        "#pragma unroll\n"
                        "        for (int u = 0; u < UG_; u++)\n"
                        "          if (nv_[u] > 0) {\n"
                        "            " + T + " x[8];\n"
                        "#pragma unroll\n"
                        "            for (int e = 0; e < 8; e++) x[e] = tab[e < nv_[u] ? kv[u][e] : 0];\n"
-                       "            *(v4*)(vals + pos_[u]) = (v4){x[0], x[1], x[2], x[3]};\n"
-                       "            *(v4*)(vals + pos_[u] + 4) = (v4){x[4], x[5], x[6], x[7]};\n"
+                       + std::string((tune("gs_nt", 0) & 1)
+                           ? "            __builtin_nontemporal_store((v4){x[0], x[1], x[2], x[3]}, (v4*)(vals + pos_[u]));\n"
+                             "            __builtin_nontemporal_store((v4){x[4], x[5], x[6], x[7]}, (v4*)(vals + pos_[u] + 4));\n"
+                           : "            *(v4*)(vals + pos_[u]) = (v4){x[0], x[1], x[2], x[3]};\n"
+                             "            *(v4*)(vals + pos_[u] + 4) = (v4){x[4], x[5], x[6], x[7]};\n") +
                        "          }\n", tune("gb_groups", 2))
           << "}\n";
       } else {
@@ -4750,6 +4836,12 @@ struct Lowering {
         fused_red_of_map[m] = r;
       }
     find_sibling_groups();
+    find_rowlast_gathers();
+    // the side buffers are computed buffers too: allocated with the others
+    // for the program's lifetime
+    for (size_t b = ncomputed; b < prog.bufs.size(); b++)
+      if (prog.bufs[b].role != BufRole::Computed) throw Failure("Lower: a scratch buffer before the roots");
+    ncomputed = (int)prog.bufs.size();
     std::vector<std::vector<int>> launches;
     std::vector<std::vector<int>> scratch_of;
     for (int r : plan.roots) {

@@ -274,6 +274,57 @@ def test_sibling_group_runs_before_a_consumer_of_its_first_root(device):
     check(g, [("x", data(F32, (rows, n), 62))], ["scan_tile_fold"])
 
 
+ROWLAST_CASES = [
+    # (rows, len, dtype, knobs): Monte Carlo's shape, ragged rows, long rows
+    # folded in order with split roles, 8-byte values, two tiles in flight
+    (1024, 64, I32, ""),
+    (1500, 333, I32, ""),
+    (2048, 9000, I32, "rs_tree=0"),
+    (1030, 64, F64, ""),
+    (4096, 64, F32, ""),
+    (1100, 70, I32, "rs_depth=2"),
+]
+
+
+def row_last_graph(rows, n, dtype):
+    """A row scan with a non-identity init; every row's last element
+    gathered through a map over the scan and another tensor of the same
+    shape, then output and summed: the Monte Carlo paths' final prices."""
+    x = D.param("x", dtype, (rows, n))
+    y = D.param("y", dtype, (rows, n))
+    p = D.scan_rows(D.add, D.const(dtype, 5), x)
+    m = D.map2(lambda a, b: D.add(D.mul(a, D.const(dtype, 3)), b), p, y)
+    idx = D.map(lambda i: D.add(D.mul(i, D.const(I32, n)), D.const(I32, n - 1)), D.iota((rows,)))
+    last = D.gather(idx, m)
+    return Graph.create("rowlast", [("last", last), ("s", D.reduce(D.add, D.const(dtype, 0), last))])
+
+
+@pytest.mark.parametrize("rows,n,dtype,knobs", ROWLAST_CASES, ids=lambda v: str(v))
+def test_row_last_gather_reads_the_scans_side_buffer(device, monkeypatch, rows, n, dtype, knobs):
+    """The gathered last elements come from the scan's side buffer: against
+    the oracle (integers bit for bit), and bit for bit against the strided
+    reads of the scan's output (rowlast=0)."""
+    if knobs:
+        monkeypatch.setenv("CCHIP_TUNE", knobs)
+    g = row_last_graph(rows, n, dtype)
+    assert "_last" in H.plan(g)
+    ins = [("x", data(dtype, (rows, n), 71)), ("y", data(dtype, (rows, n), 72))]
+    check(g, ins, ["scan_rowseq"])
+    c = H.compile(g)
+    try:
+        got = dict(H.run(c, ins))
+    finally:
+        c.release()
+    monkeypatch.setenv("CCHIP_TUNE", ",".join(k for k in (knobs, "rowlast=0") if k))
+    assert "_last" not in H.plan(g)
+    c = H.compile(g)
+    try:
+        ref = dict(H.run(c, ins))
+    finally:
+        c.release()
+    np.testing.assert_array_equal(got["last"], ref["last"])
+
+
 FOLDED_CASES = [((1 << 16) + 3, F32, "add"), ((1 << 22) + 5, F32, "add"), ((1 << 20) + 2, F64, "add"),
                 (300 * 1024 + 5, F32, "add"), (1 << 18, F32, "add"), (102421, F32, "max"),
                 ((1 << 22) + 1, I32, "add"), ((1 << 20) + 7, F32, "max"), (1 << 23, I32, "max"),

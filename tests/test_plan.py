@@ -375,3 +375,53 @@ def test_broadcast_read_in_place_by_its_consumers(monkeypatch):
     _launch_uses_live_buffers(g5)
     monkeypatch.setenv("CCHIP_TUNE", "remat_broadcast=0")
     assert "elided" not in [r for _, _, _, r in parse(H.plan(g))[0]] and len(kernels_of(g)) == 3
+
+
+def _last_col_graph(rows, n, dtype, last=None, second=False):
+    """A row scan whose rows' last elements (or the elements at column
+    `last`) are gathered through a map, then summed."""
+    x = D.param("x", dtype, (rows, n))
+    p = D.scan_rows(D.add, D.const(dtype, 0), x)
+    if second:
+        y = D.param("y", dtype, (rows, n))
+        p = D.map2(D.add, p, y)
+    col = n - 1 if last is None else last
+    idx = D.map(lambda i: D.add(D.mul(i, D.const(I32, n)), D.const(I32, col)), D.iota((rows,)))
+    g = D.gather(idx, D.map(lambda v: D.mul(v, D.const(dtype, 3)), p))
+    return Graph.create("lastcol", [("s", D.reduce(D.add, D.const(dtype, 0), g))])
+
+
+def _reads(g):
+    names, out = {}, {}
+    for f in (l.split() for l in H.plan(g).splitlines()):
+        if f[0] == "buffer":
+            names[f[1]] = f[2]
+        elif f[0] == "kernel":
+            out[f[2]] = [names[a] for a in f[f.index("args") + 1:]]
+    return out
+
+
+def test_row_last_gather_reads_the_scans_side_buffer(monkeypatch):
+    """A gather of every row's last element of a scan that folds one lane
+    a row (config 5's final prices) reads a side buffer the scan writes,
+    one value a row, instead of one cache line per row of the scan's
+    output; other columns, tile-scanned rows and rowlast=0 keep the
+    strided read."""
+    from cudacaml_amd.examples import configs as C
+
+    r = _reads(C.mc_paths(4096, 64))
+    assert any(a.endswith("_last") for a in r["scan_rowseq"])
+    assert any(a.endswith("_last") for a in r["reduce_split"])
+    g = _last_col_graph(2048, 100, I32)
+    r = _reads(g)
+    side = [a for a in r["scan_rowseq"] if a.endswith("_last")]
+    assert len(side) == 1 and side[0] in r["reduce_wave"]
+    assert not any(a.endswith("_last") for a in _reads(_last_col_graph(2048, 100, I32, last=98))["scan_rowseq"])
+    # a map over another tensor of the same shape between: that tensor is
+    # read at the gathered index, the scan from its side buffer
+    r = _reads(_last_col_graph(2048, 100, F32, second=True))
+    assert "p_y" in r["reduce_wave"] and any(a.endswith("_last") for a in r["reduce_wave"])
+    # rows long enough for the tile scan: no side buffer
+    assert "_last" not in H.plan(_last_col_graph(2048, 4096, I32))
+    monkeypatch.setenv("CCHIP_TUNE", "rowlast=0")
+    assert "_last" not in H.plan(C.mc_paths(4096, 64))
