@@ -11,6 +11,7 @@ import oracle
 from cudacaml_amd import backend_hip as H
 from cudacaml_amd import differential as Diff
 from cudacaml_amd import dsl as D
+from cudacaml_amd.examples import black_scholes as bs
 from cudacaml_amd.examples import configs as C
 from cudacaml_amd.examples import programs as P
 from cudacaml_amd.examples import refbench as RB
@@ -928,6 +929,26 @@ KNOB_CASES = [
         D.map(lambda p: D.add(D.mul(p, D.const(I32, 3)), D.const(I32, 1)), D.iota((100003,))),
         D.param("src", F32, (100003,)), (300014,)))]),
      lambda: [("src", data(F32, (100003,), 81))], "scatter_affine"),
+    # 8-byte row scans storing 4-element groups instead of pairs
+    ("rs_pairs8=0", lambda: Graph.create("s", [("p", D.scan_rows(D.add, D.const(F64, 1.0), D.param("x", F64, (1030, 68))))]),
+     lambda: [("x", data(F64, (1030, 68), 82))], "scan_rowseq"),
+    ("rs_pairs8=1,rs_nt=1", lambda: Graph.create("s", [("p", D.scan_rows(D.add, D.const(I64, 3), D.param("x", I64, (1100, 36))))]),
+     lambda: [("x", data(I64, (1100, 36), 83))], "scan_rowseq"),
+    # one-tile-a-row scans with every streaming mask
+    ("rt_nt=3", lambda: Graph.create("s", [("p", D.scan_rows(D.max, D.const(I32, -7), D.param("x", I32, (300, 5001))))]),
+     lambda: [("x", data(I32, (300, 5001), 84))], "scan_tile"),
+    ("rt_nt=2", lambda: sibling_graph(I32, 600, 3001), lambda: [("x", data(I32, (600, 3001), 85))], "scan_tile_fold"),
+    ("rt_nt=0", lambda: sibling_graph(I32, 600, 3000), lambda: [("x", data(I32, (600, 3000), 86))], "scan_tile_fold"),
+    # the scatter chain's streaming and walk depths (tile-local partition;
+    # two levels with windows)
+    ("sp_nt=3,acc_nt=1,gs_nt=3,gb_nt=0", lambda: C.scatter_gather(200003, 1 << 18, I32),
+     lambda: [("idx", scatter_idx(87, 200003, 1 << 18)), ("src", data(I32, (200003,), 88))], "gather_unpartition"),
+    ("acc_groups=4,gb_groups=3", lambda: C.scatter_gather(200003, 1 << 18, I32),
+     lambda: [("idx", scatter_idx(89, 200003, 1 << 18)), ("src", data(I32, (200003,), 90))], "scatter_accumulate"),
+    ("gb_nt=3,gs_nt=2,acc_groups=3", lambda: C.scatter_gather(300001, 1 << 24, I32),
+     lambda: [("idx", scatter_idx(91, 300001, 1 << 24)), ("src", data(I32, (300001,), 92))], "scatter_windows"),
+    # the final prices read through the strided gather again
+    ("rowlast=0", lambda: C.mc_paths(2048, 64), lambda: bs.inputs(F32, seed=7), "scan_rowseq"),
 ]
 
 
