@@ -1344,7 +1344,7 @@ struct Lowering {
     // row-last elements also writes that
     prog.kernels[main].moved_bytes = n.kind == TK::Reduce && fused_part_of_red.count(r) ? out : bytes;
     const auto rl = gen.rowlast_.find(r);
-    if (n.kind == TK::Scan && rl != gen.rowlast_.end())
+    if (rl != gen.rowlast_.end())
       prog.kernels[main].moved_bytes += prog.bufs[rl->second.first].bytes();
   }
 
@@ -1381,13 +1381,24 @@ struct Lowering {
     int out = buf_of[t];
     ElemFn f = gen.element_fn("f_" + std::to_string(n.id), t, true, true);
     src << f.code;
+    // a side buffer of each row's last element (Gen::rowlast_), if a later
+    // gather reads only those
+    const auto sd = gen.rowlast_.find(t);
+    const int side = sd != gen.rowlast_.end() ? sd->second.first : -1;
+    const int64_t SL_ = side >= 0 ? sd->second.second : 0;
     Params p;
     add_in(p, f);
     p.out.push_back(out);
+    if (side >= 0) p.out.push_back(side);
     std::vector<int> args;
     std::string params = param_list(p, args);
     int64_t N = n.numel;
     if (N == 0) return {};
+    // the side store of element e holding v
+    auto side_st = [&](const std::string &e, const std::string &v) {
+      return "if ((" + e + ") % " + std::to_string(SL_) + " == " + std::to_string(SL_ - 1) + ") b" +
+             std::to_string(side) + "[(" + e + ") / " + std::to_string(SL_) + "] = " + v + ";";
+    };
     std::string T = dt_ctype(n.dt);
     // Non-temporal streaming accesses when the kernel also gathers or moves
     // more than the MALL holds (mode 1), always (2) or never (0).
@@ -1472,6 +1483,9 @@ struct Lowering {
         k << "    cc_st" << G << "_nt(b" << out << " + i, r);\n";
       else
         k << "    *(" << VG << "<" << T << ">*)(b" << out << " + i) = r;\n";
+      if (side >= 0)
+        for (int u = 0; u < G; u++)
+          k << "    " << side_st("i + " + std::to_string(u), std::string("r.") + comp[u]) << "\n";
       if (fuse)
         for (int u = 0; u < G; u++) k << "    " << fold_in(rc, T, std::string("r.") + comp[u]) << "\n";
     } else {
@@ -1491,6 +1505,10 @@ struct Lowering {
           k << "cc_st" << G << "_nt(b" << out << " + " << iq << ", r[" << q << "]);\n";
         else
           k << "*(" << VG << "<" << T << ">*)(b" << out << " + " << iq << ") = r[" << q << "];\n";
+        // a clamped group stores its owner's values again, here as there
+        if (side >= 0)
+          for (int u = 0; u < G; u++)
+            k << "    " << side_st(iq + " + " + std::to_string(u), "r[" + std::to_string(q) + "]." + comp[u]) << "\n";
       }
       // a clamped group is its owner's: folded once, by the owner
       if (fuse)
@@ -1501,9 +1519,10 @@ struct Lowering {
     }
     k << "  }\n"
       << "  for (int i = nvec * " << G << " + blockIdx.x * 256 + threadIdx.x; i < " << N << "; i += gridDim.x * 256)";
-    if (fuse)
+    if (fuse || side >= 0)
       k << " {\n    const " << T << " v_ = " << f.call_scalar("i") << ";\n    b" << out << "[i] = v_;\n    "
-        << fold_in(rc, T, "v_") << "\n  }\n";
+        << (fuse ? fold_in(rc, T, "v_") : std::string()) << (side >= 0 ? side_st("i", "v_") : std::string())
+        << "\n  }\n";
     else
       k << "\n    b" << out << "[i] = " << f.call_scalar("i") << ";\n";
     if (fuse)
@@ -2228,11 +2247,15 @@ struct Lowering {
       if (!a.ok) continue;
       for (int s : plan.roots) {
         const TNode &sn = g.ts[s];
-        if (sn.kind != TK::Scan || !plan.materialized[s] || sn.numel == 0) continue;
+        const bool map = (sn.kind == TK::Map || sn.kind == TK::Map2) && !gen.uniform(s);
+        if ((sn.kind != TK::Scan && !map) || !plan.materialized[s] || sn.numel == 0) continue;
         const int64_t L = row_length(sn.shape), R = sn.numel / L;
         if (L < 2 || a.a != L || a.b != L - 1 || gn.numel != R) continue;
-        // the template that folds one lane a row, as lower_scan chooses it
-        if (!(R >= 1024 && !(tune("rs_tree", 1) && L >= tune("rs_tree_len", 2048) && any_order(sn.body, sn.dt, true))))
+        // a scan: the template that folds one lane a row, as lower_scan
+        // chooses it; a map root: the map template, which stores each
+        // row's last element as it computes it
+        if (!map && !(R >= 1024 && !(tune("rs_tree", 1) && L >= tune("rs_tree_len", 2048) &&
+                                     any_order(sn.body, sn.dt, true))))
           continue;
         if (!reaches(gn.b, s)) continue;
         if (!gen.rowlast_.count(s))

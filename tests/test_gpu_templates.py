@@ -326,6 +326,52 @@ def test_row_last_gather_reads_the_scans_side_buffer(device, monkeypatch, rows, 
     np.testing.assert_array_equal(got["last"], ref["last"])
 
 
+ROWLAST_MAP_CASES = [
+    # (rows, len, dtype, knobs): the Greeks' paths tensor's shape; rows not
+    # a multiple of the 4-element groups; a tail past the last group; 8-byte
+    # groups of 2; two groups a lane (clamped last groups)
+    (1024, 64, F32, ""),
+    (1030, 70, I32, ""),
+    (301, 7, I32, ""),
+    (1000, 63, F64, ""),
+    (1030, 66, I32, "map_unroll=2"),
+]
+
+
+def row_last_map_graph(rows, n, dtype):
+    """A map materialised because two roots read it (the Greeks' paths);
+    every row's last element gathered through another map, and output."""
+    x = D.param("x", dtype, (rows, n))
+    m = D.map(lambda v: D.add(D.mul(v, D.const(dtype, 2)), D.const(dtype, 1)), x)
+    idx = D.map(lambda i: D.add(D.mul(i, D.const(I32, n)), D.const(I32, n - 1)), D.iota((rows,)))
+    last = D.gather(idx, D.map(lambda v: D.mul(v, D.const(dtype, 3)), m))
+    return Graph.create("rowlastm", [("last", last), ("t", D.reduce_rows(D.max, D.const(dtype, -100), m))])
+
+
+@pytest.mark.parametrize("rows,n,dtype,knobs", ROWLAST_MAP_CASES, ids=lambda v: str(v))
+def test_row_last_gather_reads_the_maps_side_buffer(device, monkeypatch, rows, n, dtype, knobs):
+    """The same for a materialised map root: the map template stores each
+    row's last element as it computes it."""
+    if knobs:
+        monkeypatch.setenv("CCHIP_TUNE", knobs)
+    g = row_last_map_graph(rows, n, dtype)
+    assert "_last" in H.plan(g)
+    ins = [("x", data(dtype, (rows, n), 73))]
+    check(g, ins, ["map"])
+    c = H.compile(g)
+    try:
+        got = dict(H.run(c, ins))
+    finally:
+        c.release()
+    monkeypatch.setenv("CCHIP_TUNE", ",".join(k for k in (knobs, "rowlast=0") if k))
+    c = H.compile(g)
+    try:
+        ref = dict(H.run(c, ins))
+    finally:
+        c.release()
+    np.testing.assert_array_equal(got["last"], ref["last"])
+
+
 FOLDED_CASES = [((1 << 16) + 3, F32, "add"), ((1 << 22) + 5, F32, "add"), ((1 << 20) + 2, F64, "add"),
                 (300 * 1024 + 5, F32, "add"), (1 << 18, F32, "add"), (102421, F32, "max"),
                 ((1 << 22) + 1, I32, "add"), ((1 << 20) + 7, F32, "max"), (1 << 23, I32, "max"),

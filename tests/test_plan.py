@@ -423,5 +423,12 @@ def test_row_last_gather_reads_the_scans_side_buffer(monkeypatch):
     assert "p_y" in r["reduce_wave"] and any(a.endswith("_last") for a in r["reduce_wave"])
     # rows long enough for the tile scan: no side buffer
     assert "_last" not in H.plan(_last_col_graph(2048, 4096, I32))
+    # a materialised map root (the Greeks' paths tensor): its kernel writes
+    # the side buffer, and the final-price map reads it
+    lines = [l.split() for l in H.plan(C.mc_greeks(4096, 64)).splitlines()]
+    side = [f[1] for f in lines if f[0] == "buffer" and f[2].endswith("_last")]
+    users = [f[2] for f in lines if f[0] == "kernel" and side and side[0] in f[f.index("args") + 1:]]
+    assert len(side) == 1 and users == ["map", "map"]
     monkeypatch.setenv("CCHIP_TUNE", "rowlast=0")
     assert "_last" not in H.plan(C.mc_paths(4096, 64))
+    assert "_last" not in H.plan(C.mc_greeks(4096, 64))
