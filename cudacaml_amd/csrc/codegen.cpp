@@ -256,12 +256,15 @@ class Gen {
   // a side buffer: scan tensor -> (side buffer, row length); and the
   // gathers that read only those elements (index p * L + L - 1 over the
   // scan's rows), which read the side buffer at p instead. The index
-  // strings such a gather passes down map back to their row index.
+  // strings such a gather passes down map back to their row index and the
+  // row length they were made with: another tensor with a side buffer,
+  // reached at the same index, reads its buffer only if its rows are as
+  // long (through a reshape they need not be).
   std::map<int, std::pair<int, int64_t>> rowlast_;
   std::map<int, int> rowlast_gather_;  // gather tensor -> scan tensor
 
  private:
-  std::map<std::string, std::string> rowlast_idx_;
+  std::map<std::string, std::pair<std::string, int64_t>> rowlast_idx_;
 
   Val wide_product(const Val &a, const Val &b) {
     auto w = wide_.find({a.s, b.s});
@@ -318,11 +321,12 @@ class Gen {
       // computed here (loop-invariant) in place of reading the tensor's
       // buffer, 4 or 8 bytes an element
       r = inline_node(t, idx);
-    } else if (p_.materialized[t] && rowlast_.count(t) && rowlast_idx_.count(idx.s)) {
+    } else if (p_.materialized[t] && rowlast_.count(t) && rowlast_idx_.count(idx.s) &&
+               rowlast_idx_.at(idx.s).second == rowlast_.at(t).second) {
       // the row's last element, from the scan's side buffer
       const int b = rowlast_.at(t).first;
       add_unique(ptrs_, b);
-      r = def(storage_vc(g_.ts[t].dt), "b" + std::to_string(b) + "[" + rowlast_idx_.at(idx.s) + "]");
+      r = def(storage_vc(g_.ts[t].dt), "b" + std::to_string(b) + "[" + rowlast_idx_.at(idx.s).first + "]");
     } else if (p_.materialized[t]) {
       int b = buf_of_[t];
       DT d = g_.ts[t].dt;
@@ -362,7 +366,7 @@ class Gen {
         if (rl != rowlast_gather_.end()) {
           const int64_t L = rowlast_.at(rl->second).second;
           const std::string jn = "(" + idx.s + " * " + std::to_string(L) + " + " + std::to_string(L - 1) + ")";
-          rowlast_idx_[jn] = idx.s;
+          rowlast_idx_[jn] = {idx.s, L};
           return elem(n.b, Val{jn, VC::I32});
         }
         // out[i] = src[idx[i]], bounds-checked against the source extent:

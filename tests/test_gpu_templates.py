@@ -326,6 +326,19 @@ def test_row_last_gather_reads_the_scans_side_buffer(device, monkeypatch, rows, 
     np.testing.assert_array_equal(got["last"], ref["last"])
 
 
+@pytest.mark.parametrize("dtype", [I32, F32])
+def test_row_last_side_buffer_only_for_rows_as_long(device, dtype):
+    """Two scans with side buffers (rows 100 and 50 long); the first
+    gather's source adds the second scan reshaped to 100-long rows, which
+    it must read in that scan's own buffer (at p * 100 + 99, the last
+    element of its row 2p + 1), not in its side buffer at p."""
+    from test_plan import _mixed_row_last_graph
+
+    g = _mixed_row_last_graph(dtype)
+    ins = [("x", data(dtype, (2048, 100), 74)), ("y", data(dtype, (4096, 50), 75))]
+    check(g, ins, ["scan_rowseq"])
+
+
 ROWLAST_MAP_CASES = [
     # (rows, len, dtype, knobs): the Greeks' paths tensor's shape; rows not
     # a multiple of the 4-element groups; a tail past the last group; 8-byte

@@ -401,6 +401,37 @@ def _reads(g):
     return out
 
 
+def _mixed_row_last_graph(dtype):
+    """Two row scans with side buffers, of rows 100 and 50 long; the first
+    gather's source adds the second scan reshaped to the first's rows, so
+    it reads that scan at p * 100 + 99, the last element of its row 2p + 1."""
+    x = D.param("x", dtype, (2048, 100))
+    y = D.param("y", dtype, (4096, 50))
+    p = D.scan_rows(D.add, D.const(dtype, 5), x)
+    q = D.scan_rows(D.add, D.const(dtype, 0), y)
+    i2 = D.map(lambda i: D.add(D.mul(i, D.const(I32, 50)), D.const(I32, 49)), D.iota((4096,)))
+    m = D.map2(D.add, p, D.reshape((2048, 100), q))
+    i1 = D.map(lambda i: D.add(D.mul(i, D.const(I32, 100)), D.const(I32, 99)), D.iota((2048,)))
+    return Graph.create("rowlast_mixed", [("last1", D.gather(i1, m)), ("last2", D.gather(i2, q))])
+
+
+def test_row_last_side_buffer_only_for_rows_as_long():
+    """A tensor with a side buffer, reached by another gather whose rows
+    have another length, is read in its own buffer at the gathered index,
+    not in its side buffer at the other gather's row index."""
+    lines = [l.split() for l in H.plan(_mixed_row_last_graph(I32)).splitlines()]
+    names = {f[1]: f[2] for f in lines if f[0] == "buffer"}
+    kernels = [[names[a] for a in f[f.index("args") + 1:]] for f in lines if f[0] == "kernel"]
+    scans = [k for k in kernels if k[0] in ("p_x", "p_y")]
+    px_out, px_side = scans[0][1], scans[0][2]
+    py_out, py_side = scans[1][1], scans[1][2]
+    assert px_side.endswith("_last") and py_side.endswith("_last")
+    readers = [k for k in kernels if k not in scans]
+    last1 = [k for k in readers if px_side in k]
+    assert len(last1) == 1 and last1[0][:2] == [px_side, py_out]
+    assert [k[:1] for k in readers if k is not last1[0]] == [[py_side]]
+
+
 def test_row_last_gather_reads_the_scans_side_buffer(monkeypatch):
     """A gather of every row's last element of a scan that folds one lane
     a row (config 5's final prices) reads a side buffer the scan writes,
