@@ -1008,6 +1008,43 @@ KNOB_CASES = [
      lambda: [("idx", scatter_idx(91, 300001, 1 << 24)), ("src", data(I32, (300001,), 92))], "scatter_windows"),
     # the final prices read through the strided gather again
     ("rowlast=0", lambda: C.mc_paths(2048, 64), lambda: bs.inputs(F32, seed=7), "scan_rowseq"),
+    # the map's loads and stores streamed each on its own
+    ("map_ntl=0,map_nts=1", lambda: P.chain(300007).graph(), lambda: P.chain(300007).inputs(), "map"),
+    ("map_ntl=1,map_nts=0", lambda: P.chain(300007).graph(), lambda: P.chain(300007).inputs(), "map"),
+    # every streaming default taken as if the tensors were large
+    ("nt_bytes=0", lambda: C.rows(2048, 1000), lambda: [("x", data(F32, (2048, 1000), 101))], "scan_rowseq"),
+    ("nt_bytes=0", lambda: C.scatter_gather(200003, 1 << 18, F32),
+     lambda: [("idx", scatter_idx(102, 200003, 1 << 18)), ("src", data(F32, (200003,), 103))], "gather_unpartition"),
+    ("red_nt=1", lambda: Graph.create("r", [("s", D.reduce(D.add, D.const(F32, 0.5), D.param("x", F32, (300001,))))]),
+     lambda: [("x", data(F32, (300001,), 104))], "reduce_split"),
+    ("red_nt=1", lambda: Graph.create("r", [("m", D.reduce_rows(D.max, D.const(F32, 0), D.param("x", F32, (64, 30001))))]),
+     lambda: [("x", data(F32, (64, 30001), 105))], "reduce_split"),
+    # the counted partition's bucket counters in one and two copies
+    ("scatter_local_max=0,scatter_count_copies=1", lambda: C.scatter_gather((1 << 20) + 37, 1 << 16, F32),
+     lambda: [("idx", scatter_idx(106, (1 << 20) + 37, 1 << 16)), ("src", data(F32, ((1 << 20) + 37,), 107))],
+     "scatter_count"),
+    ("scatter_local_max=0,scatter_count_copies=2", lambda: scatter_graph(300001, 70000, I32),
+     lambda: [("idx", scatter_idx(108, 300001, 70000)), ("src", data(I32, (300001,), 109))], "scatter_count"),
+    # shapes: the one-slice fold over three workgroups, 128 KiB slice
+    # tables, few accumulate workgroups, two levels from eight slices up,
+    # 4096-element partition tiles
+    ("scatter_direct_wgs=3", lambda: scatter_graph(300001, 5000, F32),
+     lambda: [("idx", scatter_idx(110, 300001, 5000)), ("src", data(F32, (300001,), 111))], "scatter_direct"),
+    ("scatter_slice_lds=131072,scatter_slice_bins=32768", lambda: C.scatter_gather(300001, 1 << 18, F32),
+     lambda: [("idx", scatter_idx(112, 300001, 1 << 18)), ("src", data(F32, (300001,), 113))], "gather_unpartition"),
+    ("scatter_slice_wgs=64", lambda: C.scatter_gather(300001, 70000, F32),
+     lambda: [("idx", scatter_idx(114, 300001, 70000)), ("src", data(F32, (300001,), 115))], "scatter_accumulate"),
+    ("scatter_stage_p=8", lambda: C.scatter_gather(300001, 1 << 18, F32),
+     lambda: [("idx", scatter_idx(116, 300001, 1 << 18)), ("src", data(F32, (300001,), 117))], "scatter_coarse"),
+    ("scatter_tile=4096", lambda: C.scatter_gather(300001, 70000, F32),
+     lambda: [("idx", scatter_idx(118, 300001, 70000)), ("src", data(F32, (300001,), 119))], "scatter_partition"),
+    # split-k taken at a shorter k, and refused
+    ("mm_splitk_min_k=1024", lambda: C.matmul(3, F64, k=2048, m=3),
+     lambda: [("a", data(F64, (3, 2048), 120)), ("b", data(F64, (2048, 3), 121))], "matmul_splitk"),
+    ("mm_splitk_outputs=0", lambda: C.matmul(3, F64, k=65536, m=3),
+     lambda: [("a", data(F64, (3, 65536), 122)), ("b", data(F64, (65536, 3), 123))], "matmul_tiled"),
+    # a one-kernel program replayed from a recorded HIP graph
+    ("graphs=1,graph_min_kernels=1", lambda: P.chain(5000).graph(), lambda: P.chain(5000).inputs(), "map"),
 ]
 
 
