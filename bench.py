@@ -745,6 +745,17 @@ def main():
         roof["launch_ms_best"] = round(min(each), 4)
         roof["launch_ms_median"] = round(statistics.median(each), 4)
     roof["traffic_detail"] = traffic_detail
+    # the other kernels that move a root's bytes: counter traffic per launch
+    # beside the bytes each moves, from the same counter passes
+    others = []
+    for k, (role, moved, _, _) in sorted(kinfo.items()):
+        if k == dom or moved <= 0:
+            continue
+        t, _ = traffic_of(counters, k)
+        if t is not None:
+            others.append({"kernel": k, "template": role, "moved_bytes": moved, "traffic": t})
+    if others:
+        roof["other_kernels"] = others
 
     whole = None
     vs_baseline, vs_basis = None, None
