@@ -24,7 +24,7 @@ _lib = None
 
 def build():
     """Compile ``oracle/interp.c`` with the committed Makefile."""
-    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    subprocess.run(["make", "-B", "-s", "-C", _HERE], check=True)
 
 
 def _load():
