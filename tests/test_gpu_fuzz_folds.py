@@ -7,7 +7,13 @@ add and mul), folded as a tree. Random
 dtypes, light element-wise expressions (tests/fuzz_graphs.py), ragged
 sizes above the fold's 2^16 threshold and non-identity inits, against the
 oracle under the per-output policy: integers and max/min bit-exact, float
-sums within the accumulation band (row sums also against float64)."""
+sums within the accumulation band (row sums also against float64). A
+whole-tensor float sum is held to the exact sum of its terms instead of the
+oracle's: the interpreter's sequential f32 sum of a million terms or more
+can itself leave the band (seed 81 of this generator, 1554799 terms: the
+oracle 2.7e-4 from the exact sum, the device's tree 1.4e-6)."""
+
+import math
 
 import numpy as np
 import pytest
@@ -39,10 +45,11 @@ def folded_case(seed):
     ops = ["add", "max", "min"] + (["mul", "xor"] if dt is I32 else [])
     op = ops[int(r.integers(len(ops)))]
     comb = {"add": D.add, "max": D.max, "min": D.min, "mul": D.mul, "xor": D.bit_xor}[op]
-    init = D.const(dt, int(r.integers(-3, 4)) if dt is I32 else float(r.choice([0.0, 1.5, -2.0])))
+    iv = int(r.integers(-3, 4)) if dt is I32 else float(r.choice([0.0, 1.5, -2.0]))
+    init = D.const(dt, iv)
     g = Graph.create("fold%d" % seed, [("m", m), ("s", D.reduce(comb, init, m))])
     inputs = [("x", FG._input(r, dt, (n,))), ("y", FG._input(r, dt, (n,)))]
-    return g, inputs, (dt.name, n, op)
+    return g, inputs, (dt.name, n, op, iv)
 
 
 def tree_case(seed):
@@ -68,15 +75,22 @@ def _run(g, inputs):
     return exp, got
 
 
-@pytest.mark.parametrize("seed", range(N_CASES))
+@pytest.mark.parametrize("seed", list(range(N_CASES)) + [81])
 def test_folded_reduction_fuzz(device, seed):
     g, inputs, what = folded_case(seed)
     print("case", seed, *what, flush=True)
     t = templates(g)
     assert "reduce_split" not in t and "reduce_split_fold" in t, (what, t)
     exp, got = _run(g, inputs)
-    bad = [v for v in Diff.policy_check(g, exp, got) if not v.ok]
+    float_sum = what[0] != "i32" and what[2] == "add"
+    bad = [v for v in Diff.policy_check(g, exp, got) if not v.ok and not (float_sum and v.name == "s")]
     assert not bad, (what, bad)
+    if float_sum:
+        e, d = dict(exp), dict(got)
+        exact = math.fsum([float(what[3])] + e["m"].astype(np.float64).tolist())
+        tol = 1e-4 if what[0] == "f32" else 1e-12
+        err = abs(float(d["s"]) - exact)
+        assert err <= tol * (1 + abs(exact)), (what, float(d["s"]), exact, float(e["s"]))
 
 
 @pytest.mark.parametrize("seed", range(N_TREE_CASES))
