@@ -543,7 +543,7 @@ class Gen {
   }
 
   Val unop(const XNode &n, const Val &a) {
-    static const char *f32n[] = {"", "sqrtf", "expf", "logf", "fabsf", "sinf", "cosf", "erff", "cc_erfinvf"};
+    static const char *f32n[] = {"", "sqrtf", "cc_expf", "cc_logf", "fabsf", "cc_sinf", "cc_cosf", "cc_erff", "cc_erfinvf"};
     static const char *f64n[] = {"", "sqrt", "exp", "log", "fabs", "sin", "cos", "erf", "cc_erfinv"};
     switch (n.dt) {
       case DT::F32:
@@ -665,6 +665,75 @@ __device__ __forceinline__ float cc_minf(float x, float y) { return __builtin_el
 __device__ __forceinline__ float cc_maxf(float x, float y) { return __builtin_elementwise_maximum(x, y); }
 __device__ __forceinline__ double cc_mind(double x, double y) { return __builtin_elementwise_minimum(x, y); }
 __device__ __forceinline__ double cc_maxd(double x, double y) { return __builtin_elementwise_maximum(x, y); }
+// f32 exp and log as the interpreter computes them: the function in double
+// precision, rounded once to float. Both are evaluated in double to within
+// a few double ulps, so the rounding to float lands where the interpreter's
+// does (checked on every float: no difference from (float)exp((double)x)
+// and (float)log((double)x) of the host C library). Each takes about 40
+// instructions in a loop (the device library's single-precision calls
+// about 20; f64 FMAs issue at the f32 rate here), which the maps over 2^28
+// elements that call them hide under their HBM time.
+// exp: 2^(h/2) e^r, h = rint(2x / ln 2), r = x - h ln2/2 (ln 2 / 2 in two
+// parts; |r| <= 0.174), e^r by its Taylor polynomial to degree 10
+// (truncation below 2^-53), times sqrt 2 for odd h. Arguments beyond
+// [-150, 130] are clamped: the float result is 0 or +inf there either way.
+__device__ __forceinline__ float cc_expf(float x) {
+  if (x != x) return x;
+  double d = (double)x;
+  d = d < -150.0 ? -150.0 : (d > 130.0 ? 130.0 : d);
+  const double h = __builtin_rint(d * 2.8853900817779268);
+  double r = __builtin_fma(-h, 3.46573590184561908245e-01, d);
+  r = __builtin_fma(-h, 9.54107464635293850010e-11, r);
+  double p = 1.0 / 3628800.0;
+  p = __builtin_fma(p, r, 1.0 / 362880.0);
+  p = __builtin_fma(p, r, 1.0 / 40320.0);
+  p = __builtin_fma(p, r, 1.0 / 5040.0);
+  p = __builtin_fma(p, r, 1.0 / 720.0);
+  p = __builtin_fma(p, r, 1.0 / 120.0);
+  p = __builtin_fma(p, r, 1.0 / 24.0);
+  p = __builtin_fma(p, r, 1.0 / 6.0);
+  p = __builtin_fma(p, r, 0.5);
+  p = __builtin_fma(p, r, 1.0);
+  p = __builtin_fma(p, r, 1.0);
+  const int hi = (int)h;
+  if (hi & 1) p *= 1.4142135623730951;
+  return (float)__builtin_ldexp(p, hi >> 1);
+}
+// log: x = 2^e m with m in [sqrt(1/2), sqrt(2)) (exact in double, float
+// subnormals included), log m = 2 atanh t = 2t + 2t^3 q(t^2) with
+// t = (m - 1) / (m + 1), |t| <= 0.172, q to the t^16 term (truncation
+// below 2^-50), then e ln 2 + log m.
+__device__ __forceinline__ float cc_logf(float x) {
+  if (!(x > 0.0f) || x == __builtin_inff()) {
+    if (x == 0.0f) return -__builtin_inff();
+    return x == __builtin_inff() ? x : __builtin_nanf("");  // +inf; negative or NaN
+  }
+  const double d = (double)x;
+  const cc_u64 b = __builtin_bit_cast(cc_u64, d);
+  int e = (int)((b >> 52) & 0x7ff) - 1023;
+  double m = __builtin_bit_cast(double, (b & 0x000fffffffffffffull) | 0x3ff0000000000000ull);
+  if (m > 1.4142135623730951) {
+    m *= 0.5;
+    e += 1;
+  }
+  const double t = (m - 1.0) / (m + 1.0);
+  const double t2 = t * t;
+  double q = 1.0 / 17.0;
+  q = __builtin_fma(q, t2, 1.0 / 15.0);
+  q = __builtin_fma(q, t2, 1.0 / 13.0);
+  q = __builtin_fma(q, t2, 1.0 / 11.0);
+  q = __builtin_fma(q, t2, 1.0 / 9.0);
+  q = __builtin_fma(q, t2, 1.0 / 7.0);
+  q = __builtin_fma(q, t2, 1.0 / 5.0);
+  q = __builtin_fma(q, t2, 1.0 / 3.0);
+  const double lm = __builtin_fma(2.0 * t * t2, q, 2.0 * t);
+  return (float)__builtin_fma((double)e, 0.6931471805599453, lm);
+}
+// sin, cos and erf in f32 the same way, through the device library's
+// double-precision functions (no benchmark's inner loop calls them).
+__device__ __forceinline__ float cc_sinf(float x) { return (float)sin((double)x); }
+__device__ __forceinline__ float cc_cosf(float x) { return (float)cos((double)x); }
+__device__ __forceinline__ float cc_erff(float x) { return (float)erf((double)x); }
 // erfinv in single precision, with the structure of M. Giles,
 // "Approximating the erfinv function" (GPU Computing Gems, 2011):
 // w = -ln(1 - x^2); erfinv(x) = x p(w - 1) for w < 5, else
