@@ -1768,10 +1768,13 @@ struct Lowering {
       return b.str();
     };
     // A scan's store of tile `ktx` from the LDS buffer `buf`, thread `tid`
-    // taking the same groups it moved into LDS.
-    auto store_tile = [&](const std::string &ktx, const std::string &tid, const std::string &buf) {
+    // taking the same groups it moved into LDS. `own` where the thread then
+    // refills those LDS words with no barrier between (the split roles'
+    // loaders): it must read only the words it writes next, so the 8-byte
+    // pairs, which another thread's groups hold, are not used there.
+    auto store_tile = [&](const std::string &ktx, const std::string &tid, const std::string &buf, bool own = false) {
       std::ostringstream b;
-      if (vec && dt_size(n.dt) == 8 && pairs8) {
+      if (vec && dt_size(n.dt) == 8 && pairs8 && !own) {
         // 8-byte values in pairs: one 16-byte access a lane, consecutive
         // lanes at consecutive addresses, so each store instruction writes
         // whole lines (a 4-element group of 8-byte values is two 16-byte
@@ -1845,7 +1848,7 @@ struct Lowering {
         const std::string mine = d ? "smb" : "sma", other4 = d ? "sm4a" : "sm4b", rg = "rg" + std::to_string(d);
         std::ostringstream b;
         b << fold_tile(mine) << "      if (threadIdx.x >= 64) {\n";
-        if (scan) b << "      if (kt >= 1) {\n" << store_tile("kt - 1", "lt", other4) << "      }\n";
+        if (scan) b << "      if (kt >= 1) {\n" << store_tile("kt - 1", "lt", other4, true) << "      }\n";
         b << "      if (kt + 1 < " << NT << ") {\n" << to_lds(rg, "lt", other4) << "      }\n"
           << "      if (kt + 3 < " << NT << ") {\n"
           << load("(kt + 3) * " + std::to_string(W), rg, "lt") << "      }\n"

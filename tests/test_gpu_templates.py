@@ -275,6 +275,40 @@ def test_sibling_group_runs_before_a_consumer_of_its_first_root(device):
     check(g, [("x", data(F32, (rows, n), 62))], ["scan_tile_fold"])
 
 
+SPLIT8_CASES = [
+    # (rows, len, dtype, combine, knobs): row-sequential scans of 8-byte
+    # values with split roles (four tiles a row or more), by default
+    # (rows shorter than the tile scans' 2048) and with the in-order and
+    # plain-store knobs; the case a random-knob search found wrong before
+    # the loaders' stores kept to their own groups
+    (4096, 1000, F64, "add", ""),
+    (4096, 1000, I64, "add", ""),
+    (1100, 4000, F64, "min", "rs_tree=0,rs_nt=0"),
+    (2048, 3000, F64, "add", "rs_tree=0"),
+    (1030, 5000, I64, "max", "rs_tree=0,rs_nt=0"),
+]
+
+
+@pytest.mark.parametrize("rows,n,dtype,op,knobs", SPLIT8_CASES, ids=lambda v: str(v))
+def test_split_row_scan_of_8_byte_values(device, monkeypatch, rows, n, dtype, op, knobs):
+    """In the interpreter's order, so bit for bit against the oracle."""
+    if knobs:
+        monkeypatch.setenv("CCHIP_TUNE", knobs)
+    comb = {"add": D.add, "min": D.min, "max": D.max}[op]
+    init = D.const(dtype, 0.5 if dtype is F64 else 3)
+    g = Graph.create("split8", [("p", D.scan_rows(comb, init, D.param("x", dtype, (rows, n))))])
+    lines = [l.split() for l in H.plan(g).splitlines() if l.startswith("kernel")]
+    assert [(f[2], f[7]) for f in lines] == [("scan_rowseq", "320")], lines
+    x = data(dtype, (rows, n), 131)
+    exp = dict(oracle.run(g, [("x", x)]))["p"]
+    c = H.compile(g)
+    try:
+        got = dict(H.run(c, [("x", x)]))["p"]
+    finally:
+        c.release()
+    np.testing.assert_array_equal(got.view(np.uint8), exp.view(np.uint8))
+
+
 ROWLAST_CASES = [
     # (rows, len, dtype, knobs): Monte Carlo's shape, ragged rows, long rows
     # folded in order with split roles, 8-byte values, two tiles in flight
