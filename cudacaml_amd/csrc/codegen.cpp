@@ -1167,6 +1167,12 @@ struct Lowering {
   std::map<int, std::vector<int>> sib_reds;  // scan root -> its reductions
   std::map<int, int> sib_lead;               // first root of a group -> scan root
   std::set<int> sib_member;                  // every root of a group but the lead
+  // A reduction that folds the same rows with the same combine and init as
+  // a scan is the scan's last element of every row: the scan stores those
+  // into the reduction's buffer (its row-last side buffer) and the
+  // reduction launches nothing. It is part of the scan's group.
+  std::map<int, int> same_fold_of;  // scan root -> reduce root
+  std::set<int> same_fold_red;
 
   explicit Lowering(const Graph &gr) : g(gr), plan(fusion_plan(gr)), gen(gr, plan, buf_of) {
     gen.bufdt_ = [this](int b) { return prog.bufs[b].dt; };
@@ -1389,7 +1395,10 @@ struct Lowering {
     const TNode &sn = g.ts[scan];
     int64_t algo = root_bytes(scan), moved = fn_bytes(gen.element_fn("ab_", sn.a, false, true), g.ts[sn.a].numel) +
                                               sn.numel * dt_size(sn.dt);
-    for (int r : reds) {
+    std::vector<int> all = reds;
+    const auto sf = same_fold_of.find(scan);
+    if (sf != same_fold_of.end()) all.push_back(sf->second);
+    for (int r : all) {
       algo += root_bytes(r);
       moved += g.ts[r].numel * dt_size(g.ts[r].dt);
     }
@@ -2266,31 +2275,63 @@ struct Lowering {
   // add and mul differ by rounding only. The group's kernel runs at its
   // first root's place in the plan: every member reads only what the
   // shared tensor reads, which is ready by then.
+  //
+  // A reduction with the scan's own combine and init (the same code) over
+  // the same tensor is the scan's last element of each row, in the
+  // interpreter as in every scan template: it takes those values
+  // (same_fold=0 keeps it its own kernels). The reverse-mode adjoint of a
+  // row scan, total - prefix + adjoint, is such a pair: computed from one
+  // fold, its total and prefixes round together, as the interpreter's do.
   void find_sibling_groups() {
-    if (!tune("sibling_fuse", 1)) return;
     std::map<int, size_t> pos;
     for (size_t i = 0; i < plan.roots.size(); i++) pos[plan.roots[i]] = i;
     std::set<int> folded_in_map;
     for (auto &fr : fused_red_of_map) folded_in_map.insert(fr.second);
+    if (tune("same_fold", 1))
+      for (int s : plan.roots) {
+        const TNode &sn = g.ts[s];
+        if (sn.kind != TK::Scan || sn.numel == 0) continue;
+        const int64_t rows = sn.numel / row_length(sn.shape);
+        const std::string sc = gen.combine_fn("c_", sn.body, sn.dt), si = gen.const_fn("z_", sn.init, sn.dt);
+        for (int r : plan.roots) {
+          const TNode &rn = g.ts[r];
+          if (rn.kind != TK::Reduce || rn.a != sn.a || rn.dt != sn.dt || rn.numel != rows) continue;
+          if (same_fold_red.count(r) || folded_in_map.count(r)) continue;
+          if (gen.combine_fn("c_", rn.body, rn.dt) != sc || gen.const_fn("z_", rn.init, rn.dt) != si) continue;
+          same_fold_of[s] = r;
+          same_fold_red.insert(r);
+          break;
+        }
+      }
     for (int s : plan.roots) {
       const TNode &sn = g.ts[s];
-      if (sn.kind != TK::Scan || !scan_is_row_tile(s)) continue;
-      const int64_t len = row_length(sn.shape), rows = sn.numel / len;
+      if (sn.kind != TK::Scan) continue;
       std::vector<int> reds;
-      for (int r : plan.roots) {
-        const TNode &rn = g.ts[r];
-        if (rn.kind != TK::Reduce || rn.a != sn.a || sib_member.count(r) || folded_in_map.count(r)) continue;
-        if (row_length(g.ts[rn.a].shape) != len || rn.numel != rows || !reduce_is_tree(r)) continue;
-        reds.push_back(r);
+      if (tune("sibling_fuse", 1) && scan_is_row_tile(s)) {
+        const int64_t len = row_length(sn.shape), rows = sn.numel / len;
+        for (int r : plan.roots) {
+          const TNode &rn = g.ts[r];
+          if (rn.kind != TK::Reduce || rn.a != sn.a || sib_member.count(r) || sib_lead.count(r) ||
+              folded_in_map.count(r) || same_fold_red.count(r))
+            continue;
+          if (row_length(g.ts[rn.a].shape) != len || rn.numel != rows || !reduce_is_tree(r)) continue;
+          reds.push_back(r);
+        }
       }
-      if (reds.empty()) continue;
+      std::vector<int> members = reds;
+      const auto sf = same_fold_of.find(s);
+      if (sf != same_fold_of.end()) {
+        members.push_back(sf->second);
+        gen.rowlast_[s] = {buf_of[sf->second], row_length(sn.shape)};
+      }
+      if (members.empty()) continue;
       int lead = s;
-      for (int r : reds)
+      for (int r : members)
         if (pos[r] < pos[lead]) lead = r;
       sib_reds[s] = reds;
       sib_lead[lead] = s;
       if (lead != s) sib_member.insert(s);
-      for (int r : reds)
+      for (int r : members)
         if (r != lead) sib_member.insert(r);
     }
   }
@@ -2367,6 +2408,10 @@ struct Lowering {
     if (rows == 0) return {};
     ElemFn f = gen.element_fn("f_" + id, n.a, false, true);
     src << f.code;
+    // a side buffer of each row's last element (Gen::rowlast_): the tile
+    // and wave templates store it here, the row-sequential one on its own
+    const auto sd = gen.rowlast_.find(t);
+    const int side = sd != gen.rowlast_.end() ? sd->second.first : -1;
     // 1024 rows or more scan one lane a row, in order, unless the rows are
     // long (rs_tree_len) and the combine allows any grouping (bit-exact for
     // max, min and integer ops; float add and mul within rounding): those
@@ -2386,6 +2431,7 @@ struct Lowering {
       Params p;
       add_in(p, f);
       p.out.push_back(out);
+      if (side >= 0) p.out.push_back(side);
       std::vector<int> args;
       std::string params = param_list(p, args);
       std::ostringstream k;
@@ -2405,8 +2451,9 @@ struct Lowering {
       for (int64_t off = 1; off < S; off *= 2)
         k << "    { const " << T << " u = __shfl_up(v, " << off << "); if (sl >= " << off << ") v = " << cmb
           << "(u, v); }\n";
-      k << "    if (valid) b" << out << "[i] = v;\n"
-        << "  }\n}\n";
+      k << "    if (valid) b" << out << "[i] = v;\n";
+      if (side >= 0) k << "    if (valid && sl == " << len - 1 << ") b" << side << "[r] = v;\n";
+      k << "  }\n}\n";
       src << k.str();
       int64_t waves = cdiv(rows, rpw);
       int grid = (int)std::min<int64_t>(cdiv(waves, 4), 65536);
@@ -2478,6 +2525,7 @@ struct Lowering {
     add_in(p, f);
     p.out.push_back(out);
     for (int o : rout) p.out.push_back(o);
+    if (side >= 0) p.out.push_back(side);
     if (chained) p.err = true;
     std::vector<int> args;
     std::string params = param_list(p, args);
@@ -2812,6 +2860,11 @@ struct Lowering {
       for (int c = 0; c < 4; c++)
         k << "    if (e + " << c << " < tl) b" << out << "[base + e + " << c << "] = v[u][" << c << "];\n";
     }
+    // the row's last element, held by one thread of the row's last tile
+    if (side >= 0)
+      k << "    if (tin == " << tpr - 1 << ")\n"
+        << "#pragma unroll\n"
+        << "      for (int c = 0; c < 4; c++) if (e + c == tl - 1) b" << side << "[row] = v[u][c];\n";
     k << "  }\n"
       << "}\n";
     src << k.str();

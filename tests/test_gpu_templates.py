@@ -309,6 +309,57 @@ def test_split_row_scan_of_8_byte_values(device, monkeypatch, rows, n, dtype, op
     np.testing.assert_array_equal(got.view(np.uint8), exp.view(np.uint8))
 
 
+SAME_FOLD_CASES = [
+    # (shape, dtype, op, init, knobs, template): every scan template
+    ((100, 37), I32, "add", 3, "", "scan_wave"),
+    ((100, 50), F32, "add", 0.0, "", "scan_wave"),
+    ((300, 1000), F32, "add", 0.0, "", "scan_tile"),
+    ((200, 4097), F64, "add", 0.5, "", "scan_tile"),
+    ((300, 1001), I64, "max", 3, "", "scan_tile_fold"),  # with a tree sibling
+    ((5, 300001), I32, "add", 0, "", "scan_lookback"),
+    ((8, 100003), F64, "add", 0.5, "", "scan_lookback"),
+    ((1 << 18,), F32, "add", 0.0, "", "scan_lookback"),
+    ((2048, 300), F32, "add", 0.0, "", "scan_rowseq"),
+    ((1024, 40000), F32, "add", 0.0, "rs_tree=0", "scan_rowseq"),  # split roles
+    ((1030, 5000), I64, "max", 3, "rs_tree=0,rs_nt=0", "scan_rowseq"),
+    ((1100, 70), F64, "add", 0.5, "rs_depth=2", "scan_rowseq"),
+]
+
+
+@pytest.mark.parametrize("shape,dtype,op,iv,knobs,template", SAME_FOLD_CASES, ids=lambda v: str(v))
+def test_same_fold_reduction_is_the_scans_row_end(device, monkeypatch, shape, dtype, op, iv, knobs, template):
+    """A reduction with the scan's combine and init over the same tensor
+    takes the scan's last element of every row, bit for bit; both against
+    the oracle to the policy bar, and bit for bit where the scan folds in
+    the interpreter's order or the combine is exact in any order."""
+    if knobs:
+        monkeypatch.setenv("CCHIP_TUNE", knobs)
+    comb = {"add": D.add, "max": D.max}[op]
+    init = D.const(dtype, iv)
+    x = D.param("x", dtype, shape)
+    one_d = len(shape) == 1
+    outs = [("s", D.scan(comb, init, x) if one_d else D.scan_rows(comb, init, x)),
+            ("r", D.reduce(comb, init, x) if one_d else D.reduce_rows(comb, init, x))]
+    if template == "scan_tile_fold":
+        outs.append(("m", D.reduce_rows(D.min, D.const(dtype, 0), x)))
+    g = Graph.create("same_fold", outs)
+    assert [t for t in templates(g) if t != "scan_init"] == [template]
+    xv = data(dtype, shape, 97)
+    exp = dict(oracle.run(g, [("x", xv)]))
+    c = H.compile(g)
+    try:
+        got = dict(H.run(c, [("x", xv)]))
+    finally:
+        c.release()
+    last = np.ascontiguousarray(got["s"][..., -1])
+    np.testing.assert_array_equal(np.ascontiguousarray(got["r"]).reshape(last.shape).view(np.uint8),
+                                  last.view(np.uint8))
+    bad = [v for v in Diff.policy_check(g, list(exp.items()), list(got.items())) if not v.ok]
+    assert not bad, bad
+    if template == "scan_rowseq" or not dtype.is_float or op != "add":
+        np.testing.assert_array_equal(got["r"].view(np.uint8), exp["r"].view(np.uint8))
+
+
 ROWLAST_CASES = [
     # (rows, len, dtype, knobs): Monte Carlo's shape, ragged rows, long rows
     # folded in order with split roles, 8-byte values, two tiles in flight
@@ -911,12 +962,12 @@ KNOB_CASES = [
      lambda: [("x", data(I64, (1, 200000), 58))], "scan_lookback"),
     ("rs_tree=0,rs_nt=0", lambda: C.rows(1024, 3000), lambda: [("x", data(F32, (1024, 3000), 59))], "scan_rowseq"),
     ("rs_nt=2", lambda: C.rows(2048, 1000), lambda: [("x", data(F32, (2048, 1000), 60))], "reduce_rowseq"),
-    ("rr_tree=1,rr_bytes=16384,rr_groups=64", lambda: C.rows(1500, 2001),
+    ("rr_tree=1,rr_bytes=16384,rr_groups=64,same_fold=0", lambda: C.rows(1500, 2001),
      lambda: [("x", data(F32, (1500, 2001), 61))], "reduce_rowseq"),
     # two tiles in flight: an odd tile count with a ragged last tile
     ("rs_tree=0,rs_depth=2,rs_bytes=4096,rr_depth=2,rr_bytes=16384", lambda: C.rows(1024, 3000),
      lambda: [("x", data(F32, (1024, 3000), 62))], "scan_rowseq"),
-    ("rs_tree=0,rr_tree=1,rr_depth=2,rr_bytes=16384", lambda: C.rows(2048, 5003),
+    ("rs_tree=0,rr_tree=1,rr_depth=2,rr_bytes=16384,same_fold=0", lambda: C.rows(2048, 5003),
      lambda: [("x", data(F32, (2048, 5003), 63))], "reduce_rowseq"),
     ("rs_tree=0,rs_chunk=4,rr_chunk=128", lambda: C.rows(1024, 3000), lambda: [("x", data(F32, (1024, 3000), 64))], "scan_rowseq"),
     # long rows folded in order: floats bit-identical to the interpreter,

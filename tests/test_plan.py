@@ -278,17 +278,79 @@ def test_sibling_row_roots_share_one_kernel(monkeypatch):
                            ("b", D.reduce_rows(D.max, D.const(F32, 0.0), x)),
                            ("c", D.reduce(D.add, D.const(F32, 0.0), x))])
     assert [t for _, t in kernels_of(g)] == ["reduce_block", "scan_tile_fold", "reduce_split", "reduce_split_fold"]
-    monkeypatch.setenv("CCHIP_TUNE", "sibling_fuse=0")
+    monkeypatch.setenv("CCHIP_TUNE", "sibling_fuse=0,same_fold=0")
     assert [t for _, t in kernels_of(C.rows())] == ["reduce_block", "reduce_block", "scan_tile"]
     # in order (the interpreter's exact folds): nothing to share
-    monkeypatch.setenv("CCHIP_TUNE", "rr_tree=1,rs_tree=0")
+    monkeypatch.setenv("CCHIP_TUNE", "rr_tree=1,rs_tree=0,same_fold=0")
     assert [t for _, t in kernels_of(C.rows())] == ["reduce_rowseq", "reduce_block", "scan_rowseq"]
     # a look-back scan (several tiles a row) keeps the reductions apart
     monkeypatch.delenv("CCHIP_TUNE")
     z = D.param("z", I32, (4, 100000))
     g = Graph.create("lb", [("p", D.scan_rows(D.add, D.const(I32, 0), z)),
-                            ("s", D.reduce_rows(D.add, D.const(I32, 0), z))])
+                            ("s", D.reduce_rows(D.max, D.const(I32, 0), z))])
     assert "scan_tile_fold" not in [t for _, t in kernels_of(g)]
+
+
+def _kernel_args(g):
+    """(template, [buffer names]) of every kernel, in launch order."""
+    lines = [l.split() for l in H.plan(g).splitlines()]
+    names = {f[1]: f[2] for f in lines if f[0] == "buffer"}
+    return [(f[2], [names[a] for a in f[f.index("args") + 1:]]) for f in lines if f[0] == "kernel"]
+
+
+SAME_FOLD_SHAPES = [
+    ((100, 50), F32, "scan_wave", ""),
+    ((600, 3000), F32, "scan_tile", ""),
+    ((4, 100000), I32, "scan_lookback", ""),
+    ((2048, 300), F32, "scan_rowseq", ""),
+    ((1024, 40000), F32, "scan_rowseq", "rs_tree=0"),  # split roles
+    ((1 << 20,), F64, "scan_lookback", ""),
+]
+
+
+@pytest.mark.parametrize("shape,dt,template,knobs", SAME_FOLD_SHAPES)
+def test_same_fold_reduction_reads_the_scans_row_ends(monkeypatch, shape, dt, template, knobs):
+    """A reduction with the scan's own combine and init over the same
+    tensor launches nothing: whichever template the scan takes stores each
+    row's last element into the reduction's buffer. Another init, another
+    combine or same_fold=0 keeps the reduction's own kernels."""
+    monkeypatch.setenv("CCHIP_TUNE", knobs)
+    x = D.param("x", dt, shape)
+    z = D.const(dt, 0 if dt is I32 else 0.0)
+
+    def graph(init, comb=D.add):
+        return Graph.create("sf", [("s", D.scan(D.add, z, x) if len(shape) == 1 else D.scan_rows(D.add, z, x)),
+                                   ("r", D.reduce(comb, init, x) if len(shape) == 1 else D.reduce_rows(comb, init, x))])
+
+    g = graph(z)
+    main = [k for k in _kernel_args(g) if k[0] != "scan_init"]
+    assert [t for t, _ in main] == [template]
+    bufs = {n: l.split()[2] for l in H.plan(g).splitlines() for n in ["s", "r"]
+            if l.startswith("download " + n + " ")}
+    assert bufs["r"] in main[0][1] and bufs["s"] in main[0][1]
+    # otherwise its own kernels, or a tree sibling of a one-tile-a-row scan
+    def templates(g):
+        return [t for t, _ in _kernel_args(g) if t != "scan_init"]
+    one = D.const(dt, 1 if dt is I32 else 1.0)
+    assert templates(graph(one)) != [template]
+    assert templates(graph(z, D.max)) != [template]
+    monkeypatch.setenv("CCHIP_TUNE", ",".join(k for k in [knobs, "same_fold=0"] if k))
+    assert templates(graph(z)) != [template]
+
+
+def test_same_fold_runs_at_the_reductions_place():
+    """A same-fold pair whose reduction comes first in the plan, with a root
+    reading the reduction in between: the scan's kernel runs at the
+    reduction's place, so the reader runs after it. Monte Carlo greeks lose
+    their row reduction of the adjoint (total - prefix + adjoint)."""
+    x = D.param("x", F32, (2048, 300))
+    z = D.const(F32, 0.0)
+    r = D.reduce_rows(D.add, z, x)
+    m = D.map(lambda v: D.mul(v, D.const(F32, 2.0)), r)
+    s = D.scan_rows(D.add, z, x)
+    g = Graph.create("sf", [("m", m), ("s", s)])
+    assert [t for t, _ in _kernel_args(g)] == ["scan_rowseq", "map"]
+    assert "reduce_rowseq" not in [t for _, t in kernels_of(C.mc_greeks())]
 
 
 def _launch_uses_live_buffers(g):
