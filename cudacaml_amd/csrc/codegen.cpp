@@ -1160,6 +1160,9 @@ struct Lowering {
   };
   std::map<int, int> fused_red_of_map;
   std::map<int, FusedPartials> fused_part_of_red;
+  // bytes a map kernel reads for its folded reduction's expression beyond
+  // its own loads
+  std::map<int, int64_t> map_extra_moved;
   // Row roots over one tensor fused into one kernel: a row scan that takes
   // the one-workgroup-a-row tile template, and the reductions of the same
   // tensor's rows that fold as a tree. The group's first root in the plan
@@ -1425,6 +1428,8 @@ struct Lowering {
     // (scratch): it moves its output alone; a scan with a side buffer of
     // row-last elements also writes that
     prog.kernels[main].moved_bytes = n.kind == TK::Reduce && fused_part_of_red.count(r) ? out : bytes;
+    const auto em = map_extra_moved.find(r);
+    if (em != map_extra_moved.end()) prog.kernels[main].moved_bytes += em->second;
     const auto rl = gen.rowlast_.find(r);
     if (rl != gen.rowlast_.end())
       prog.kernels[main].moved_bytes += prog.bufs[rl->second.first].bytes();
@@ -1463,6 +1468,23 @@ struct Lowering {
     int out = buf_of[t];
     ElemFn f = gen.element_fn("f_" + std::to_string(n.id), t, true, true);
     src << f.code;
+    // A whole-tensor reduction folded here (below). When its input is an
+    // element-wise expression of this output and of other tensors at the
+    // same index rather than the output itself: that expression's element
+    // function (fe), and fx, the same function with only the tensors it
+    // loads beyond this map's own loads and output.
+    const auto fr = fused_red_of_map.find(t);
+    const bool fuse = fr != fused_red_of_map.end();
+    const bool fexpr = fuse && g.ts[fr->second].a != t;
+    ElemFn fe, fx;
+    if (fexpr) {
+      fe = gen.element_fn("fe_" + std::to_string(g.ts[fr->second].id), g.ts[fr->second].a, false, true);
+      src << fe.code;
+      fx = fe;
+      fx.ident.clear();
+      for (int b : fe.ident)
+        if (b != out && std::find(f.ident.begin(), f.ident.end(), b) == f.ident.end()) fx.ident.push_back(b);
+    }
     // a side buffer of each row's last element (Gen::rowlast_), if a later
     // gather reads only those
     const auto sd = gen.rowlast_.find(t);
@@ -1470,6 +1492,7 @@ struct Lowering {
     const int64_t SL_ = side >= 0 ? sd->second.second : 0;
     Params p;
     add_in(p, f);
+    if (fexpr) add_in(p, fx);
     p.out.push_back(out);
     if (side >= 0) p.out.push_back(side);
     std::vector<int> args;
@@ -1485,9 +1508,12 @@ struct Lowering {
     // Non-temporal streaming accesses when the kernel also gathers or moves
     // more than the MALL holds (mode 1), always (2) or never (0).
     int64_t nt_mode = tune("map_nt", 1);
-    bool nt = nt_mode == 2 || (nt_mode == 1 && (!f.ptrs.empty() || streams(fn_bytes(f, N) + N * dt_size(n.dt))));
+    bool nt = nt_mode == 2 || (nt_mode == 1 && (!f.ptrs.empty() || !fx.ptrs.empty() ||
+                                                 streams(fn_bytes(f, N) + (fexpr ? fn_bytes(fx, N) : 0) +
+                                                         N * dt_size(n.dt))));
     if (n.dt == DT::BOOL) nt = false;
     for (int b : f.ident) nt = nt && prog.bufs[b].dt != DT::BOOL;
+    for (int b : fx.ident) nt = nt && prog.bufs[b].dt != DT::BOOL;
     // Loads and stores separately: -1 follows map_nt, 0 plain, 1 streaming.
     // A map that reads no stream (a fill from scalars) stores plainly: that
     // measured faster for write-only kernels (1 GiB: 168 us against 190).
@@ -1496,11 +1522,14 @@ struct Lowering {
     bool nts = nts_k < 0 ? nt && (nt_mode == 2 || !f.ident.empty()) : nts_k != 0;
     if (n.dt == DT::BOOL) nts = false;
     for (int b : f.ident) ntl = ntl && prog.bufs[b].dt != DT::BOOL;
+    for (int b : fx.ident) ntl = ntl && prog.bufs[b].dt != DT::BOOL;
     // Elements per thread and access: 16 bytes of the widest type, so each
     // wave instruction covers one contiguous run (4 for 4-byte types, 2 when
     // any operand is 8 bytes wide).
     int G = dt_size(n.dt) == 8 ? 2 : 4;
     for (int b : f.ident)
+      if (dt_size(prog.bufs[b].dt) == 8) G = 2;
+    for (int b : fx.ident)
       if (dt_size(prog.bufs[b].dt) == 8) G = 2;
     const std::string VG = "cc_v" + std::to_string(G);
     // Groups per lane per iteration. An element function with a long
@@ -1523,14 +1552,13 @@ struct Lowering {
     // waves may hold none), and the reduction's root folds the partials.
     // Its input is then never read back (config 1: s = sum(r) over 2^24).
     // No workgroup barrier: waves leave as they finish.
-    const auto fr = fused_red_of_map.find(t);
-    const bool fuse = fr != fused_red_of_map.end();
-    std::string rc, ri;
+    std::string rc, ri, TR = T;
     int part = -1, pflag = -1;
     if (fuse) {
       const TNode &rn = g.ts[fr->second];
       rc = "c_" + std::to_string(rn.id);
       ri = "z_" + std::to_string(rn.id);
+      TR = dt_ctype(rn.dt);
       src << gen.combine_fn(rc, rn.body, rn.dt) << gen.const_fn(ri, rn.init, rn.dt);
       const int64_t np = 4 * std::min<int64_t>(cdiv(std::max<int64_t>(1, N / G), 256 * UN), tune("map_blocks", 1 << 22));
       part = add_buf("t" + std::to_string(rn.id) + "_partials", rn.dt, np, BufRole::Scratch);
@@ -1544,6 +1572,13 @@ struct Lowering {
       params = param_list(p, args);
     }
     static const char *comp[] = {"x", "y", "z", "w"};
+    // the value folded for element u of the group at i held in rv: the
+    // output's own, or the reduction's expression over it and the loads
+    auto fold_val = [&](const std::string &i, const std::string &rv, int u) {
+      if (!fexpr) return rv + "." + comp[u];
+      const std::string idx = u == 0 ? i : "(" + i + " + " + std::to_string(u) + ")";
+      return fe.call(idx, [&](int b) { return (b == out ? rv : "l" + std::to_string(b)) + "." + comp[u]; });
+    };
     // Each workgroup takes a contiguous run of 256 * UN groups, lane l its
     // groups l, l + 256, ..., and the grid covers the whole tensor, so each
     // lane makes one pass. Resident waves then touch one contiguous window
@@ -1555,11 +1590,12 @@ struct Lowering {
     k << "extern \"C\" __global__ __launch_bounds__(256) void " << kname << "(" << params << ") {\n"
       << "  const int stride = gridDim.x * " << 256 * UN << ";\n"
       << "  const int nvec = " << N / G << ";\n";
-    if (fuse) k << "  " << T << " acc = " << ri << "();\n  bool has = false;\n";
+    if (fuse) k << "  " << TR << " acc = " << ri << "();\n  bool has = false;\n";
     if (UN == 1) {
       k << "  for (int v = blockIdx.x * 256 + threadIdx.x; v < nvec; v += stride) {\n"
         << "    const int i = v * " << G << ";\n"
-        << vec_loads(f, "i", "    ", tyof(), ntl, G) << "    " << VG << "<" << T << "> r;\n";
+        << vec_loads(f, "i", "    ", tyof(), ntl, G) << (fexpr ? vec_loads(fx, "i", "    ", tyof(), ntl, G) : "")
+        << "    " << VG << "<" << T << "> r;\n";
       for (int u = 0; u < G; u++) k << "    r." << comp[u] << " = " << lane_call(f, "i", u) << ";\n";
       if (nts)
         k << "    cc_st" << G << "_nt(b" << out << " + i, r);\n";
@@ -1569,15 +1605,23 @@ struct Lowering {
         for (int u = 0; u < G; u++)
           k << "    " << side_st("i + " + std::to_string(u), std::string("r.") + comp[u]) << "\n";
       if (fuse)
-        for (int u = 0; u < G; u++) k << "    " << fold_in(rc, T, std::string("r.") + comp[u]) << "\n";
+        for (int u = 0; u < G; u++) k << "    " << fold_in(rc, TR, fold_val("i", "r", u)) << "\n";
     } else {
       k << "  for (int v0 = blockIdx.x * " << 256 * UN << " + threadIdx.x; v0 < nvec; v0 += stride) {\n"
         << "    " << VG << "<" << T << "> r[" << UN << "];\n";
       for (int64_t q = 0; q < UN; q++) {
         k << "    {\n"
           << "      const int i = min(v0 + " << q * 256 << ", nvec - 1) * " << G << ";\n"
-          << vec_loads(f, "i", "      ", tyof(), ntl, G);
+          << vec_loads(f, "i", "      ", tyof(), ntl, G) << (fexpr ? vec_loads(fx, "i", "      ", tyof(), ntl, G) : "");
         for (int u = 0; u < G; u++) k << "      r[" << q << "]." << comp[u] << " = " << lane_call(f, "i", u) << ";\n";
+        // an expression's loads live in this block: folded here, in the
+        // same order (a clamped group is its owner's: folded once)
+        if (fexpr)
+          for (int u = 0; u < G; u++)
+            k << "      "
+              << fold_in_if(rc, TR, fold_val("i", "r[" + std::to_string(q) + "]", u),
+                            "v0 + " + std::to_string(q * 256) + " < nvec")
+              << "\n";
         k << "    }\n";
       }
       for (int64_t q = 0; q < UN; q++) {
@@ -1593,22 +1637,27 @@ struct Lowering {
             k << "    " << side_st(iq + " + " + std::to_string(u), "r[" + std::to_string(q) + "]." + comp[u]) << "\n";
       }
       // a clamped group is its owner's: folded once, by the owner
-      if (fuse)
+      if (fuse && !fexpr)
         for (int64_t q = 0; q < UN; q++)
           for (int u = 0; u < G; u++)
-            k << "    " << fold_in_if(rc, T, "r[" + std::to_string(q) + "]." + comp[u], "v0 + " + std::to_string(q * 256) + " < nvec")
+            k << "    " << fold_in_if(rc, TR, "r[" + std::to_string(q) + "]." + comp[u], "v0 + " + std::to_string(q * 256) + " < nvec")
               << "\n";
     }
     k << "  }\n"
       << "  for (int i = nvec * " << G << " + blockIdx.x * 256 + threadIdx.x; i < " << N << "; i += gridDim.x * 256)";
     if (fuse || side >= 0)
       k << " {\n    const " << T << " v_ = " << f.call_scalar("i") << ";\n    b" << out << "[i] = v_;\n    "
-        << (fuse ? fold_in(rc, T, "v_") : std::string()) << (side >= 0 ? side_st("i", "v_") : std::string())
+        << (fuse ? fold_in(rc, TR,
+                           fexpr ? fe.call("i", [&](int b) { return b == out ? std::string("v_")
+                                                                             : "b" + std::to_string(b) + "[i]"; })
+                                 : std::string("v_"))
+                 : std::string())
+        << (side >= 0 ? side_st("i", "v_") : std::string())
         << "\n  }\n";
     else
       k << "\n    b" << out << "[i] = " << f.call_scalar("i") << ";\n";
     if (fuse)
-      k << "  for (int off = 32; off > 0; off >>= 1) " << xor_combine(rc, T, "off") << "\n"
+      k << "  for (int off = 32; off > 0; off >>= 1) " << xor_combine(rc, TR, "off") << "\n"
         << "  if ((threadIdx.x & 63) == 0) {\n"
         << "    const int w = blockIdx.x * 4 + (threadIdx.x >> 6);\n"
         << "    b" << part << "[w] = acc;\n"
@@ -1618,6 +1667,7 @@ struct Lowering {
     src << k.str();
     int64_t nvec = std::max<int64_t>(1, N / G);
     int grid = (int)std::min<int64_t>(cdiv(nvec, 256 * UN), tune("map_blocks", 1 << 22));
+    if (fexpr) map_extra_moved[t] = fn_bytes(fx, N);
     return {add_kernel(kname, args, grid, 256, "map")};
   }
 
@@ -4975,18 +5025,65 @@ struct Lowering {
     // 2^28 0.52 / 0.67 ms; the degree-64 Horner map (VALU-bound, 48 lines or
     // more, as for map_unroll) 0.129 / 0.124 ms, since its waves then end
     // on the fold's dependent tail.
-    if (tune("fuse_reduce", 1))
-      for (size_t ri = 1; ri < plan.roots.size(); ri++) {
-        const int r = plan.roots[ri], m = plan.roots[ri - 1];
-        const TNode &n = g.ts[r], &mn = g.ts[m];
-        if (n.kind != TK::Reduce || n.numel != 1 || n.a != m) continue;
-        if (mn.kind != TK::Map && mn.kind != TK::Map2) continue;
-        if (mn.dt != n.dt || n.dt == DT::BOOL || mn.numel < (1 << 16) || gen.uniform(m)) continue;
-        if (row_length(mn.shape) != mn.numel) continue;
+    //
+    // The same when the reduction's input is an element-wise expression
+    // (not materialised) of the map's output and of other tensors at the
+    // same index (fuse_reduce_expr=0: its own split reduction): the map
+    // kernel also loads those tensors, evaluates the expression on the
+    // values it has just computed, and folds that. Its output is not read
+    // back. The functions of both together stay under 48 lines. Config 5's
+    // adjoint sums, sum(a * b) beside the map that makes a, are such.
+    if (tune("fuse_reduce", 1)) {
+      std::map<int, size_t> pos;
+      for (size_t i = 0; i < plan.roots.size(); i++) pos[plan.roots[i]] = i;
+      std::map<int, int> root_of_buf;
+      for (int r : plan.roots) root_of_buf[buf_of[r]] = r;
+      // m's kernel is the map template (a gather root takes it too, unless
+      // it reads a scatter back through its partition)
+      auto light = [&](int m, int64_t more, bool gathers) {
+        const TNode &mn = g.ts[m];
+        const bool gather = gathers && mn.kind == TK::Gather && !gbp_root_of.count(mn.b);
+        if (mn.kind != TK::Map && mn.kind != TK::Map2 && !gather) return false;
+        if (mn.numel < (1 << 16) || gen.uniform(m) || fused_red_of_map.count(m)) return false;
         const std::string code = gen.element_fn("fz_", m, true, true).code;
-        if (std::count(code.begin(), code.end(), '\n') >= 48) continue;
+        return std::count(code.begin(), code.end(), '\n') + more < 48;
+      };
+      for (size_t ri = 0; ri < plan.roots.size(); ri++) {
+        const int r = plan.roots[ri];
+        const TNode &n = g.ts[r];
+        if (n.kind != TK::Reduce || n.numel != 1 || n.dt == DT::BOOL) continue;
+        if (plan.materialized[n.a]) {
+          // the map's own output, the root just before
+          const int m = n.a;
+          if (ri == 0 || plan.roots[ri - 1] != m || g.ts[m].dt != n.dt || !light(m, 0, false)) continue;
+          fused_red_of_map[m] = r;
+          continue;
+        }
+        // An expression: folded in the kernel of the last root among the
+        // tensors it reads (every other one is ready by then), when that
+        // root is a map whose output it reads at its own index.
+        if (!tune("fuse_reduce_expr", 1)) continue;
+        const ElemFn fe = gen.element_fn("fz_", n.a, false, true);
+        int m = -1;
+        bool known = true;
+        for (const auto *v : {&fe.ident, &fe.ptrs})
+          for (int b : *v) {
+            const auto ro = root_of_buf.find(b);
+            if (ro == root_of_buf.end()) {
+              known = known && prog.bufs[b].role == BufRole::Param;
+              continue;
+            }
+            if (m < 0 || pos[ro->second] > pos[m]) m = ro->second;
+          }
+        if (!known || m < 0 || pos[m] > ri || g.ts[m].numel != g.ts[n.a].numel) continue;
+        const int mb = buf_of[m];
+        if (std::find(fe.ident.begin(), fe.ident.end(), mb) == fe.ident.end() ||
+            std::find(fe.ptrs.begin(), fe.ptrs.end(), mb) != fe.ptrs.end())
+          continue;
+        if (!light(m, std::count(fe.code.begin(), fe.code.end(), '\n'), true)) continue;
         fused_red_of_map[m] = r;
       }
+    }
     find_sibling_groups();
     find_rowlast_gathers();
     // the side buffers are computed buffers too: allocated with the others

@@ -141,7 +141,17 @@ def case_bs_mc_bands(run):
     p2 = bs.scalar_out(list(run(bs.call_mc_paths(16384, 8, F64), ins).items()), "price")
     assert abs(p2 - cf["price"]) <= e["call_mc_paths_16384x8_price_tol"]
     o = list(run(bs.call_greeks(65536, F64), ins).items())
-    assert bs.scalar_out(o, "price") == price  # the forward price of the grad graph is the same value
+    # the forward price of the grad graph is the same value (the interpreter,
+    # test_black_scholes.ml:27-30). On the device both prices are sums in a
+    # fixed tree, of different shapes: the grad graph materialises the
+    # terminal prices and folds its sum inside that map's kernel, the
+    # forward graph computes them inside its reduction. There the same value
+    # to the float64 band (the reference holds its CUDA backend's Greeks to
+    # the interpreter's within 1e-6, test_system.ml:150).
+    if run is run_device:
+        assert abs(bs.scalar_out(o, "price") - price) <= 1e-12 * (1 + abs(price))
+    else:
+        assert bs.scalar_out(o, "price") == price
     gn = lambda w: bs.scalar_out(o, G.grad_name("price", w))  # noqa: E731
     assert abs(gn("s0") - cf["delta"]) <= e["greeks_65536_delta_tol"]
     assert abs(gn("vol") - cf["vega"]) <= e["greeks_65536_vega_tol"]

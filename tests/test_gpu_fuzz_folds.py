@@ -148,3 +148,82 @@ def test_tile_row_scan_fuzz(device, seed):
         return
     for (name, e), (_, d) in zip(exp, got):
         np.testing.assert_array_equal(e.view(np.uint8), d.view(np.uint8), err_msg=str(what))
+
+
+N_EXPR_CASES = 24
+
+
+def expr_folded_case(seed):
+    """m = a map of x and y (an output); s = a reduction of an element-wise
+    expression of m and z, and in some cases of a gather of z, a scalar, or
+    of an f64 tensor cast down; m 1-D or 2-D (s reads it flattened); in
+    some cases another root between m and s. Returns the graph, the graph
+    with the expression as its output (for the exact float sum), inputs
+    and a description."""
+    r = np.random.default_rng(8000 + seed)
+    dt = [F32, F64, I32][seed % 3]
+    n = int(2 ** r.uniform(16.1, 21)) + int(r.integers(0, 4))
+    two_d = r.random() < 0.35
+    shape = (int(r.choice([64, 257])), 0) if two_d else (n,)
+    if two_d:
+        shape = (shape[0], max(1, n // shape[0]))
+        n = shape[0] * shape[1]
+    expr = FG._int_expr if dt is I32 else FG._float_expr
+    x, y, z = D.param("x", dt, shape), D.param("y", dt, shape), D.param("z", dt, shape)
+    inputs = [("x", FG._input(r, dt, shape)), ("y", FG._input(r, dt, shape)), ("z", FG._input(r, dt, shape))]
+    m = D.map2(lambda a, b: expr(r, [a, b], 2), x, y)
+    extra = str(r.choice(["plain", "gather", "scalar", "cast", "between"]))
+    outs = [("m", m)]
+    if extra == "between":
+        outs.append(("u", D.map(lambda a: D.add(a, a), x)))
+    e = D.map2(lambda a, c: expr(r, [a, c], 2), m, z)
+    flat = D.flatten(e) if two_d else e
+    if extra == "gather":
+        idx = D.param("idx", I32, (n,))
+        inputs.append(("idx", r.integers(0, n, size=n).astype(np.int32)))
+        flat = D.map2(lambda a, v: D.max(a, v), flat, D.gather(idx, D.flatten(z) if two_d else z))
+    elif extra == "scalar":
+        k = D.scalar("k", dt)
+        inputs.append(("k", np.array(3 if dt is I32 else 1.25, dtype=dt.np)))
+        flat = D.map2(lambda a, v: D.mul(a, v), flat, D.broadcast((n,), k))
+    elif extra == "cast":
+        w = D.param("w", F64 if dt is not F64 else F32, (n,))
+        inputs.append(("w", r.uniform(0.5, 1.5, size=n).astype(w.dtype.np)))
+        flat = D.map2(lambda a, v: D.add(a, D.cast(dt, v)), flat, w)
+    ops = ["add", "max", "min"] + (["mul", "xor"] if dt is I32 else [])
+    op = ops[int(r.integers(len(ops)))]
+    comb = {"add": D.add, "max": D.max, "min": D.min, "mul": D.mul, "xor": D.bit_xor}[op]
+    iv = int(r.integers(-3, 4)) if dt is I32 else float(r.choice([0.0, 1.5, -2.0]))
+    s = D.reduce(comb, D.const(dt, iv), flat)
+    g = Graph.create("efold%d" % seed, outs + [("s", s)])
+    g_terms = Graph.create("eterms%d" % seed, [("e", flat)])
+    knobs = "map_unroll=2" if seed % 4 == 3 else ""
+    return g, g_terms, inputs, (dt.name, shape, extra, op, iv, knobs)
+
+
+@pytest.mark.parametrize("seed", range(N_EXPR_CASES))
+def test_expression_fold_fuzz(device, monkeypatch, seed):
+    """A whole-tensor reduction of an element-wise expression of a map's
+    output folds inside that map's kernel: integers, max and min bit-exact
+    against the oracle; a float sum within the band of the exact sum of
+    its terms (the oracle's own terms, which the device's map matches)."""
+    g, g_terms, inputs, what = expr_folded_case(seed)
+    print("case", seed, *what, flush=True)
+    if what[5]:
+        monkeypatch.setenv("CCHIP_TUNE", what[5])
+    t = templates(g)
+    assert "reduce_split" not in t and "reduce_split_fold" in t, (what, t)
+    exp, got = _run(g, inputs)
+    float_sum = what[0] != "i32" and what[3] == "add"
+    bad = [v for v in Diff.policy_check(g, exp, got) if not v.ok and not (float_sum and v.name == "s")]
+    assert not bad, (what, bad)
+    e, d = dict(exp), dict(got)
+    if not float_sum:
+        np.testing.assert_array_equal(np.atleast_1d(e["s"]).view(np.uint8), np.atleast_1d(d["s"]).view(np.uint8),
+                                      err_msg=str(what))
+        return
+    names = {n for n, _ in g_terms.params}
+    terms = dict(oracle.run(g_terms, [(k, v) for k, v in inputs if k in names]))["e"]
+    exact = math.fsum([float(what[4])] + terms.astype(np.float64).tolist())
+    tol = 1e-4 if what[0] == "f32" else 1e-12
+    assert abs(float(d["s"]) - exact) <= tol * (1 + abs(exact)), (what, float(d["s"]), exact, float(e["s"]))

@@ -163,7 +163,10 @@ def test_matmul_small_cases_on_device(device):
 
 def test_black_scholes_mc_on_device(device):
     """call_mc at 65536 paths within 0.25 of the closed form, call_mc_paths
-    16384 x 8 within 0.5; the Greeks graph's forward price equals call_mc's."""
+    16384 x 8 within 0.5; the Greeks graph's forward price equals call_mc's
+    to the float64 band: the interpreter's two sums are the same sequence,
+    the device's two fixed trees have different shapes (the Greeks graph
+    folds its sum inside the kernel that writes the terminal prices)."""
     cf = bs.analytic()
     ins = bs.inputs(F64, seed=7)
     _, got = assert_policy(bs.call_mc(65536, F64), ins)
@@ -172,4 +175,4 @@ def test_black_scholes_mc_on_device(device):
     _, got = assert_policy(bs.call_mc_paths(16384, 8, F64), ins)
     assert abs(bs.scalar_out(got, "price") - cf["price"]) <= 0.5
     _, got = assert_policy(bs.call_greeks(65536, F64), ins)
-    assert bs.scalar_out(got, "price") == price
+    assert abs(bs.scalar_out(got, "price") - price) <= 1e-12 * (1 + abs(price))

@@ -56,6 +56,46 @@ def test_saxpy_is_map_then_reduce(monkeypatch):
     assert [t for _, t in ks] == ["map", "reduce_split", "reduce_split_fold"]
 
 
+def test_reduction_of_an_expression_folds_in_its_producer(monkeypatch):
+    """sum(a * z) beside the map that makes a folds inside that map's
+    kernel, which also loads z; so does an expression of a 2-D map read
+    flattened, of a gather root's output, and one with another root in
+    between. Not when the expression reads the map's output at another
+    index, or when fuse_reduce_expr=0."""
+    n = 1 << 18
+    x, y, z = (D.param(c, F32, (n,)) for c in "xyz")
+    z0 = D.const(F32, 0.0)
+    a = D.map2(D.add, x, y)
+    g = Graph.create("e", [("a", a), ("s", D.reduce(D.add, z0, D.map2(D.mul, a, z)))])
+    assert [t for _, t in kernels_of(g)] == ["map", "reduce_split_fold"]
+    moved = _bytes(g, "moved")
+    assert moved["map"] == 3 * 4 * n + 4 * n  # x, y, a, and z for the expression
+    # a root in between, reading the sum's other input
+    u = D.map(lambda v: D.mul(v, v), z)
+    g = Graph.create("e", [("a", a), ("u", u), ("s", D.reduce(D.max, z0, D.map2(D.mul, a, z)))])
+    assert [t for _, t in kernels_of(g)] == ["map", "map", "reduce_split_fold"]
+    # 2-D, flattened
+    x2, w2 = D.param("x2", F32, (64, 4096)), D.param("w2", F32, (64, 4096))
+    a2 = D.map(lambda v: D.add(v, v), x2)
+    g = Graph.create("e", [("a", a2), ("s", D.reduce(D.add, z0, D.flatten(D.map2(D.mul, a2, w2))))])
+    assert [t for _, t in kernels_of(g)] == ["map", "reduce_split_fold"]
+    # a gather root
+    idx = D.param("idx", I32, (n,))
+    st = D.map(D.exp, D.gather(idx, x))
+    g = Graph.create("e", [("st", st), ("s", D.reduce(D.add, z0, D.map(lambda v: D.max(v, z0), st)))])
+    assert "reduce_split" not in [t for _, t in kernels_of(g)]
+    # the map's output read at another index: its own split reduction
+    rev = D.map(lambda i: D.sub(D.const(I32, n - 1), i), D.iota((n,)))
+    g = Graph.create("e", [("a", a), ("s", D.reduce(D.add, z0, D.map2(D.mul, D.gather(rev, a), z)))])
+    assert "reduce_split" in [t for _, t in kernels_of(g)]
+    monkeypatch.setenv("CCHIP_TUNE", "fuse_reduce_expr=0")
+    g = Graph.create("e", [("a", a), ("s", D.reduce(D.add, z0, D.map2(D.mul, a, z)))])
+    assert [t for _, t in kernels_of(g)] == ["map", "reduce_split", "reduce_split_fold"]
+    monkeypatch.delenv("CCHIP_TUNE")
+    # config 5's adjoint sums and its price: no split reduction left
+    assert "reduce_split" not in [t for _, t in kernels_of(C.mc_greeks())]
+
+
 def test_fanout_materialises_shared_node_once():
     bufs, ks, _ = parse(H.plan(P.fanout(1000).graph()))
     computed = [b for b in bufs if b[3] == "computed"]
