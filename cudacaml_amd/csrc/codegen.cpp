@@ -262,6 +262,11 @@ class Gen {
   // long (through a reshape they need not be).
   std::map<int, std::pair<int, int64_t>> rowlast_;
   std::map<int, int> rowlast_gather_;  // gather tensor -> scan tensor
+  // Scatters whose index is a * j + b with a != 0 and every value in range,
+  // so that each bin is 0 + its one source value or 0: tensor -> (a, b).
+  // A read of such a tensor computes that element from the source at j
+  // instead of loading the scatter's buffer.
+  std::map<int, std::pair<int64_t, int64_t>> scatter_inline_;
 
  private:
   std::map<std::string, std::pair<std::string, int64_t>> rowlast_idx_;
@@ -327,6 +332,20 @@ class Gen {
       const int b = rowlast_.at(t).first;
       add_unique(ptrs_, b);
       r = def(storage_vc(g_.ts[t].dt), "b" + std::to_string(b) + "[" + rowlast_idx_.at(idx.s).first + "]");
+    } else if (p_.materialized[t] && scatter_inline_.count(t)) {
+      // bin idx of scatter_add(a * j + b, src): 0 + src[j] where idx = a * j
+      // + b for some j in range, else 0 (the scatter's own kernel computes
+      // the same)
+      const TNode &sn = g_.ts[t];
+      const std::string A = std::to_string(scatter_inline_.at(t).first);
+      const std::string N = std::to_string(g_.ts[sn.a].numel);
+      const Val q = def(VC::I32, "(" + idx.s + ") - (" + std::to_string(scatter_inline_.at(t).second) + ")");
+      const Val ok = def(VC::B, "(" + q.s + " % (" + A + ")) == 0 && " + q.s + " / (" + A + ") >= 0 && " + q.s +
+                                    " / (" + A + ") < " + N);
+      const Val j = def(VC::I32, ok.s + " ? " + q.s + " / (" + A + ") : 0");
+      const Val v = elem(sn.b, j);
+      const std::string z = zero_of(sn.dt);
+      r = def(storage_vc(sn.dt), ok.s + " ? (" + z + " + " + as_storage(v, sn.dt) + ") : " + z);
     } else if (p_.materialized[t]) {
       int b = buf_of_[t];
       DT d = g_.ts[t].dt;
@@ -4962,12 +4981,12 @@ struct Lowering {
   // does not output: their kernels are dropped and their buffers never
   // allocated. The fusion plan itself is unchanged.
   void elide_unread_broadcasts(std::vector<std::vector<int>> &launches) {
-    if (!tune("remat_broadcast", 1)) return;
+    const bool remat = tune("remat_broadcast", 1) != 0;
     std::vector<char> dead_kernel(prog.kernels.size(), 0);
     bool any = false;
     for (size_t ri = 0; ri < plan.roots.size(); ri++) {
       const int r = plan.roots[ri];
-      if (!gen.uniform(r)) continue;
+      if (!(remat && gen.uniform(r)) && !gen.scatter_inline_.count(r)) continue;
       const int b = buf_of[r];
       bool needed = false;
       for (auto &o : g.outputs) needed |= o.second == r;
@@ -5017,6 +5036,24 @@ struct Lowering {
         if (n.kind != TK::Gather) continue;
         const int S = n.b;
         if (g.ts[S].kind == TK::Scatter && g.ts[S].a == n.a && !gbp_root_of.count(S)) gbp_root_of[S] = r;
+      }
+    // Scatters with an injective affine index in range are computed where
+    // they are read (Gen::scatter_inline_; scatter_inline=0 reads their
+    // buffers); their kernels and buffers go when nothing else reads them
+    // (elide_unread_broadcasts). Config 5's gather adjoint, which puts each
+    // path's adjoint at p * 64 + 63 of a 2^28-element tensor that one map
+    // reads: 1 GiB written and read back.
+    if (tune("scatter_inline", 1))
+      for (int r : plan.roots) {
+        const TNode &n = g.ts[r];
+        if (n.kind != TK::Scatter || n.dt == DT::BOOL) continue;
+        const int64_t M = n.numel, N = g.ts[n.a].numel;
+        const Aff ia = aff_t(n.a);
+        if (!ia.ok || ia.a == 0 || M <= 0 || N <= 0 || M > INT32_MAX - 4) continue;
+        if (ia.a > INT32_MAX || ia.a < -INT32_MAX || ia.b > INT32_MAX || ia.b < -INT32_MAX) continue;
+        const __int128 e0 = ia.b, e1 = (__int128)ia.a * (N - 1) + ia.b;
+        if (std::min(e0, e1) < 0 || std::max(e0, e1) >= M) continue;
+        gen.scatter_inline_[r] = {ia.a, ia.b};
       }
     // A reduction of a whole map output to one value, right after the map's
     // own root, is folded inside the map kernel when the map is light

@@ -327,12 +327,12 @@ def check_pathwise(o, zsum, steps, tol):
 def test_config5_greeks_f64_full_size_pathwise(device):
     """The benchmark's f64 graph at 2^22 paths x 64 steps (its gather
     adjoint, a scatter into 2^28 bins through the strided index p*64 + 63,
-    is one pass over the bins) against the pathwise estimator on the same
+    is computed where the adjoint map reads it) against the pathwise estimator on the same
     Philox draws, within 1e-9 relative (summation order is the only
     difference)."""
     n, steps = C.PATHS5, C.STEPS5
     g = C.mc_greeks(n, steps, F64)
-    assert {"scatter_affine", "scan_rowseq"} <= set(roles(g)) and "reduce_rowseq" not in roles(g)
+    assert "scan_rowseq" in roles(g) and not {"scatter_affine", "reduce_rowseq"} & set(roles(g))
     o = run_dev(g, bs.inputs(F64, seed=7))
     zg = Graph.create("z", [("z", rng.normal(F64, D.scalar("seed", I32), (n, steps)))])
     z = run_dev(zg, [("seed", np.array(7, np.int32))])["z"]
@@ -404,7 +404,7 @@ def test_config5_greeks_f32_full_size(device):
     zf = gen(C.gen_normals((n, steps), F32), 7)
     assert np.isfinite(zf).all()
     g = bs.call_paths_greeks(n, steps, F32, draws=D.param("z", F32, (n, steps)))
-    assert {"scatter_affine", "scan_rowseq"} <= set(roles(g)) and "reduce_rowseq" not in roles(g)
+    assert "scan_rowseq" in roles(g) and not {"scatter_affine", "reduce_rowseq"} & set(roles(g))
     o = run_dev(g, [x for x in bs.inputs(F32) if x[0] != "seed"] + [("z", zf)])
     zsum = zf.sum(axis=1, dtype=np.float64)
     del zf

@@ -796,6 +796,54 @@ def test_broadcast_read_from_its_source(device, dtype):
 
 
 @pytest.mark.parametrize("dtype", [F32, F64, I32])
+def test_affine_scatter_read_in_place(device, dtype):
+    """A scatter_add through an injective affine index in range, read by a
+    map at its own index, gathered at random indices, reduced and scanned
+    by max, and read as a matmul operand, each computing its elements in
+    place (no scatter kernel): bit-exact against the oracle, including a
+    -0.0 source landing as +0.0 and NaN/inf sources."""
+    n = 100003
+    for a, b, m in [(3, 1, 3 * n + 5), (-2, 2 * n + 7, 2 * n + 9), (64, 63, 64 * n)]:
+        idx = D.map(lambda p: D.add(D.mul(p, D.const(I32, a)), D.const(I32, b)), D.iota((n,)))
+        src, y = D.param("src", dtype, (n,)), D.param("y", dtype, (m,))
+        gi = D.param("gi", I32, (5000,))
+        h = D.scatter_add(idx, D.map(lambda v: D.add(v, v), src), (m,))
+        one = D.const(dtype, 1 if not dtype.is_float else 1.0)
+        g1 = Graph.create("inplace", [("o", D.map2(lambda u, v: D.add(D.mul(u, v), u), h, y)),
+                                      ("g", D.gather(gi, h))])
+        lo = D.const(dtype, -(1 << 30) if not dtype.is_float else -1e30)
+        g2 = Graph.create("inplace2", [("mx", D.reduce(D.max, lo, D.map(lambda u: D.add(u, one), h))),
+                                       ("sc", D.scan(D.max, lo, h))])
+        for g in (g1, g2):
+            assert "scatter_affine" not in templates(g), (a, b, templates(g))
+        x = data(dtype, (n,), 31)
+        ins = [("src", x), ("y", data(dtype, (m,), 32)),
+               ("gi", np.random.default_rng(33).integers(0, m, size=5000).astype(np.int32))]
+        for g, special in ((g1, True), (g2, False)):
+            xs = x.copy()
+            if special and dtype.is_float:
+                xs[:8] = [-0.0, np.nan, np.inf, -np.inf, 0.0, -1.5, 2.5, -0.0]
+            gins = [(k, xs if k == "src" else v) for k, v in ins if k in {nm for nm, _ in g.params}]
+            exp = dict(oracle.run(g, gins))
+            c = H.compile(g)
+            try:
+                got = dict(H.run(c, gins))
+            finally:
+                c.release()
+            for k in exp:
+                np.testing.assert_array_equal(np.atleast_1d(got[k]).view(np.uint8), np.atleast_1d(exp[k]).view(np.uint8),
+                                              err_msg="%s %s %s" % (a, b, k))
+    if dtype in (F32, F64):
+        # a matmul operand computes it as its element function
+        src = D.param("src", dtype, (1 << 14,))
+        idx = D.map(lambda p: D.add(D.mul(p, D.const(I32, 64)), D.const(I32, 63)), D.iota((1 << 14,)))
+        h = D.scatter_add(idx, src, (1 << 20,))
+        g = Graph.create("mm", [("c", D.matmul(D.reshape((1024, 1024), h), D.param("w", dtype, (1024, 64))))])
+        assert "scatter_affine" not in templates(g)
+        check(g, [("src", data(dtype, (1 << 14,), 34)), ("w", data(dtype, (1024, 64), 35))], [])
+
+
+@pytest.mark.parametrize("dtype", [F32, F64, I32])
 def test_scatter_affine_index(device, dtype):
     """scatter_add through an index a*i + b built from iota (a strided,
     reversed, offset index; also through a reshape): one pass over the bins,

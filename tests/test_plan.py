@@ -96,6 +96,35 @@ def test_reduction_of_an_expression_folds_in_its_producer(monkeypatch):
     assert "reduce_split" not in [t for _, t in kernels_of(C.mc_greeks())]
 
 
+def test_affine_scatter_is_read_in_place(monkeypatch):
+    """A scatter_add whose index is a*j + b, injective and in range, is
+    computed where it is read (0 + its one source value, or 0): no scatter
+    kernel, its buffer elided. It keeps both when it is an output, and with
+    scatter_inline=0; an index that can leave the range is never read in
+    place."""
+    n = 1 << 16
+    src, y = D.param("src", F32, (n,)), D.param("y", F32, (64 * n,))
+    idx = D.map(lambda p: D.add(D.mul(p, D.const(I32, 64)), D.const(I32, 63)), D.iota((n,)))
+    h = D.scatter_add(idx, D.map(lambda v: D.mul(v, v), src), (64 * n,))
+    o = D.map2(D.mul, h, y)
+    g = Graph.create("s", [("o", o)])
+    bufs, ks, _ = parse(H.plan(g))
+    assert [t for _, t in ks] == ["map"]
+    assert [b[3] for b in bufs if b[2] == 64 * n] == ["param", "elided", "computed"]
+    assert [t for _, t in kernels_of(Graph.create("s", [("o", o), ("h", h)]))] == ["scatter_affine", "map"]
+    # a matmul operand computes it too, as its element function
+    w = D.param("w", F32, (64, 16))
+    assert [t for _, t in kernels_of(Graph.create("m", [("c", D.matmul(D.reshape((n, 64), h), w))]))] == ["matmul_tiled"]
+    wide = D.map(lambda p: D.mul(p, D.const(I32, 65)), D.iota((n,)))
+    g = Graph.create("s", [("o", D.map2(D.mul, D.scatter_add(wide, src, (64 * n,)), y))])
+    assert "map" in [t for _, t in kernels_of(g)] and len(kernels_of(g)) > 1
+    monkeypatch.setenv("CCHIP_TUNE", "scatter_inline=0")
+    assert [t for _, t in kernels_of(Graph.create("s", [("o", o)]))] == ["scatter_affine", "map"]
+    monkeypatch.delenv("CCHIP_TUNE")
+    # config 5's gather adjoint
+    assert "scatter_affine" not in [t for _, t in kernels_of(C.mc_greeks())]
+
+
 def test_fanout_materialises_shared_node_once():
     bufs, ks, _ = parse(H.plan(P.fanout(1000).graph()))
     computed = [b for b in bufs if b[3] == "computed"]
