@@ -402,6 +402,11 @@ class Gen {
         std::string jn = "v" + std::to_string(ntmp_++);
         body_ << "  int " << jn << " = " << j.s << ";\n";
         body_ << "  if ((unsigned)" << jn << " >= " << src.numel << "u) { cc_flag(err, 1); " << jn << " = 0; }\n";
+        // one element: read at 0 whatever the index (the check above still
+        // flags one out of range), so the load and what is computed from it
+        // do not depend on the element and leave the kernel's loop (a
+        // gradient spreads a whole reduction's adjoint by gather(i / n))
+        if (src.numel == 1) return elem(n.b, Val{"0", VC::I32});
         return elem(n.b, Val{jn, VC::I32});
       }
       case TK::Reshape: return elem(n.a, idx);
