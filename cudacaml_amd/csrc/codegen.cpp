@@ -18,6 +18,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cctype>
 #include <cstring>
 #include <functional>
 #include <set>
@@ -1058,6 +1059,25 @@ int64_t tune(const char *key, int64_t dflt) {
   return dflt;
 }
 
+// Whether generated code calls one of the f32 functions computed in double.
+bool calls_f32_fn(const std::string &code) {
+  for (const char *fn : {"cc_expf(", "cc_logf(", "cc_sinf(", "cc_cosf(", "cc_erff(", "cc_erfinvf("})
+    if (code.find(fn) != std::string::npos) return true;
+  return false;
+}
+
+// Whether generated code loads a buffer (b<k>[...]) at anything but index 0.
+bool varying_load(const std::string &code) {
+  for (size_t q = code.find('b'); q != std::string::npos; q = code.find('b', q + 1)) {
+    if (q > 0 && (std::isalnum((unsigned char)code[q - 1]) || code[q - 1] == '_')) continue;
+    size_t e = q + 1;
+    while (e < code.size() && std::isdigit((unsigned char)code[e])) e++;
+    if (e == q + 1 || e >= code.size() || code[e] != '[') continue;
+    if (code.compare(e, 3, "[0]") != 0) return true;
+  }
+  return false;
+}
+
 // Accumulation with an empty flag (`acc`, `has` in scope): x is folded in on
 // the right; the first value is taken as is.
 std::string fold_in(const std::string &cmb, const std::string &T, const std::string &x) {
@@ -1567,8 +1587,20 @@ struct Lowering {
     // is unconditional too: a lane past the end recomputes the last group
     // and stores the same values its owner stores. A guarded store would
     // let the compiler sink the whole second chain under the guard.
+    //
+    // A lighter function that calls one of the f32 functions computed in
+    // double (about 40 instructions each) and also loads a buffer at an
+    // index that varies by element leaves each group's loads exposed behind
+    // that work: two groups a lane overlap them (map_unroll_gx=0: one).
+    // Config 5's adjoint map (exp of the path, and the terminal price
+    // gathered for the gather's adjoint computed in place): 528 -> 426 us;
+    // its maps that only stream measured slower with two groups (325 ->
+    // 360 us), as did the f32 Horner map above.
     int64_t UN = tune("map_unroll", -1);
-    if (UN < 0) UN = std::count(f.code.begin(), f.code.end(), '\n') >= 48 ? 4 / G : 1;
+    if (UN < 0) {
+      UN = std::count(f.code.begin(), f.code.end(), '\n') >= 48 ? 4 / G : 1;
+      if (UN == 1 && G == 4 && tune("map_unroll_gx", 1) && calls_f32_fn(f.code) && varying_load(f.code)) UN = 2;
+    }
     UN = std::max<int64_t>(1, std::min<int64_t>(4, UN));
     // A whole-tensor reduction of this output folds it here: each lane
     // folds the elements it stores, each wave combines its lanes and stores
