@@ -1207,6 +1207,10 @@ struct Lowering {
   // bytes a map kernel reads for its folded reduction's expression beyond
   // its own loads
   std::map<int, int64_t> map_extra_moved;
+  // Map roots whose output nothing reads once their reduction folds in
+  // their kernel (set by lower_program for a second lowering): their
+  // kernels store nothing but the partials, and their buffers are elided.
+  std::set<int> no_store;
   // Row roots over one tensor fused into one kernel: a row scan that takes
   // the one-workgroup-a-row tile template, and the reductions of the same
   // tensor's rows that fold as a tree. The group's first root in the plan
@@ -1474,6 +1478,7 @@ struct Lowering {
     prog.kernels[main].moved_bytes = n.kind == TK::Reduce && fused_part_of_red.count(r) ? out : bytes;
     const auto em = map_extra_moved.find(r);
     if (em != map_extra_moved.end()) prog.kernels[main].moved_bytes += em->second;
+    if (no_store.count(r)) prog.kernels[main].moved_bytes -= out;
     const auto rl = gen.rowlast_.find(r);
     if (rl != gen.rowlast_.end())
       prog.kernels[main].moved_bytes += prog.bufs[rl->second.first].bytes();
@@ -1534,10 +1539,12 @@ struct Lowering {
     const auto sd = gen.rowlast_.find(t);
     const int side = sd != gen.rowlast_.end() ? sd->second.first : -1;
     const int64_t SL_ = side >= 0 ? sd->second.second : 0;
+    const bool store = !no_store.count(t);
+    if (!store) prog.bufs[out].elided = true;
     Params p;
     add_in(p, f);
     if (fexpr) add_in(p, fx);
-    p.out.push_back(out);
+    if (store) p.out.push_back(out);
     if (side >= 0) p.out.push_back(side);
     std::vector<int> args;
     std::string params = param_list(p, args);
@@ -1653,9 +1660,9 @@ struct Lowering {
         << vec_loads(f, "i", "    ", tyof(), ntl, G) << (fexpr ? vec_loads(fx, "i", "    ", tyof(), ntl, G) : "")
         << "    " << VG << "<" << T << "> r;\n";
       for (int u = 0; u < G; u++) k << "    r." << comp[u] << " = " << lane_call(f, "i", u) << ";\n";
-      if (nts)
+      if (store && nts)
         k << "    cc_st" << G << "_nt(b" << out << " + i, r);\n";
-      else
+      else if (store)
         k << "    *(" << VG << "<" << T << ">*)(b" << out << " + i) = r;\n";
       if (side >= 0)
         for (int u = 0; u < G; u++)
@@ -1682,11 +1689,10 @@ struct Lowering {
       }
       for (int64_t q = 0; q < UN; q++) {
         std::string iq = "min(v0 + " + std::to_string(q * 256) + ", nvec - 1) * " + std::to_string(G);
-        k << "    ";
-        if (nts)
-          k << "cc_st" << G << "_nt(b" << out << " + " << iq << ", r[" << q << "]);\n";
-        else
-          k << "*(" << VG << "<" << T << ">*)(b" << out << " + " << iq << ") = r[" << q << "];\n";
+        if (store && nts)
+          k << "    cc_st" << G << "_nt(b" << out << " + " << iq << ", r[" << q << "]);\n";
+        else if (store)
+          k << "    *(" << VG << "<" << T << ">*)(b" << out << " + " << iq << ") = r[" << q << "];\n";
         // a clamped group stores its owner's values again, here as there
         if (side >= 0)
           for (int u = 0; u < G; u++)
@@ -1702,7 +1708,8 @@ struct Lowering {
     k << "  }\n"
       << "  for (int i = nvec * " << G << " + blockIdx.x * 256 + threadIdx.x; i < " << N << "; i += gridDim.x * 256)";
     if (fuse || side >= 0)
-      k << " {\n    const " << T << " v_ = " << f.call_scalar("i") << ";\n    b" << out << "[i] = v_;\n    "
+      k << " {\n    const " << T << " v_ = " << f.call_scalar("i") << ";\n    "
+        << (store ? "b" + std::to_string(out) + "[i] = v_;\n    " : std::string())
         << (fuse ? fold_in(rc, TR,
                            fexpr ? fe.call("i", [&](int b) { return b == out ? std::string("v_")
                                                                              : "b" + std::to_string(b) + "[i]"; })
@@ -5234,6 +5241,31 @@ int64_t tune_knob(const char *key, int64_t dflt) { return tune(key, dflt); }
 ProgramIR lower_program(const Graph &g) {
   Lowering l(g);
   l.run();
+  // A map root whose reduction folds in its kernel may have no reader
+  // left: a tensor materialised because the reduction's expression uses it
+  // twice (config 5's last adjoint map, 1 GiB). Lowered again, its kernel
+  // stores only the partials (skip_unread_stores=0 keeps the store).
+  if (tune("skip_unread_stores", 1)) {
+    std::set<int> unread;
+    for (auto &fr : l.fused_red_of_map) {
+      const int m = fr.first, b = l.buf_of[m];
+      const std::string own = "k_" + std::to_string(g.ts[m].id);
+      bool read = l.gen.rowlast_.count(m) > 0;
+      for (auto &o : g.outputs) read |= o.second == m;
+      for (const KernelSpec &k : l.prog.kernels) {
+        if (read) break;
+        if (k.name == own) continue;
+        for (int a : k.args) read |= a == b;
+      }
+      if (!read) unread.insert(m);
+    }
+    if (!unread.empty()) {
+      Lowering l2(g);
+      l2.no_store = unread;
+      l2.run();
+      return l2.prog;
+    }
+  }
   return l.prog;
 }
 

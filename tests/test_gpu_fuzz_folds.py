@@ -172,11 +172,15 @@ def expr_folded_case(seed):
     x, y, z = D.param("x", dt, shape), D.param("y", dt, shape), D.param("z", dt, shape)
     inputs = [("x", FG._input(r, dt, shape)), ("y", FG._input(r, dt, shape)), ("z", FG._input(r, dt, shape))]
     m = D.map2(lambda a, b: expr(r, [a, b], 2), x, y)
-    extra = str(r.choice(["plain", "gather", "scalar", "cast", "between"]))
-    outs = [("m", m)]
+    extra = str(r.choice(["plain", "gather", "scalar", "cast", "between", "unread"]))
+    # unread: m is no output, only the expression reads it (twice, so the
+    # plan materialises it), and its kernel stores nothing but the partials
+    outs = [] if extra == "unread" else [("m", m)]
     if extra == "between":
         outs.append(("u", D.map(lambda a: D.add(a, a), x)))
     e = D.map2(lambda a, c: expr(r, [a, c], 2), m, z)
+    if extra == "unread":
+        e = D.map2(lambda u, v: D.add(u, v), e, m)
     flat = D.flatten(e) if two_d else e
     if extra == "gather":
         idx = D.param("idx", I32, (n,))
@@ -213,6 +217,8 @@ def test_expression_fold_fuzz(device, monkeypatch, seed):
         monkeypatch.setenv("CCHIP_TUNE", what[5])
     t = templates(g)
     assert "reduce_split" not in t and "reduce_split_fold" in t, (what, t)
+    if what[2] == "unread":
+        assert " elided" in H.plan(g), what
     exp, got = _run(g, inputs)
     float_sum = what[0] != "i32" and what[3] == "add"
     bad = [v for v in Diff.policy_check(g, exp, got) if not v.ok and not (float_sum and v.name == "s")]

@@ -88,6 +88,15 @@ def test_reduction_of_an_expression_folds_in_its_producer(monkeypatch):
     rev = D.map(lambda i: D.sub(D.const(I32, n - 1), i), D.iota((n,)))
     g = Graph.create("e", [("a", a), ("s", D.reduce(D.add, z0, D.map2(D.mul, D.gather(rev, a), z)))])
     assert "reduce_split" in [t for _, t in kernels_of(g)]
+    # a read only by the expression (twice, so materialised): its kernel
+    # stores nothing but the partials, and its buffer is elided
+    g = Graph.create("e", [("s", D.reduce(D.add, z0, D.map2(D.add, D.map2(D.mul, a, z), a)))])
+    bufs, ks, _ = parse(H.plan(g))
+    assert [t for _, t in ks] == ["map", "reduce_split_fold"]
+    assert [b[3] for b in bufs if b[2] == n] == ["param", "param", "param", "elided"]
+    assert _bytes(g, "moved")["map"] == 3 * 4 * n
+    monkeypatch.setenv("CCHIP_TUNE", "skip_unread_stores=0")
+    assert [b[3] for b in parse(H.plan(g))[0] if b[2] == n] == ["param", "param", "param", "computed"]
     monkeypatch.setenv("CCHIP_TUNE", "fuse_reduce_expr=0")
     g = Graph.create("e", [("a", a), ("s", D.reduce(D.add, z0, D.map2(D.mul, a, z)))])
     assert [t for _, t in kernels_of(g)] == ["map", "reduce_split", "reduce_split_fold"]
