@@ -233,3 +233,33 @@ def test_expression_fold_fuzz(device, monkeypatch, seed):
     exact = math.fsum([float(what[4])] + terms.astype(np.float64).tolist())
     tol = 1e-4 if what[0] == "f32" else 1e-12
     assert abs(float(d["s"]) - exact) <= tol * (1 + abs(exact)), (what, float(d["s"]), exact, float(e["s"]))
+
+
+def test_expression_fold_reports_index_errors(device):
+    """A sum of an expression that gathers, folded inside the map that
+    writes its operand: an index out of range is reported as the unfused
+    reduction reports it, and the next run with good indices is clean and
+    matches the oracle."""
+    n = (1 << 18) + 3
+    x, z = D.param("x", F32, (n,)), D.param("z", F32, (n,))
+    idx = D.param("idx", I32, (n,))
+    a = D.map(lambda v: D.add(v, D.const(F32, 0.5)), x)
+    s = D.reduce(D.max, D.const(F32, -1e30), D.map2(D.mul, a, D.gather(idx, z)))
+    g = Graph.create("eerr", [("a", a), ("s", s)])
+    t = templates(g)
+    assert "reduce_split" not in t and "reduce_split_fold" in t, t
+    r = np.random.default_rng(9)
+    good = r.integers(0, n, size=n).astype(np.int32)
+    bad = good.copy()
+    bad[n // 2] = n
+    base = [("x", r.uniform(-1, 1, n).astype(np.float32)), ("z", r.uniform(-1, 1, n).astype(np.float32))]
+    c = H.compile(g)
+    try:
+        with pytest.raises(ValueError, match="gather index out of bounds"):
+            H.run(c, base + [("idx", bad)])
+        got = dict(H.run(c, base + [("idx", good)]))
+    finally:
+        c.release()
+    exp = dict(oracle.run(g, base + [("idx", good)]))
+    for k in exp:
+        np.testing.assert_array_equal(np.atleast_1d(got[k]).view(np.uint8), np.atleast_1d(exp[k]).view(np.uint8))

@@ -737,6 +737,33 @@ def test_gather_back_through_the_partition(device, n, bins, dtype, two, monkeypa
         np.testing.assert_array_equal(o["back"], plain["back"])
 
 
+@pytest.mark.parametrize("bad", [1, -1, None])
+def test_one_element_gather(device, bad):
+    """A gather from a one-element tensor (how a gradient spreads a whole
+    sum's adjoint) reads that element at any index in range, loaded once
+    outside the kernel's loop; an index out of range still raises, and a
+    good run after it is clean."""
+    n = 70001
+    x, idx = D.param("x", F32, (n,)), D.param("idx", I32, (n,))
+    tot = D.reduce(D.add, D.const(F32, 0.0), x)
+    g = Graph.create("g1", [("o", D.map2(D.mul, x, D.gather(idx, D.map(lambda v: D.mul(v, v), tot))))])
+    xv = data(F32, (n,), 41)
+    iv = np.zeros(n, np.int32)
+    c = H.compile(g)
+    try:
+        if bad is not None:
+            biv = iv.copy()
+            biv[n - 1] = bad
+            with pytest.raises(ValueError, match="gather index out of bounds"):
+                H.run(c, [("x", xv), ("idx", biv)])
+        got = dict(H.run(c, [("x", xv), ("idx", iv)]))["o"]
+    finally:
+        c.release()
+    exp = dict(oracle.run(g, [("x", xv), ("idx", iv)]))["o"]
+    bad_v = [v for v in Diff.policy_check(g, [("o", exp)], [("o", got)]) if not v.ok]
+    assert not bad_v, bad_v
+
+
 @pytest.mark.parametrize("two", [False, True])
 def test_gather_back_out_of_range_raises(device, two):
     """An index out of range is skipped by the scatter's partition, so it
