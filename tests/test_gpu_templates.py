@@ -1205,7 +1205,53 @@ KNOB_CASES = [
      lambda: [("a", data(F64, (3, 65536), 122)), ("b", data(F64, (65536, 3), 123))], "matmul_tiled"),
     # a one-kernel program replayed from a recorded HIP graph
     ("graphs=1,graph_min_kernels=1", lambda: P.chain(5000).graph(), lambda: P.chain(5000).inputs(), "map"),
+    # the lowering's own rewrites turned off, each on a graph that takes it
+    ("same_fold=0", lambda: _pair_graph(), lambda: [("x", data(F32, (2048, 300), 124))], "reduce_rowseq"),
+    ("fuse_reduce_expr=0", lambda: _expr_sum_graph(True), lambda: _expr_sum_inputs(125), "reduce_split"),
+    ("skip_unread_stores=0", lambda: _expr_sum_graph(False), lambda: _expr_sum_inputs(126), "map"),
+    ("scatter_inline=0", lambda: _affine_read_graph(), lambda: _affine_read_inputs(127), "scatter_affine"),
+    ("map_unroll_gx=0", lambda: _exp_gather_graph(), lambda: _exp_gather_inputs(128), "map"),
 ]
+
+
+def _pair_graph():
+    x, z = D.param("x", F32, (2048, 300)), D.const(F32, 0.0)
+    return Graph.create("pair", [("s", D.scan_rows(D.add, z, x)), ("r", D.reduce_rows(D.add, z, x))])
+
+
+def _expr_sum_graph(out):
+    n = 300001
+    x, y, z = (D.param(c, F32, (n,)) for c in "xyz")
+    a = D.map2(lambda u, v: D.add(D.mul(u, D.const(F32, 2.0)), v), x, y)
+    e = D.map2(D.mul, a, z) if out else D.map2(D.add, D.map2(D.mul, a, z), a)
+    return Graph.create("esum", ([("a", a)] if out else []) + [("s", D.reduce(D.max, D.const(F32, -1e30), e))])
+
+
+def _expr_sum_inputs(seed):
+    return [(c, data(F32, (300001,), seed + k)) for k, c in enumerate("xyz")]
+
+
+def _affine_read_graph():
+    n = 100003
+    idx = D.map(lambda p: D.add(D.mul(p, D.const(I32, 64)), D.const(I32, 63)), D.iota((n,)))
+    h = D.scatter_add(idx, D.param("src", F32, (n,)), (64 * n,))
+    return Graph.create("aread", [("o", D.map2(D.mul, h, D.param("y", F32, (64 * n,))))])
+
+
+def _affine_read_inputs(seed):
+    return [("src", data(F32, (100003,), seed)), ("y", data(F32, (64 * 100003,), seed + 1))]
+
+
+def _exp_gather_graph():
+    n = 300001
+    x, y, gi = D.param("x", F32, (n,)), D.param("y", F32, (n,)), D.param("gi", I32, (n,))
+    return Graph.create("eg", [("o", D.map2(lambda u, v: D.mul(D.exp(u), v), x, D.gather(gi, y)))])
+
+
+def _exp_gather_inputs(seed):
+    n = 300001
+    return [("x", data(F32, (n,), seed)), ("y", data(F32, (n,), seed + 1)),
+            ("gi", np.random.default_rng(seed).integers(0, n, size=n).astype(np.int32))]
 
 
 @pytest.mark.parametrize("knob,graph,inputs,tpl", KNOB_CASES, ids=[c[0] for c in KNOB_CASES])
