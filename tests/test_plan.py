@@ -134,6 +134,26 @@ def test_affine_scatter_is_read_in_place(monkeypatch):
     assert "scatter_affine" not in [t for _, t in kernels_of(C.mc_greeks())]
 
 
+def test_two_groups_a_lane_for_exp_maps_with_varying_loads(monkeypatch):
+    """An f32 map that calls exp and gathers at varying indices takes two
+    16-byte groups a lane; one that calls exp but only streams, or only
+    gathers, keeps one; map_unroll_gx=0 keeps one everywhere."""
+    n = 1 << 18
+    x, y, gi = D.param("x", F32, (n,)), D.param("y", F32, (n,)), D.param("gi", I32, (n,))
+
+    def groups(g):
+        src = H.source(g)
+        k = src[src.index("void k_"):]
+        return 2 if "cc_v4<float> r[2];" in k else 1 if "cc_v4<float> r;" in k else 0
+
+    both = Graph.create("eg", [("o", D.map2(lambda u, v: D.mul(D.exp(u), v), x, D.gather(gi, y)))])
+    stream = Graph.create("e", [("o", D.map2(lambda u, v: D.mul(D.exp(u), v), x, y))])
+    gather = Graph.create("g", [("o", D.map2(D.mul, x, D.gather(gi, y)))])
+    assert (groups(both), groups(stream), groups(gather)) == (2, 1, 1)
+    monkeypatch.setenv("CCHIP_TUNE", "map_unroll_gx=0")
+    assert groups(both) == 1
+
+
 def test_fanout_materialises_shared_node_once():
     bufs, ks, _ = parse(H.plan(P.fanout(1000).graph()))
     computed = [b for b in bufs if b[3] == "computed"]
