@@ -2103,7 +2103,58 @@ struct Lowering {
         src << k.str();
         ks.push_back(add_kernel(name, args, (int)cdiv(count, per), 256, "reduce_split_fold"));
       };
-      if (np > 1024) {
+      // Up to fold_one partials (16384; 0: never) fold in one workgroup of
+      // 1024 threads instead of two kernels: thread t folds partials t,
+      // t + 1024, ... in that order, sixteen loads in flight at a time,
+      // then the waves fold by butterfly and thread 0 folds the 16 waves in
+      // order and applies init once. A small kernel costs a few
+      // microseconds whatever it moves, so the second one is what goes: the
+      // S20 Greeks step (three sums of 16384 partials) 0.105 -> 0.100 ms.
+      // Past that, one workgroup's share of the loads costs what the
+      // second kernel saves (f64 S20, 32768 partials: 0.154 -> 0.160 ms;
+      // config 1, 65536: no change).
+      const int64_t one = tune("fold_one", 16384);
+      if (np > 1024 && np <= one) {
+        Params p;
+        p.in.push_back(in);
+        p.in.push_back(flags);
+        p.out.push_back(out);
+        std::vector<int> args;
+        std::string params = param_list(p, args);
+        const int64_t K = cdiv(np, 1024), CH = std::min<int64_t>(16, K);
+        const std::string P = "b" + std::to_string(in), F = "b" + std::to_string(flags);
+        std::ostringstream k;
+        k << "extern \"C\" __global__ __launch_bounds__(1024) void " << kname << "(" << params << ") {\n"
+          << "  __shared__ " << T << " wpart[16];\n"
+          << "  __shared__ bool whas[16];\n"
+          << "  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;\n"
+          << "  " << T << " acc = " << ini << "();\n"
+          << "  bool has = false;\n"
+          << "  for (int u0 = 0; u0 < " << K << "; u0 += " << CH << ") {\n"
+          << "    " << T << " v[" << CH << "];\n"
+          << "    bool ok[" << CH << "];\n"
+          << "#pragma unroll\n"
+          << "    for (int u = 0; u < " << CH << "; u++) {\n"
+          << "      const int q = (int)threadIdx.x + 1024 * (u0 + u), qc = min(q, " << np - 1 << ");\n"
+          << "      v[u] = " << P << "[qc];\n"
+          << "      ok[u] = q < " << np << " && " << F << "[qc] != 0;\n"
+          << "    }\n"
+          << "#pragma unroll\n"
+          << "    for (int u = 0; u < " << CH << "; u++) " << fold_in_if(cmb, T, "v[u]", "ok[u]") << "\n"
+          << "  }\n"
+          << "  for (int off = 32; off > 0; off >>= 1) " << xor_combine(cmb, T, "off") << "\n"
+          << "  if (lane == 0) { wpart[wid] = acc; whas[wid] = has; }\n"
+          << "  __syncthreads();\n"
+          << "  if (threadIdx.x == 0) {\n"
+          << "    " << T << " t = " << ini << "();\n"
+          << "    bool th = false;\n"
+          << "    for (int w = 0; w < 16; w++) if (whas[w]) { t = th ? " << cmb << "(t, wpart[w]) : wpart[w]; th = true; }\n"
+          << "    b" << out << "[0] = " << cmb << "(" << ini << "(), t);\n"
+          << "  }\n"
+          << "}\n";
+        src << k.str();
+        ks.push_back(add_kernel(kname, args, 1, 1024, "reduce_split_fold"));
+      } else if (np > 1024) {
         const int64_t n1 = cdiv(np, 1024);
         int mid = add_buf("t" + id + "_partials2", n.dt, n1, BufRole::Scratch);
         fold_kernel(kname + "_fold", in, mid, np, 1024, false);

@@ -477,21 +477,29 @@ FOLDED_CASES = [((1 << 16) + 3, F32, "add"), ((1 << 22) + 5, F32, "add"), ((1 <<
 
 
 @pytest.mark.parametrize("n,dtype,comb", FOLDED_CASES, ids=lambda v: str(v))
-def test_reduce_folded_into_its_map(device, n, dtype, comb):
+def test_reduce_folded_into_its_map(device, monkeypatch, n, dtype, comb):
     """A whole-tensor reduce of the previous root's map output folds inside
     the map kernel: one partial a wave (flagged where the wave held no
-    element), then one fold kernel, or two where there are more than 1024
-    partials (past 2^18 4-byte elements). Ragged tails,
-    init not the identity (folded once), integers exact."""
+    element), then one fold kernel: up to 1024 partials in 256 threads, up
+    to 16384 in one workgroup of 1024; past that, or past 1024 partials
+    (2^18 4-byte elements) with fold_one=0, 1024 a workgroup and then a
+    second kernel. Ragged tails, init not the identity (folded once),
+    integers exact."""
     x, y = D.param("x", dtype, (n,)), D.param("y", dtype, (n,))
     r = D.map2(lambda a, b: D.add(D.mul(a, D.const(dtype, 2)), b), x, y)
     op = D.add if comb == "add" else D.max
     g = Graph.create("mr", [("r", r), ("s", D.reduce(op, D.const(dtype, 3), r))])
     t = templates(g)
-    assert t[0] == "map" and "reduce_split" not in t, t
     groups = n // (2 if dtype is F64 else 4)  # 16-byte groups, one a lane, 256 lanes a workgroup
-    assert t.count("reduce_split_fold") == (2 if 4 * -(-groups // 256) > 1024 else 1), t  # one partial a wave
-    check(g, [("x", data(dtype, (n,), 31)), ("y", data(dtype, (n,), 32))], ["map", "reduce_split_fold"])
+    parts = 4 * -(-groups // 256)  # one partial a wave
+    assert t[0] == "map" and "reduce_split" not in t, t
+    assert t.count("reduce_split_fold") == (1 if parts <= 16384 else 2), (parts, t)
+    ins = [("x", data(dtype, (n,), 31)), ("y", data(dtype, (n,), 32))]
+    check(g, ins, ["map", "reduce_split_fold"])
+    if 1024 < parts <= 16384:
+        monkeypatch.setenv("CCHIP_TUNE", "fold_one=0")
+        assert templates(g).count("reduce_split_fold") == 2
+        check(g, ins, ["map", "reduce_split_fold"])
 
 
 @pytest.mark.parametrize("order", ["sum_first", "map_first"])

@@ -49,7 +49,14 @@ def test_saxpy_is_map_then_reduce(monkeypatch):
     bufs, kk, _ = parse(H.plan(sx.program(1 << 18, 2.0)))
     part = [b for b in bufs if b[0].endswith("_partials")]
     assert len(part) == 1 and part[0][3] == "scratch" and part[0][2] == 4 * 256  # one a wave
-    # 2^20: more partials than one workgroup folds at once, so two fold kernels
+    # 2^20: 4096 partials, folded by one workgroup of 1024 threads;
+    # fold_one=0, or 2^24 (65536 partials): 1024 a workgroup, then a
+    # second kernel
+    assert [t for _, t in kernels_of(sx.program(1 << 20, 2.0))] == ["map", "reduce_split_fold"]
+    fold = [f.split() for f in H.plan(sx.program(1 << 20, 2.0)).splitlines() if "reduce_split_fold" in f]
+    assert fold[0][fold[0].index("grid") + 1] == "1" and fold[0][fold[0].index("block") + 1] == "1024"
+    assert [t for _, t in kernels_of(sx.program(1 << 24, 2.0))] == ["map", "reduce_split_fold", "reduce_split_fold"]
+    monkeypatch.setenv("CCHIP_TUNE", "fold_one=0")
     assert [t for _, t in kernels_of(sx.program(1 << 20, 2.0))] == ["map", "reduce_split_fold", "reduce_split_fold"]
     monkeypatch.setenv("CCHIP_TUNE", "fuse_reduce=0")
     ks = kernels_of(sx.program(1 << 20, 2.0))
